@@ -1,0 +1,116 @@
+"""ctypes binding of ``libg4rollout.so`` (declared in ``include/g4_rollout.h``).
+
+Loading fails loudly: there is no CPU or PyTorch fallback for any entry point. The structs below
+mirror the header field by field (ctypes applies the same C alignment rules).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_size_t, c_uint8, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libg4rollout.so"
+
+G4_OK = 0
+G4_DTYPE_F32 = 0
+G4_DTYPE_BF16 = 1
+G4_CACHE_LINEAR = 0
+G4_CACHE_RING = 1
+G4_APPEND_NORM_K = 1
+G4_APPEND_NORM_V = 2
+G4_APPEND_ROPE_K = 4
+G4_APPEND_NORM_Q = 8
+G4_APPEND_ROPE_Q = 16
+
+
+class G4AppendArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32), ("kind", c_int32), ("batch", c_int32), ("seq", c_int32), ("kv_heads", c_int32),
+        ("group", c_int32), ("head_dim", c_int32), ("capacity", c_int32), ("slot_stride", c_int32),
+        ("flags", c_int32), ("eps", c_float), ("write_pos_scalar", c_int32), ("write_pos", c_void_p),
+        ("k", c_void_p), ("v", c_void_p), ("q", c_void_p), ("in_row_stride", c_int64),
+        ("q_norm_weight", c_void_p), ("k_norm_weight", c_void_p), ("rope_cos", c_void_p), ("rope_sin", c_void_p),
+        ("cache_k", c_void_p), ("cache_vt", c_void_p), ("q_out", c_void_p), ("k_out", c_void_p),
+        ("vt_out", c_void_p), ("chunk_stride", c_int32),
+    ]
+
+
+class G4DecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32), ("kind", c_int32), ("batch", c_int32), ("kv_heads", c_int32), ("group", c_int32),
+        ("head_dim", c_int32), ("capacity", c_int32), ("slot_stride", c_int32), ("window", c_int32),
+        ("q_pos_scalar", c_int32), ("q_pos", c_void_p), ("key_mask", c_void_p), ("key_mask_stride", c_int32),
+        ("q", c_void_p), ("cache_k", c_void_p), ("cache_vt", c_void_p), ("cache_k_w", c_void_p),
+        ("new_k", c_void_p), ("new_v", c_void_p), ("out", c_void_p), ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t), ("num_splits", c_int32),
+    ]
+
+
+class G4PrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32), ("batch", c_int32), ("seq", c_int32), ("kv_heads", c_int32), ("group", c_int32),
+        ("head_dim", c_int32), ("window", c_int32), ("key_mask", c_void_p), ("key_mask_stride", c_int32),
+        ("q", c_void_p), ("k", c_void_p), ("vt", c_void_p), ("k_stride", c_int32), ("out", c_void_p),
+    ]
+
+
+# Every symbol include/g4_rollout.h declares, with its ctypes prototype.
+PROTOTYPES = {
+    "g4_kv_append": (c_int32, [POINTER(G4AppendArgs), c_void_p]),
+    "g4_decode_workspace_size": (c_size_t, [POINTER(G4DecodeArgs)]),
+    "g4_decode_attention": (c_int32, [POINTER(G4DecodeArgs), c_void_p]),
+    "g4_prefill_attention": (c_int32, [POINTER(G4PrefillArgs), c_void_p]),
+    "g4_kv_source_layers": (c_int32, [c_int32, c_int32, POINTER(c_int32), POINTER(c_int32)]),
+    "g4_ring_slot_positions": (c_int32, [c_int32, c_int32, POINTER(c_int32)]),
+    "g4_last_error": (c_char_p, []),
+    "g4_version": (c_char_p, []),
+}
+
+_lib = None
+
+
+class G4Error(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises if it has not been built (no fallback path exists)."""
+
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise G4Error(f"{LIB_PATH} is missing: build it with __graft_entry__.build() (hipcc, gfx950)")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, argtypes) in PROTOTYPES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != G4_OK:
+        msg = lib().g4_last_error().decode(errors="replace")
+        raise G4Error(f"{what} failed ({rc}): {msg}")
+
+
+def kv_source_layers(layer_types: list[int], num_kv_shared_layers: int) -> list[int]:
+    n = len(layer_types)
+    arr_in = (c_int32 * n)(*layer_types)
+    arr_out = (c_int32 * n)()
+    check(lib().g4_kv_source_layers(n, num_kv_shared_layers, arr_in, arr_out), "g4_kv_source_layers")
+    return list(arr_out)
+
+
+def ring_slot_positions(last_written: int, window_capacity: int) -> list[int]:
+    out = (c_int32 * window_capacity)()
+    check(lib().g4_ring_slot_positions(last_written, window_capacity, out), "g4_ring_slot_positions")
+    return list(out)
+
+
+__all__ = [
+    "G4AppendArgs", "G4DecodeArgs", "G4PrefillArgs", "G4Error", "PROTOTYPES", "LIB_PATH", "lib", "check",
+    "kv_source_layers", "ring_slot_positions", "c_uint8",
+]

@@ -1,0 +1,205 @@
+// Fused q/k/v preparation + KV-cache append (g4_kv_append).
+//
+// Replaces forward_rms_norm / forward_rotary_embedding on q and k, the unscaled v norm, and
+// _update_layer_cache of gemma4_posttrain_jax/model.py:463-491, 368-390 with one launch per
+// layer. One workgroup handles one token (b, s); each wave takes whole head vectors, with lane l
+// owning elements [l*D/64, (l+1)*D/64) so a RoPE partner (d +- D/2) is lane l^32 in the same
+// register. K rows go to the head-major key cache, V to the transposed value cache
+// (cache_vt[b, h, d, slot]) that the MFMA attention kernels read as contiguous key runs.
+#include "g4_common.h"
+#include "g4_internal.h"
+
+namespace g4 {
+namespace {
+
+enum VecKind { kQ = 0, kK = 1, kV = 2 };
+
+template <bool BF16, int D>
+__global__ __launch_bounds__(256) void append_kernel(G4AppendArgs a) {
+  using E = Elem<BF16>;
+  using T = typename E::T;
+  // D >= 64: lane l owns d in [l*D/64, (l+1)*D/64) and its RoPE partner is lane l^32;
+  // D < 64: lane l < D owns d = l and its partner is lane l^(D/2).
+  constexpr int PER = D >= 64 ? D / 64 : 1;
+  constexpr int PARTNER = D >= 64 ? 32 : D / 2;
+  const int lane = threadIdx.x & 63;
+  const bool lane_on = D >= 64 || lane < D;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int S = a.seq;
+  const int token = blockIdx.x;
+  const int b = token / S;
+  const int s = token - b * S;
+  const int H = a.kv_heads;
+  const int R = a.group;
+  const int nq = a.q ? H * R : 0;
+  const int nvec = nq + (a.k ? 2 * H : 0);
+
+  // Destination slot (model.py:373-390): linear writes at start + s with XLA's
+  // dynamic_update_slice start clamp; a ring keeps only the chunk's last Wc tokens.
+  const int64_t start = a.write_pos ? (int64_t)a.write_pos[b] : (int64_t)a.write_pos_scalar;
+  const int64_t cap = a.capacity;
+  int64_t slot;
+  bool to_cache;
+  if (a.kind == G4_CACHE_RING) {
+    const int64_t keep = S < cap ? S : cap;
+    to_cache = s >= S - keep;
+    slot = floor_mod(start + s, cap);
+  } else {
+    int64_t st = start < 0 ? 0 : start;
+    if (st > cap - S) st = cap - S;
+    slot = st + s;
+    to_cache = true;
+  }
+
+  const int64_t in_base = (int64_t)token * a.in_row_stride;
+  const int64_t rope_base = (int64_t)token * D;
+
+  for (int vec = wave; vec < nvec; vec += nwaves) {
+    int kind, head, r = 0;
+    const T* src;
+    if (vec < nq) {
+      kind = kQ;
+      head = vec / R;
+      r = vec - head * R;
+      src = reinterpret_cast<const T*>(a.q) + in_base + (int64_t)vec * D;
+    } else if (vec < nq + H) {
+      kind = kK;
+      head = vec - nq;
+      src = reinterpret_cast<const T*>(a.k) + in_base + (int64_t)head * D;
+    } else {
+      kind = kV;
+      head = vec - nq - H;
+      src = reinterpret_cast<const T*>(a.v) + in_base + (int64_t)head * D;
+    }
+
+    float x[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) x[e] = lane_on ? E::load(src, lane * PER + e) : 0.f;
+
+    const bool norm = (kind == kQ && (a.flags & G4_APPEND_NORM_Q)) || (kind == kK && (a.flags & G4_APPEND_NORM_K)) ||
+                      (kind == kV && (a.flags & G4_APPEND_NORM_V));
+    if (norm) {
+      // forward_rms_norm (model.py:278-285): f32 statistics, x * (mean(x^2) + eps)^-0.5 * w.
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) ss += x[e] * x[e];
+      ss = wave_sum(ss);
+      const float inv = 1.0f / __fsqrt_rn(ss / (float)D + a.eps);
+      const T* w = kind == kQ ? reinterpret_cast<const T*>(a.q_norm_weight)
+                              : (kind == kK ? reinterpret_cast<const T*>(a.k_norm_weight) : nullptr);
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        float y = x[e] * inv;
+        if (w && lane_on) y = y * E::load(w, lane * PER + e);
+        x[e] = E::round(y);
+      }
+    }
+
+    const bool rope = (kind == kQ && (a.flags & G4_APPEND_ROPE_Q)) || (kind == kK && (a.flags & G4_APPEND_ROPE_K));
+    if (rope) {
+      // x*cos + rotate_half(x)*sin with cos/sin first rounded to the activation dtype
+      // (model.py:309-317); products and sum are rounded separately (no FMA contraction).
+#pragma clang fp contract(off)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const int d = lane * PER + e;
+        const float partner = __shfl_xor(x[e], PARTNER, 64);
+        const float rot = d < D / 2 ? -partner : partner;
+        const float c = lane_on ? E::round(a.rope_cos[rope_base + d]) : 0.f;
+        const float sn = lane_on ? E::round(a.rope_sin[rope_base + d]) : 0.f;
+        const float t0 = x[e] * c;  // plain operators: the pragma above keeps them unfused
+        const float t1 = rot * sn;
+        x[e] = E::round(t0 + t1);
+      }
+    }
+
+    const int64_t bh = (int64_t)b * H + head;
+    if (!lane_on) continue;
+    if (kind == kQ) {
+      T* dst = reinterpret_cast<T*>(a.q_out) + ((((int64_t)token) * H + head) * R + r) * D;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) E::store(dst, lane * PER + e, x[e]);
+    } else if (kind == kK) {
+      if (to_cache) {
+        T* dst = reinterpret_cast<T*>(a.cache_k) + (bh * a.slot_stride + slot) * D;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) E::store(dst, lane * PER + e, x[e]);
+      }
+      if (a.k_out) {
+        T* dst = reinterpret_cast<T*>(a.k_out) + (bh * a.chunk_stride + s) * D;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) E::store(dst, lane * PER + e, x[e]);
+      }
+    } else {
+      if (to_cache) {
+        T* dst = reinterpret_cast<T*>(a.cache_vt) + bh * D * a.slot_stride + slot;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) E::store(dst, (int64_t)(lane * PER + e) * a.slot_stride, x[e]);
+      }
+      if (a.vt_out) {
+        T* dst = reinterpret_cast<T*>(a.vt_out) + bh * D * a.chunk_stride + s;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) E::store(dst, (int64_t)(lane * PER + e) * a.chunk_stride, x[e]);
+      }
+    }
+  }
+}
+
+template <bool BF16>
+int launch_append(const G4AppendArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)((int64_t)a.batch * a.seq));
+  const dim3 block(256);
+  switch (a.head_dim) {
+    case 8: hipLaunchKernelGGL((append_kernel<BF16, 8>), grid, block, 0, st, a); break;
+    case 16: hipLaunchKernelGGL((append_kernel<BF16, 16>), grid, block, 0, st, a); break;
+    case 32: hipLaunchKernelGGL((append_kernel<BF16, 32>), grid, block, 0, st, a); break;
+    case 64: hipLaunchKernelGGL((append_kernel<BF16, 64>), grid, block, 0, st, a); break;
+    case 128: hipLaunchKernelGGL((append_kernel<BF16, 128>), grid, block, 0, st, a); break;
+    case 256: hipLaunchKernelGGL((append_kernel<BF16, 256>), grid, block, 0, st, a); break;
+    case 512: hipLaunchKernelGGL((append_kernel<BF16, 512>), grid, block, 0, st, a); break;
+    default: return fail(G4_ERR_UNSUPPORTED, "g4_kv_append: head_dim %d", a.head_dim);
+  }
+  return check_launch("g4_kv_append");
+}
+
+}  // namespace
+}  // namespace g4
+
+extern "C" int g4_kv_append(const G4AppendArgs* args, void* stream) {
+  using g4::fail;
+  if (!args) return fail(G4_ERR_INVALID, "g4_kv_append: args is NULL");
+  const G4AppendArgs& a = *args;
+  if (a.dtype != G4_DTYPE_F32 && a.dtype != G4_DTYPE_BF16) return fail(G4_ERR_INVALID, "g4_kv_append: dtype %d", a.dtype);
+  if (a.kind != G4_CACHE_LINEAR && a.kind != G4_CACHE_RING) return fail(G4_ERR_INVALID, "g4_kv_append: kind %d", a.kind);
+  if (a.batch <= 0 || a.seq <= 0 || a.kv_heads <= 0)
+    return fail(G4_ERR_INVALID, "g4_kv_append: batch/seq/kv_heads must be positive (%d, %d, %d)", a.batch, a.seq,
+                a.kv_heads);
+  if (!g4::supported_head_dim(a.head_dim)) return fail(G4_ERR_UNSUPPORTED, "g4_kv_append: head_dim %d", a.head_dim);
+  if (a.capacity <= 0 || a.slot_stride < a.capacity || a.slot_stride % 64)
+    return fail(G4_ERR_INVALID, "g4_kv_append: capacity %d / slot_stride %d (need stride >= capacity, multiple of 64)",
+                a.capacity, a.slot_stride);
+  if (a.kind == G4_CACHE_LINEAR && a.seq > a.capacity)
+    return fail(G4_ERR_INVALID, "g4_kv_append: %d tokens do not fit a linear cache of %d slots", a.seq, a.capacity);
+  if (a.k || a.v) {
+    if (!a.k || !a.v || !a.cache_k || !a.cache_vt)
+      return fail(G4_ERR_INVALID, "g4_kv_append: k/v/cache pointer is NULL");
+  } else if (!a.q) {
+    return fail(G4_ERR_INVALID, "g4_kv_append: nothing to do (q, k and v are NULL)");
+  }
+  if (a.in_row_stride < (int64_t)a.kv_heads * a.head_dim)
+    return fail(G4_ERR_INVALID, "g4_kv_append: in_row_stride %lld too small", (long long)a.in_row_stride);
+  if (a.q) {
+    if (a.group <= 0 || !a.q_out) return fail(G4_ERR_INVALID, "g4_kv_append: q needs group > 0 and q_out");
+  }
+  if ((a.flags & (G4_APPEND_ROPE_K | G4_APPEND_ROPE_Q)) && (!a.rope_cos || !a.rope_sin))
+    return fail(G4_ERR_INVALID, "g4_kv_append: RoPE flags need rope_cos/rope_sin");
+  if ((a.flags & G4_APPEND_NORM_K) && !a.k_norm_weight) return fail(G4_ERR_INVALID, "g4_kv_append: NORM_K needs k_norm_weight");
+  if ((a.flags & G4_APPEND_NORM_Q) && a.q && !a.q_norm_weight)
+    return fail(G4_ERR_INVALID, "g4_kv_append: NORM_Q needs q_norm_weight");
+  if ((a.k_out || a.vt_out) && (a.chunk_stride < a.seq || a.chunk_stride % 64))
+    return fail(G4_ERR_INVALID, "g4_kv_append: chunk_stride %d (need >= seq, multiple of 64)", a.chunk_stride);
+  if ((int64_t)a.batch * a.seq > 0x7fffffffLL) return fail(G4_ERR_UNSUPPORTED, "g4_kv_append: too many tokens");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  return a.dtype == G4_DTYPE_BF16 ? g4::launch_append<true>(a, st) : g4::launch_append<false>(a, st);
+}

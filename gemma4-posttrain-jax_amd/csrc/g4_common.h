@@ -1,0 +1,87 @@
+// Device helpers shared by the gfx950 kernels: bf16 rounding, element access, MFMA types,
+// wavefront reductions, and the ring-slot arithmetic of model.py:355-357.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace g4 {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// jnp.finfo(bf16).min / jnp.finfo(f32).min: the masked-score fill value (model.py:497).
+constexpr float kBf16Min = -3.3895313892515355e38f;
+constexpr float kF32Min = -3.4028234663852886e38f;
+
+__host__ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+#ifdef __HIP_DEVICE_COMPILE__
+  return __uint_as_float(b << 16);
+#else
+  union { uint32_t u; float f; } c;
+  c.u = b << 16;
+  return c.f;
+#endif
+}
+
+// float32 -> bf16 bits, round to nearest even; NaN -> canonical quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// Element access for the two storage types (bf16 as raw uint16 bits, f32 as float).
+template <bool BF16> struct Elem;
+template <> struct Elem<true> {
+  typedef uint16_t T;
+  static constexpr float kMin = kBf16Min;
+  __device__ static __forceinline__ float load(const T* p, int64_t i) { return bf16_bits_to_f32(p[i]); }
+  __device__ static __forceinline__ void store(T* p, int64_t i, float v) { p[i] = (uint16_t)f32_to_bf16_bits(v); }
+  __device__ static __forceinline__ float round(float v) { return round_bf16(v); }
+};
+template <> struct Elem<false> {
+  typedef float T;
+  static constexpr float kMin = kF32Min;
+  __device__ static __forceinline__ float load(const T* p, int64_t i) { return p[i]; }
+  __device__ static __forceinline__ void store(T* p, int64_t i, float v) { p[i] = v; }
+  __device__ static __forceinline__ float round(float v) { return v; }
+};
+
+// Wave64 reductions over lanes that differ in the given xor masks.
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// Ring slot r of a Wc-slot buffer holds the greatest position p <= last with p % Wc == r
+// (model.py:357); negative means never written.
+__host__ __device__ __forceinline__ int64_t ring_slot_position(int64_t last, int64_t slot, int64_t wc) {
+  int64_t diff = last - slot;
+  int64_t q = diff >= 0 ? diff / wc : -((-diff + wc - 1) / wc);  // floor division
+  return slot + q * wc;
+}
+
+__host__ __device__ __forceinline__ int64_t floor_mod(int64_t a, int64_t m) {
+  int64_t r = a % m;
+  return r < 0 ? r + m : r;
+}
+
+// 16-byte global load / store of 8 bf16 values (raw bits).
+__device__ __forceinline__ u32x4 load16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ floatx4 mfma16x16x32(bf16x8 a, bf16x8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace g4

@@ -1,0 +1,221 @@
+"""PyTorch-tensor front end of the native kernels: shape checks, then one C-ABI call each.
+
+Tensors are device buffers only; every computation runs in ``libg4rollout.so`` on the current
+torch stream. bf16 tensors are passed by their raw bits (torch.bfloat16 storage is the same
+16-bit format the kernels use).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .kvcache import LayerKVCache
+
+_DTYPES = {torch.float32: _lib.G4_DTYPE_F32, torch.bfloat16: _lib.G4_DTYPE_BF16}
+
+
+def _code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; the kernels take float32 or bfloat16") from None
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("kernel operands must be device tensors")
+    return t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _check_rows(t: torch.Tensor, name: str, B: int, S: int, n: int, D: int, row_stride: int) -> None:
+    """``t`` is a [B, S, n, D] view whose tokens are ``row_stride`` elements apart."""
+
+    if tuple(t.shape) != (B, S, n, D):
+        raise ValueError(f"{name}: shape {tuple(t.shape)} != {(B, S, n, D)}")
+    bad = (D > 1 and t.stride(3) != 1) or (n > 1 and t.stride(2) != D)
+    bad = bad or (S > 1 and t.stride(1) != row_stride) or (B > 1 and t.stride(0) != S * row_stride)
+    if bad:
+        raise ValueError(f"{name}: strides {t.stride()} do not follow rows of {row_stride} elements")
+
+
+def kv_append(
+    layer: LayerKVCache,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    write_pos: int | torch.Tensor,
+    flags: int = 0,
+    eps: float = 1e-6,
+    q: torch.Tensor | None = None,
+    q_out: torch.Tensor | None = None,
+    q_norm_weight: torch.Tensor | None = None,
+    k_norm_weight: torch.Tensor | None = None,
+    rope_cos: torch.Tensor | None = None,
+    rope_sin: torch.Tensor | None = None,
+    k_out: torch.Tensor | None = None,
+    vt_out: torch.Tensor | None = None,
+) -> None:
+    """g4_kv_append: k/v ``[B, S, Hkv, D]`` (and optional q ``[B, S, Hkv, R, D]``) views of rows
+    sharing one row stride; writes ``layer`` in place (model.py:368-390 + 463-482)."""
+
+    B, S, H, D = k.shape
+    rs = k.stride(1) if S > 1 else (k.stride(0) if B > 1 else H * D)
+    _check_rows(k, "k", B, S, H, D, rs)
+    _check_rows(v, "v", B, S, H, D, rs)
+    if k.dtype != layer.key.dtype or v.dtype != k.dtype:
+        raise TypeError("k/v/cache dtypes differ")
+    if tuple(layer.key.shape[:2]) != (B, H) or layer.key.shape[3] != D:
+        raise ValueError(f"cache {tuple(layer.key.shape)} does not match k {tuple(k.shape)}")
+    R = 0
+    if q is not None:
+        R = q.shape[3]
+        if tuple(q.shape) != (B, S, H, R, D) or q.stride(4) != 1 or q.stride(3) != D or q.stride(2) != R * D:
+            raise ValueError(f"q: shape {tuple(q.shape)} / strides {q.stride()}")
+        if (S > 1 and q.stride(1) != rs) or (B > 1 and q.stride(0) != S * rs):
+            raise ValueError("q must share k's row stride")
+        if q_out is None or tuple(q_out.shape) != (B, S, H, R, D) or not q_out.is_contiguous():
+            raise ValueError("q_out must be a contiguous [B, S, Hkv, R, D] tensor")
+    chunk_stride = 0
+    if k_out is not None or vt_out is not None:
+        if k_out is None or vt_out is None:
+            raise ValueError("k_out and vt_out go together")
+        chunk_stride = k_out.shape[2]
+        if tuple(k_out.shape) != (B, H, chunk_stride, D) or tuple(vt_out.shape) != (B, H, D, chunk_stride):
+            raise ValueError("k_out / vt_out shapes")
+        if not (k_out.is_contiguous() and vt_out.is_contiguous()):
+            raise ValueError("k_out / vt_out must be contiguous")
+    if isinstance(write_pos, torch.Tensor):
+        if write_pos.dtype != torch.int32 or tuple(write_pos.shape) != (B,) or not write_pos.is_contiguous():
+            raise ValueError("write_pos must be a contiguous int32 [B] tensor")
+        wp_ptr, wp_scalar = _ptr(write_pos), 0
+    else:
+        wp_ptr, wp_scalar = None, int(write_pos)
+    if flags & (_lib.G4_APPEND_ROPE_K | _lib.G4_APPEND_ROPE_Q):
+        for t in (rope_cos, rope_sin):
+            if t is None or t.dtype != torch.float32 or tuple(t.shape) != (B, S, D) or not t.is_contiguous():
+                raise ValueError("rope_cos/rope_sin must be contiguous float32 [B, S, D]")
+    a = _lib.G4AppendArgs(
+        dtype=_code(k), kind=_lib.G4_CACHE_RING if layer.ring else _lib.G4_CACHE_LINEAR, batch=B, seq=S, kv_heads=H,
+        group=R, head_dim=D, capacity=layer.capacity, slot_stride=layer.slot_stride, flags=flags, eps=eps,
+        write_pos_scalar=wp_scalar, write_pos=wp_ptr, k=_ptr(k), v=_ptr(v), q=_ptr(q), in_row_stride=rs,
+        q_norm_weight=_ptr(q_norm_weight), k_norm_weight=_ptr(k_norm_weight), rope_cos=_ptr(rope_cos),
+        rope_sin=_ptr(rope_sin), cache_k=_ptr(layer.key), cache_vt=_ptr(layer.value_t), q_out=_ptr(q_out),
+        k_out=_ptr(k_out), vt_out=_ptr(vt_out), chunk_stride=chunk_stride,
+    )
+    _lib.check(_lib.lib().g4_kv_append(ctypes.byref(a), _stream()), "g4_kv_append")
+
+
+def prepare_q(
+    q: torch.Tensor,
+    q_out: torch.Tensor,
+    *,
+    flags: int,
+    eps: float,
+    q_norm_weight: torch.Tensor | None,
+    rope_cos: torch.Tensor | None,
+    rope_sin: torch.Tensor | None,
+) -> None:
+    """g4_kv_append with q only (kv-shared layers): q ``[B, S, Hkv, R, D]`` view -> ``q_out``."""
+
+    B, S, H, R, D = q.shape
+    rs = q.stride(1) if S > 1 else (q.stride(0) if B > 1 else H * R * D)
+    if q.stride(4) != 1 or q.stride(3) != D or q.stride(2) != R * D or (B > 1 and q.stride(0) != S * rs):
+        raise ValueError(f"q strides {q.stride()}")
+    if tuple(q_out.shape) != (B, S, H, R, D) or not q_out.is_contiguous() or q_out.dtype != q.dtype:
+        raise ValueError("q_out must be a contiguous [B, S, Hkv, R, D] tensor in q's dtype")
+    if flags & _lib.G4_APPEND_ROPE_Q:
+        for t in (rope_cos, rope_sin):
+            if t is None or t.dtype != torch.float32 or tuple(t.shape) != (B, S, D) or not t.is_contiguous():
+                raise ValueError("rope_cos/rope_sin must be contiguous float32 [B, S, D]")
+    a = _lib.G4AppendArgs(
+        dtype=_code(q), kind=_lib.G4_CACHE_LINEAR, batch=B, seq=S, kv_heads=H, group=R, head_dim=D, capacity=S,
+        slot_stride=(S + 63) // 64 * 64, flags=flags, eps=eps, write_pos_scalar=0, write_pos=None, k=None, v=None,
+        q=_ptr(q), in_row_stride=rs, q_norm_weight=_ptr(q_norm_weight), k_norm_weight=None, rope_cos=_ptr(rope_cos),
+        rope_sin=_ptr(rope_sin), cache_k=None, cache_vt=None, q_out=_ptr(q_out), k_out=None, vt_out=None,
+        chunk_stride=0,
+    )
+    _lib.check(_lib.lib().g4_kv_append(ctypes.byref(a), _stream()), "g4_kv_append")
+
+
+def decode_attention(
+    layer: LayerKVCache,
+    q: torch.Tensor,
+    key_mask: torch.Tensor,
+    *,
+    q_pos: int | torch.Tensor,
+    window: int,
+    out: torch.Tensor | None = None,
+    new_k: torch.Tensor | None = None,
+    new_v: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """g4_decode_attention: q ``[B, Hkv, R, D]`` against ``layer``; returns ``[B, Hkv, R, D]``.
+    With ``new_k``/``new_v`` (``[B, Hkv, D]``) the token's K/V is stored at ``q_pos`` first."""
+
+    B, H, R, D = q.shape
+    if not q.is_contiguous() or q.dtype != layer.key.dtype:
+        raise ValueError("q must be contiguous and in the cache dtype")
+    if tuple(layer.key.shape[:2]) != (B, H) or layer.key.shape[3] != D:
+        raise ValueError(f"cache {tuple(layer.key.shape)} does not match q {tuple(q.shape)}")
+    if key_mask.dtype != torch.bool or key_mask.dim() != 2 or key_mask.shape[0] != B or key_mask.stride(1) != 1:
+        raise ValueError("key_mask must be a [B, C] bool tensor with unit inner stride")
+    if out is None:
+        out = torch.empty_like(q)
+    elif tuple(out.shape) != (B, H, R, D) or not out.is_contiguous() or out.dtype != q.dtype:
+        raise ValueError("out must be a contiguous [B, Hkv, R, D] tensor in q's dtype")
+    for name, t in (("new_k", new_k), ("new_v", new_v)):
+        if t is not None and (tuple(t.shape) != (B, H, D) or not t.is_contiguous() or t.dtype != q.dtype):
+            raise ValueError(f"{name} must be a contiguous [B, Hkv, D] tensor in q's dtype")
+    if isinstance(q_pos, torch.Tensor):
+        if q_pos.dtype != torch.int32 or tuple(q_pos.shape) != (B,) or not q_pos.is_contiguous():
+            raise ValueError("q_pos must be a contiguous int32 [B] tensor")
+        qp_ptr, qp_scalar = _ptr(q_pos), 0
+    else:
+        qp_ptr, qp_scalar = None, int(q_pos)
+    a = _lib.G4DecodeArgs(
+        dtype=_code(q), kind=_lib.G4_CACHE_RING if layer.ring else _lib.G4_CACHE_LINEAR, batch=B, kv_heads=H,
+        group=R, head_dim=D, capacity=layer.capacity, slot_stride=layer.slot_stride, window=window,
+        q_pos_scalar=qp_scalar, q_pos=qp_ptr, key_mask=_ptr(key_mask), key_mask_stride=key_mask.stride(0),
+        q=_ptr(q), cache_k=_ptr(layer.key), cache_vt=_ptr(layer.value_t), cache_k_w=_ptr(layer.key),
+        new_k=_ptr(new_k), new_v=_ptr(new_v), out=_ptr(out), workspace=None, workspace_bytes=0, num_splits=0,
+    )
+    _lib.check(_lib.lib().g4_decode_attention(ctypes.byref(a), _stream()), "g4_decode_attention")
+    return out
+
+
+def prefill_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    vt: torch.Tensor,
+    key_mask: torch.Tensor,
+    *,
+    window: int,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """g4_prefill_attention: q ``[B, S, Hkv, R, D]``, k ``[B, Hkv, Sp, D]``, vt ``[B, Hkv, D, Sp]``
+    (Sp >= S, multiple of 64); returns ``[B, S, Hkv, R, D]``."""
+
+    B, S, H, R, D = q.shape
+    Sp = k.shape[2]
+    if not q.is_contiguous() or tuple(k.shape) != (B, H, Sp, D) or tuple(vt.shape) != (B, H, D, Sp):
+        raise ValueError(f"q {tuple(q.shape)} / k {tuple(k.shape)} / vt {tuple(vt.shape)}")
+    if not (k.is_contiguous() and vt.is_contiguous()) or k.dtype != q.dtype or vt.dtype != q.dtype:
+        raise ValueError("k/vt must be contiguous and in q's dtype")
+    if key_mask.dtype != torch.bool or key_mask.dim() != 2 or key_mask.shape[0] != B or key_mask.stride(1) != 1:
+        raise ValueError("key_mask must be a [B, >=S] bool tensor with unit inner stride")
+    if out is None:
+        out = torch.empty_like(q)
+    a = _lib.G4PrefillArgs(
+        dtype=_code(q), batch=B, seq=S, kv_heads=H, group=R, head_dim=D, window=window, key_mask=_ptr(key_mask),
+        key_mask_stride=key_mask.stride(0), q=_ptr(q), k=_ptr(k), vt=_ptr(vt), k_stride=Sp, out=_ptr(out),
+    )
+    _lib.check(_lib.lib().g4_prefill_attention(ctypes.byref(a), _stream()), "g4_prefill_attention")
+    return out

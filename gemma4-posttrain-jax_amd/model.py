@@ -1,0 +1,384 @@
+"""Gemma 4 text decoder forward on MI355X: the drop-in for gemma4_posttrain_jax/model.py's
+generation path (``init_kv_cache``, ``forward_gemma4_text``, ``forward_gemma4_lm``).
+
+Parameters use the reference's pytree (``Gemma4TextParams`` and friends, model.py:193-235) with
+torch device tensors. On first use each params object is packed once into the kernel-friendly
+layout (``PackedWeights``): q/k/v projections fused into one ``[M, (H*R + 2H)*D]`` matrix with
+query columns in (kv head, r) order, o_proj rows in the same order, gate|up fused. Per layer the
+forward runs one hipBLASLt GEMM for q/k/v, the native ``g4_kv_append`` (q/k norms, RoPE, v norm,
+cache append), the native prefill or decode attention kernel, and GEMMs for o_proj and the MLP.
+RMSNorm / residual / gelu glue runs as PyTorch-ROCm elementwise ops with the reference's f32
+rounding points.
+"""
+
+from __future__ import annotations
+
+import math
+import weakref
+from typing import Literal, NamedTuple
+
+import numpy as np
+import torch
+
+from . import _lib, kernels
+from .config import (
+    FULL,
+    SLIDING,
+    Gemma4TextConfig,
+    is_kv_shared,
+    kv_source_layers,
+    layer_has_v_proj,
+    layer_head_dim,
+    layer_intermediate_size,
+    layer_kv_heads,
+)
+from .kvcache import KVCache, LayerKVCache, init_kv_cache, slot_stride_for
+
+# --- parameter pytree (model.py:193-235) -----------------------------------------------------------
+
+
+class RMSNormParams(NamedTuple):
+    weight: torch.Tensor  # [dim]
+
+
+class AttentionParams(NamedTuple):
+    q_proj: torch.Tensor  # [M, R, H, D]
+    k_proj: torch.Tensor | None  # [M, H, D]
+    v_proj: torch.Tensor | None  # [M, H, D]
+    o_proj: torch.Tensor  # [R, H, D, M]
+    q_norm: RMSNormParams
+    k_norm: RMSNormParams | None
+
+
+class MLPParams(NamedTuple):
+    gate_proj: torch.Tensor  # [M, F]
+    up_proj: torch.Tensor  # [M, F]
+    down_proj: torch.Tensor  # [F, M]
+
+
+class PerLayerInputParams(NamedTuple):
+    gate: torch.Tensor  # [M, P]
+    projection: torch.Tensor  # [P, M]
+    post_norm: RMSNormParams
+
+
+class DecoderLayerParams(NamedTuple):
+    input_norm: RMSNormParams
+    attention: AttentionParams
+    post_attention_norm: RMSNormParams
+    pre_feedforward_norm: RMSNormParams
+    mlp: MLPParams
+    post_feedforward_norm: RMSNormParams
+    per_layer_input: PerLayerInputParams | None
+    layer_scalar: torch.Tensor  # []
+
+
+class Gemma4TextParams(NamedTuple):
+    embed_tokens: torch.Tensor  # [V, M]
+    embed_tokens_per_layer: torch.Tensor | None  # [Vp, L, P]
+    per_layer_model_projection: torch.Tensor | None  # [M, L, P]
+    per_layer_projection_norm: RMSNormParams | None
+    layers: tuple
+    final_norm: RMSNormParams
+
+
+class Gemma4Output(NamedTuple):
+    logits: torch.Tensor  # [B, S', V]
+    hidden: torch.Tensor  # [B, S, M]
+    kv_cache: KVCache | None
+
+
+def params_from_numpy(p, config: Gemma4TextConfig, *, dtype=torch.bfloat16, device="cuda") -> Gemma4TextParams:
+    """Build device params from an object with the reference's field names holding numpy arrays
+    (plain arrays for norm weights)."""
+
+    def t(x):
+        return None if x is None else torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dtype).to(device)
+
+    def n(x):
+        return None if x is None else RMSNormParams(t(x))
+
+    layers = []
+    for lp in p.layers:
+        a = lp.attention
+        ple = None
+        if lp.per_layer_input is not None:
+            ple = PerLayerInputParams(t(lp.per_layer_input.gate), t(lp.per_layer_input.projection),
+                                      n(lp.per_layer_input.post_norm))
+        layers.append(DecoderLayerParams(
+            n(lp.input_norm), AttentionParams(t(a.q_proj), t(a.k_proj), t(a.v_proj), t(a.o_proj), n(a.q_norm),
+                                              n(a.k_norm)),
+            n(lp.post_attention_norm), n(lp.pre_feedforward_norm),
+            MLPParams(t(lp.mlp.gate_proj), t(lp.mlp.up_proj), t(lp.mlp.down_proj)), n(lp.post_feedforward_norm), ple,
+            t(np.asarray(lp.layer_scalar, np.float32)).reshape(())))
+    return Gemma4TextParams(t(p.embed_tokens), t(p.embed_tokens_per_layer), t(p.per_layer_model_projection),
+                            n(p.per_layer_projection_norm), tuple(layers), n(p.final_norm))
+
+
+# --- packed device weights ---------------------------------------------------------------------------
+
+
+class PackedLayer(NamedTuple):
+    w_qkv: torch.Tensor  # [M, (H*R [+ H [+ H]])*D]: q in (h, r) order, then k, then v
+    w_o: torch.Tensor  # [H*R*D, M] rows in (h, r, d) order
+    w_gate_up: torch.Tensor  # [M, 2F]
+    w_down: torch.Tensor  # [F, M]
+    heads: int
+    group: int
+    head_dim: int
+    has_k: bool
+    has_v: bool
+
+
+class PackedWeights(NamedTuple):
+    layers: tuple
+    embed_scale: torch.Tensor  # bf16/f32 scalar sqrt(M) rounded to the param dtype (model.py:600)
+    inv_freq: dict  # layer type -> f32 [D/2] device tensor (model.py:294-302)
+
+
+_PACKED: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+_PACKED_BY_ID: dict = {}
+
+
+def _rope_inv_freq(config: Gemma4TextConfig) -> dict:
+    """model.py:294-302 in numpy float32 (host-side configuration constants)."""
+
+    dim = config.head_dim
+    inv_s = (np.float32(1.0) / np.power(np.float32(config.rope_theta_sliding),
+                                        np.arange(0, dim, 2, dtype=np.float32) / np.float32(dim))).astype(np.float32)
+    dim = config.global_head_dim
+    angles = int(config.full_partial_rotary_factor * dim // 2)
+    inv_r = (np.float32(1.0) / np.power(np.float32(config.rope_theta_full),
+                                        np.arange(0, 2 * angles, 2, dtype=np.float32) / np.float32(dim))).astype(np.float32)
+    inv_f = np.concatenate([inv_r, np.zeros(dim // 2 - angles, np.float32)])
+    return {SLIDING: inv_s, FULL: inv_f}
+
+
+def pack_weights(params: Gemma4TextParams, config: Gemma4TextConfig) -> PackedWeights:
+    """Fuse and reorder the projection weights once per params object (cached)."""
+
+    key = id(params)
+    hit = _PACKED_BY_ID.get(key)
+    if hit is not None and hit[0] is params:
+        return hit[1]
+    layers = []
+    for i, lp in enumerate(params.layers):
+        a = lp.attention
+        M, R, H, D = a.q_proj.shape
+        wq = a.q_proj.permute(0, 2, 1, 3).reshape(M, H * R * D)
+        parts = [wq]
+        has_k = a.k_proj is not None
+        has_v = a.v_proj is not None
+        if has_k:
+            parts.append(a.k_proj.reshape(M, H * D))
+        if has_v:
+            parts.append(a.v_proj.reshape(M, H * D))
+        w_qkv = torch.cat(parts, dim=1).contiguous()
+        w_o = a.o_proj.permute(1, 0, 2, 3).reshape(H * R * D, M).contiguous()
+        w_gu = torch.cat([lp.mlp.gate_proj, lp.mlp.up_proj], dim=1).contiguous()
+        layers.append(PackedLayer(w_qkv, w_o, w_gu, lp.mlp.down_proj.contiguous(), H, R, D, has_k, has_v))
+    dev = params.embed_tokens.device
+    dt = params.embed_tokens.dtype
+    inv = {k: torch.from_numpy(v).to(dev) for k, v in _rope_inv_freq(config).items()}
+    packed = PackedWeights(tuple(layers), torch.tensor(math.sqrt(config.hidden_size), dtype=dt, device=dev), inv)
+    _PACKED_BY_ID.clear()  # one live params object at a time (rollout reuses the same weights)
+    _PACKED_BY_ID[key] = (params, packed)
+    return packed
+
+
+# --- elementwise glue (PyTorch-ROCm ops, reference rounding points) ----------------------------------
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.Tensor:
+    """model.py:278-285: f32 ``x * (mean(x^2) + eps)^-0.5 * w``, cast back to x's dtype."""
+
+    x32 = x.float()
+    y = x32 * torch.pow(x32.square().mean(-1, keepdim=True) + eps, -0.5)
+    if weight is not None:
+        y = y * weight.float()
+    return y.to(x.dtype)
+
+
+def gelu_tanh_f32(x: torch.Tensor) -> torch.Tensor:
+    return torch.nn.functional.gelu(x.float(), approximate="tanh")
+
+
+def rotary_tables(inv_freq: torch.Tensor, position_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """model.py:288-291: f32 cos/sin ``[B, S, D]`` of ``concat(f, f)``, f = pos * inv_freq."""
+
+    freqs = position_ids.float()[..., None] * inv_freq[None, None, :]
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return torch.cos(emb).contiguous(), torch.sin(emb).contiguous()
+
+
+# --- forward ----------------------------------------------------------------------------------------------
+
+
+def _per_layer_inputs(params: Gemma4TextParams, config: Gemma4TextConfig, ids: torch.Tensor, x: torch.Tensor):
+    """model.py:414-426."""
+
+    P = config.hidden_size_per_layer_input
+    L = config.num_hidden_layers
+    B, S, M = x.shape
+    dt = x.dtype
+    token = params.embed_tokens_per_layer[ids]  # [B, S, L, P]
+    token = (token.float() * torch.tensor(math.sqrt(P), dtype=dt, device=x.device).float()).to(dt)
+    ctx = (x.reshape(B * S, M) @ params.per_layer_model_projection.reshape(M, L * P)).reshape(B, S, L, P)
+    ctx = (ctx.float() * (config.hidden_size ** -0.5)).to(dt)
+    ctx = rms_norm(ctx, params.per_layer_projection_norm.weight, config.rms_norm_eps)
+    return ((ctx.float() + token.float()).to(dt).float() * (2.0 ** -0.5)).to(dt)
+
+
+def forward_gemma4_text(
+    params: Gemma4TextParams,
+    input_ids: torch.Tensor,
+    position_ids: torch.Tensor,
+    *,
+    config: Gemma4TextConfig,
+    attention_mask: torch.Tensor | None = None,
+    kv_cache: KVCache | None = None,
+    cache_mode: Literal["prefill", "append"] = "prefill",
+    lora=None,
+) -> tuple[torch.Tensor, KVCache | None]:
+    """model.py:571-673: hidden after the final norm and the updated cache.
+
+    Without a cache the forward runs in prefill form over a scratch cache (the reference's
+    cache-less path computes the same attention). ``lora`` must be None: the rollout path runs
+    without adapters (the reference applies LoRA inside the projections, lora.py:107-113)."""
+
+    if lora is not None:
+        raise NotImplementedError("LoRA adapters are not supported by the native rollout path")
+    B, S = input_ids.shape
+    dev = input_ids.device
+    pw = pack_weights(params, config)
+    eps = config.rms_norm_eps
+    if attention_mask is None:
+        attention_mask = torch.ones((B, S), dtype=torch.bool, device=dev)
+    attention_mask = attention_mask.to(torch.bool)
+
+    x = params.embed_tokens[input_ids.long()]
+    x = (x.float() * pw.embed_scale.float()).to(x.dtype)
+    pli = _per_layer_inputs(params, config, input_ids.long(), x) if config.hidden_size_per_layer_input else None
+
+    scratch_cache = kv_cache is None
+    if scratch_cache:
+        kv_cache = init_kv_cache(config, B, S, x.dtype, dev)
+        cache_mode = "prefill"
+    if cache_mode == "append" and S != 1:
+        raise ValueError(f'cache_mode="append" requires one token, got {S}')
+    length = int(kv_cache.length)
+    key_mask = kv_cache.key_mask.clone()
+    key_mask[:, length:length + S] = attention_mask
+    rot = {t: rotary_tables(pw.inv_freq[t], position_ids) for t in (SLIDING, FULL)}
+    sources = kv_source_layers(config)
+
+    flags_q = _lib.G4_APPEND_NORM_Q | _lib.G4_APPEND_ROPE_Q
+    flags_kv = _lib.G4_APPEND_NORM_K | _lib.G4_APPEND_ROPE_K | _lib.G4_APPEND_NORM_V
+    prompt_kv: dict = {}  # layer index -> (k [B,H,Sp,D], vt [B,H,D,Sp]) for prefill attention
+    new_layers = []
+    for i, (lp, pk) in enumerate(zip(params.layers, pw.layers)):
+        lt = config.layer_types[i]
+        window = config.sliding_window if lt == SLIDING else 0
+        H, R, D = pk.heads, pk.group, pk.head_dim
+        residual = x
+        h = rms_norm(x, lp.input_norm.weight, eps)
+        qkv = (h.reshape(B * S, -1) @ pk.w_qkv).reshape(B, S, -1)
+        q = qkv[..., : H * R * D].view(B, S, H, R, D)
+        q_out = torch.empty((B, S, H, R, D), dtype=x.dtype, device=dev)
+        cos, sin = rot[lt]
+        layer_cache = kv_cache.layers[i]
+        if is_kv_shared(config, i):
+            kernels.prepare_q(q, q_out, q_norm_weight=lp.attention.q_norm.weight, eps=eps, rope_cos=cos,
+                              rope_sin=sin, flags=flags_q)
+            src = sources[i]
+            src_cache = new_layers[src]
+            new_layers.append(None)
+        else:
+            k = qkv[..., H * R * D: (H * R + H) * D].view(B, S, H, D)
+            v = qkv[..., (H * R + H) * D:].view(B, S, H, D) if pk.has_v else k
+            k_out = vt_out = None
+            if cache_mode == "prefill" and layer_cache.ring:
+                sp = slot_stride_for(S)
+                k_out = torch.empty((B, H, sp, D), dtype=x.dtype, device=dev)
+                vt_out = torch.zeros((B, H, D, sp), dtype=x.dtype, device=dev)
+            kernels.kv_append(layer_cache, k, v, write_pos=length, flags=flags_q | flags_kv, eps=eps, q=q,
+                              q_out=q_out, q_norm_weight=lp.attention.q_norm.weight,
+                              k_norm_weight=lp.attention.k_norm.weight, rope_cos=cos, rope_sin=sin, k_out=k_out,
+                              vt_out=vt_out)
+            if k_out is not None:
+                prompt_kv[i] = (k_out, vt_out)
+            src = i
+            src_cache = layer_cache
+            new_layers.append(layer_cache)
+        if cache_mode == "prefill":
+            if length != 0:
+                raise NotImplementedError("prefill into a non-empty cache is not supported")
+            if src in prompt_kv:
+                kk, vt = prompt_kv[src]
+            else:
+                kk, vt = src_cache.key, src_cache.value_t
+            attn = kernels.prefill_attention(q_out, kk, vt, key_mask, window=window)
+        else:
+            attn = kernels.decode_attention(src_cache, q_out.view(B, H, R, D), key_mask, q_pos=length,
+                                            window=config.sliding_window).view(B, 1, H, R, D)
+        o = (attn.reshape(B * S, H * R * D) @ pk.w_o).reshape(B, S, -1)
+        o = rms_norm(o, lp.post_attention_norm.weight, eps)
+        x = residual + o
+        residual = x
+        h = rms_norm(x, lp.pre_feedforward_norm.weight, eps)
+        gu = h.reshape(B * S, -1) @ pk.w_gate_up
+        F = gu.shape[1] // 2
+        act = (gelu_tanh_f32(gu[:, :F]) * gu[:, F:].float()).to(x.dtype)
+        d = (act @ pk.w_down).reshape(B, S, -1)
+        d = rms_norm(d, lp.post_feedforward_norm.weight, eps)
+        x = residual + d
+        if lp.per_layer_input is not None:
+            g = x.reshape(B * S, -1) @ lp.per_layer_input.gate
+            g = (gelu_tanh_f32(g) * pli[:, :, i].reshape(B * S, -1).float()).to(x.dtype)
+            g = (g @ lp.per_layer_input.projection).reshape(B, S, -1)
+            g = rms_norm(g, lp.per_layer_input.post_norm.weight, eps)
+            x = x + g
+        x = (x.float() * lp.layer_scalar.float()).to(x.dtype)
+    hidden = rms_norm(x, params.final_norm.weight, eps)
+    if scratch_cache:
+        return hidden, None
+    return hidden, KVCache(tuple(new_layers), key_mask, length + S)
+
+
+def forward_lm_head(embed_tokens: torch.Tensor, hidden: torch.Tensor, softcap: float | None) -> torch.Tensor:
+    """model.py:676-680: tied-embedding logits, ``tanh(x / cap) * cap``."""
+
+    B, S, M = hidden.shape
+    logits = (hidden.reshape(B * S, M) @ embed_tokens.t()).reshape(B, S, -1)
+    if softcap is not None:
+        logits = (torch.tanh(logits.float() / softcap) * softcap).to(logits.dtype)
+    return logits
+
+
+def forward_gemma4_lm(
+    params: Gemma4TextParams,
+    input_ids: torch.Tensor,
+    position_ids: torch.Tensor,
+    *,
+    config: Gemma4TextConfig,
+    attention_mask: torch.Tensor | None = None,
+    kv_cache: KVCache | None = None,
+    cache_mode: Literal["prefill", "append"] = "prefill",
+    logits_to_keep: int = 0,
+    lora=None,
+) -> Gemma4Output:
+    """model.py:683-709."""
+
+    hidden, cache = forward_gemma4_text(params, input_ids, position_ids, config=config,
+                                        attention_mask=attention_mask, kv_cache=kv_cache, cache_mode=cache_mode,
+                                        lora=lora)
+    head_in = hidden[:, -logits_to_keep:] if logits_to_keep > 0 else hidden
+    return Gemma4Output(forward_lm_head(params.embed_tokens, head_in, config.final_logit_softcapping), hidden, cache)
+
+
+__all__ = [
+    "RMSNormParams", "AttentionParams", "MLPParams", "PerLayerInputParams", "DecoderLayerParams",
+    "Gemma4TextParams", "Gemma4Output", "Gemma4TextConfig", "KVCache", "LayerKVCache", "init_kv_cache",
+    "forward_gemma4_text", "forward_gemma4_lm", "forward_lm_head", "params_from_numpy", "pack_weights",
+    "rms_norm", "layer_head_dim", "layer_kv_heads", "layer_has_v_proj", "layer_intermediate_size",
+]

@@ -1,0 +1,189 @@
+/*
+ * g4_rollout.h — C ABI of libg4rollout.so, the MI355X (gfx950) kernels behind the Gemma 4
+ * rollout prefill + KV-cache decode path of gemma4_posttrain_jax.
+ *
+ * The reference has no native layer: each entry point below replaces an XLA-lowered JAX
+ * expression of gemma4_posttrain_jax/model.py, cited per function. All entry points are
+ * stream-ordered on the `hipStream_t` passed as `stream`, launch nothing else, allocate
+ * nothing, never synchronise the device, and keep no state between calls (reentrant). They
+ * return 0 on success or a negative G4_ERR_* code after a host-side argument check, before any
+ * launch; `g4_last_error()` then describes the failure (thread-local text).
+ *
+ * Device data layout (per cache layer, element type = `dtype`):
+ *   cache_k   [B, Hkv, slot_stride, D]   key rows, head-major; row b,h,slot at
+ *             ((b*Hkv + h)*slot_stride + slot)*D
+ *   cache_vt  [B, Hkv, D, slot_stride]   values stored transposed (d-major); value (b,h,slot,d)
+ *             at ((b*Hkv + h)*D + d)*slot_stride + slot
+ * `capacity` is the logical slot count: C (= prompt + new tokens) for a linear (global-layer)
+ * cache, Wc = min(window, C) for a ring (sliding-layer) cache. `slot_stride` >= capacity is a
+ * multiple of 64, so every K row and V^T row starts 128-byte aligned.
+ * Query/output rows of one kv head are contiguous: q and attention output are
+ * [B, S, Hkv, R, D] (R = query heads per kv head; reference head order is h*R + r).
+ * key_mask is [B, key_mask_stride] uint8 over absolute positions (1 = real token).
+ */
+#ifndef G4_ROLLOUT_H
+#define G4_ROLLOUT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  G4_OK = 0,
+  G4_ERR_INVALID = -1,     /* bad shape / null pointer / unsupported combination */
+  G4_ERR_UNSUPPORTED = -2, /* valid but not implemented for this dtype / size */
+  G4_ERR_LAUNCH = -3,      /* the HIP launch itself failed */
+  G4_ERR_WORKSPACE = -4    /* workspace missing or too small */
+};
+
+enum { G4_DTYPE_F32 = 0, G4_DTYPE_BF16 = 1 };
+enum { G4_CACHE_LINEAR = 0, G4_CACHE_RING = 1 };
+
+/* Flags of G4AppendArgs.flags. */
+enum {
+  G4_APPEND_NORM_K = 1, /* k = RMSNorm(k) * k_norm_weight (model.py:480) */
+  G4_APPEND_NORM_V = 2, /* v = RMSNorm(v), no scale (model.py:482) */
+  G4_APPEND_ROPE_K = 4, /* k = k*cos + rotate_half(k)*sin (model.py:481, 309-317) */
+  G4_APPEND_NORM_Q = 8, /* q = RMSNorm(q) * q_norm_weight (model.py:465) */
+  G4_APPEND_ROPE_Q = 16 /* q = RoPE(q) (model.py:466) */
+};
+
+/*
+ * Fused q/k/v preparation + cache append. Replaces, for one layer:
+ *   forward_rms_norm(q_norm) + forward_rotary_embedding on q   (model.py:465-466)
+ *   forward_rms_norm(k_norm) + forward_rotary_embedding on k   (model.py:480-481)
+ *   forward_rms_norm(None) on v                                 (model.py:482)
+ *   _update_layer_cache(cache, k, v, start, circular)           (model.py:368-390)
+ * Each of S new tokens of row b is written at absolute position p = write_pos[b] + s; a linear
+ * cache stores it in slot p, a ring cache in slot p mod Wc, and of a chunk longer than Wc only
+ * the last Wc tokens are stored (model.py:383-386). With flags == 0 and q == NULL this is the
+ * pure data movement of _update_layer_cache and is bit-exact. With k == v == NULL only q is
+ * prepared (kv-shared layers, model.py:469-470). RoPE tables are f32 [B, S, D]
+ * (model.py:288-291); they are rounded to `dtype` before use, as model.py:313-314 does.
+ */
+typedef struct G4AppendArgs {
+  int32_t dtype;        /* G4_DTYPE_*: inputs, cache and outputs */
+  int32_t kind;         /* G4_CACHE_LINEAR or G4_CACHE_RING */
+  int32_t batch;        /* B */
+  int32_t seq;          /* S new tokens per row */
+  int32_t kv_heads;     /* Hkv */
+  int32_t group;        /* R = query heads per kv head (only read when q != NULL) */
+  int32_t head_dim;     /* D: 64, 128, 256 or 512 */
+  int32_t capacity;     /* logical slots: C (linear) or Wc (ring) */
+  int32_t slot_stride;  /* physical slots per (b, h): >= capacity, multiple of 64 */
+  int32_t flags;        /* G4_APPEND_* */
+  float eps;            /* RMSNorm epsilon */
+  int32_t write_pos_scalar;   /* start position used when write_pos == NULL (the reference's scalar length) */
+  const int32_t* write_pos;   /* device [B] per-row start position, or NULL */
+  const void* k;        /* token (b,s): k + (b*S + s)*in_row_stride, heads [Hkv, D] */
+  const void* v;        /* same indexing as k (may alias k: K=V layers, model.py:479) */
+  const void* q;        /* optional: token (b,s): q + (b*S + s)*in_row_stride, heads [Hkv, R, D] */
+  int64_t in_row_stride;      /* elements between consecutive tokens of q / k / v */
+  const void* q_norm_weight;  /* [D] in dtype (G4_APPEND_NORM_Q) */
+  const void* k_norm_weight;  /* [D] in dtype (G4_APPEND_NORM_K) */
+  const float* rope_cos;      /* [B, S, D] f32 (G4_APPEND_ROPE_*) */
+  const float* rope_sin;      /* [B, S, D] f32 */
+  void* cache_k;        /* [B, Hkv, slot_stride, D] */
+  void* cache_vt;       /* [B, Hkv, D, slot_stride] */
+  void* q_out;          /* optional [B, S, Hkv, R, D] prepared q */
+  void* k_out;          /* optional [B, Hkv, chunk_stride, D] prepared k of this chunk (prefill input) */
+  void* vt_out;         /* optional [B, Hkv, D, chunk_stride] prepared v, transposed */
+  int32_t chunk_stride; /* >= S, multiple of 64; required when k_out or vt_out is set */
+} G4AppendArgs;
+
+int g4_kv_append(const G4AppendArgs* args, void* stream);
+
+/*
+ * One-token GQA decode attention over a ring or linear cache. Replaces
+ * make_cached_qk_masks (model.py:338-365) + the score/softmax/value einsums of
+ * forward_attention (model.py:496-499) for S = 1, scale 1.0.
+ * The query of row b sits at absolute position q_pos[b] (the cache length before this token's
+ * append, i.e. the last written position). Validity of a key:
+ *   linear slot t:  t <= q  and key_mask[b, t]
+ *   ring slot r:    p = r + floor((q - r)/Wc)*Wc, p >= 0, p > q - window, key_mask[b, p]
+ * Rounding follows the reference: scores rounded to `dtype`, masked scores = finfo(dtype).min,
+ * f32 softmax over the whole row, probabilities rounded to `dtype`, f32-accumulated
+ * probs @ v rounded to `dtype`. A row with no valid key averages all `capacity` slots, as the
+ * reference's softmax over an all-min row does. Exact global softmax normalisation (not an
+ * online rescale) keeps the probability rounding identical to the reference's.
+ * With new_k/new_v set, the kernel first stores this token's K/V row (prepared, [B, Hkv, D])
+ * at position q_pos[b] — the fused append — and attends over the updated cache.
+ */
+typedef struct G4DecodeArgs {
+  int32_t dtype;
+  int32_t kind;
+  int32_t batch;
+  int32_t kv_heads;
+  int32_t group;        /* R <= 16 */
+  int32_t head_dim;     /* 64, 128, 256 or 512 */
+  int32_t capacity;     /* C or Wc */
+  int32_t slot_stride;
+  int32_t window;       /* sliding window W (ring caches); ignored for linear */
+  int32_t q_pos_scalar; /* used when q_pos == NULL */
+  const int32_t* q_pos; /* device [B] or NULL */
+  const uint8_t* key_mask;     /* device [B, key_mask_stride] */
+  int32_t key_mask_stride;     /* >= the largest absolute position + 1 (the full capacity C) */
+  const void* q;        /* [B, Hkv, R, D] */
+  const void* cache_k;  /* [B, Hkv, slot_stride, D] */
+  void* cache_vt;       /* [B, Hkv, D, slot_stride]; written only with new_v */
+  void* cache_k_w;      /* same as cache_k, writable; required with new_k */
+  const void* new_k;    /* optional [B, Hkv, D] */
+  const void* new_v;    /* optional [B, Hkv, D] */
+  void* out;            /* [B, Hkv, R, D] */
+  void* workspace;      /* split-K scratch, >= g4_decode_workspace_size(args) bytes */
+  size_t workspace_bytes;
+  int32_t num_splits;   /* 0 = choose automatically; 1 = one workgroup per (b, h) */
+} G4DecodeArgs;
+
+size_t g4_decode_workspace_size(const G4DecodeArgs* args);
+int g4_decode_attention(const G4DecodeArgs* args, void* stream);
+
+/*
+ * Causal (optionally sliding-window) prefill attention on the chunk's own K/V. Replaces
+ * make_qk_masks (model.py:320-335) + the attention einsums of forward_attention
+ * (model.py:496-499) in prefill mode (model.py:455-457, 621-623). Query s of row b attends key
+ * t iff t <= s, key_mask[b, t] and (window == 0 or t > s - window) — physical indices, pads
+ * count toward the window. Rounding as for g4_decode_attention; a row with no valid key
+ * averages all S keys. bf16 runs on MFMA (v_mfma_f32_16x16x32_bf16).
+ */
+typedef struct G4PrefillArgs {
+  int32_t dtype;
+  int32_t batch;
+  int32_t seq;          /* S (queries = keys) */
+  int32_t kv_heads;
+  int32_t group;        /* R */
+  int32_t head_dim;
+  int32_t window;       /* 0 = global (causal only) */
+  const uint8_t* key_mask;   /* [B, key_mask_stride] */
+  int32_t key_mask_stride;
+  const void* q;        /* [B, S, Hkv, R, D] */
+  const void* k;        /* [B, Hkv, k_stride, D] */
+  const void* vt;       /* [B, Hkv, D, k_stride] */
+  int32_t k_stride;     /* >= S, multiple of 64 */
+  void* out;            /* [B, S, Hkv, R, D] */
+} G4PrefillArgs;
+
+int g4_prefill_attention(const G4PrefillArgs* args, void* stream);
+
+/*
+ * Host-side: KV-sharing map (model.py:153-168). layer_types[i] is 0 (sliding) or 1 (full);
+ * out[i] = index of the layer whose K/V layer i uses (itself when not shared).
+ */
+int g4_kv_source_layers(int32_t num_layers, int32_t num_kv_shared_layers, const int32_t* layer_types,
+                        int32_t* out);
+
+/* Host-side ring-slot arithmetic (model.py:355-357), the same code the kernels run:
+ * out[r] = position held by slot r of a Wc-slot ring after position `last_written` was written
+ * (negative = never written). */
+int g4_ring_slot_positions(int32_t last_written, int32_t window_capacity, int32_t* out);
+
+const char* g4_last_error(void);
+const char* g4_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* G4_ROLLOUT_H */

@@ -1,0 +1,240 @@
+"""GPU parity of the three kernels against the oracle, through the C ABI.
+
+Bars: cache contents after append are bit-exact (pure data movement, and RoPE with the oracle's
+op order); attention outputs are within max-abs 2e-2 (bf16) / 1e-5 (fp32).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import TOL, bits, cache_to_ref, np_bits, ref_to_cache, to_dev, to_np
+from oracle import g4_oracle as O
+
+from gemma4_posttrain_jax_amd import _lib, kernels
+from gemma4_posttrain_jax_amd.kvcache import new_layer_cache
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(rng, shape, dtype):
+    return O.cast(rng.standard_normal(shape, dtype=np.float32), dtype)
+
+
+# --- append ---------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [O.BF16, O.F32])
+@pytest.mark.parametrize("ring", [True, False])
+@pytest.mark.parametrize("S", [1, 5, 40])
+def test_append_is_bit_exact(device, dtype, ring, S):
+    """_update_layer_cache (model.py:368-390): per-row start positions, chunks longer than the ring."""
+
+    rng = np.random.default_rng(S + 10 * ring)
+    B, H, D = 3, 2, 64
+    cap = 16 if ring else 64
+    layer = new_layer_cache(B, H, D, cap, ring, __import__("gpu_util").TORCH_DTYPE[dtype], device)
+    k0, v0 = _rand(rng, (B, cap, H, D), dtype), _rand(rng, (B, cap, H, D), dtype)
+    ref_to_cache(layer, k0, v0, dtype)
+    k, v = _rand(rng, (B, S, H, D), dtype), _rand(rng, (B, S, H, D), dtype)
+    starts = rng.integers(0, 50 if ring else cap - S + 1, B).astype(np.int32)
+    kernels.kv_append(layer, to_dev(k, dtype, device), to_dev(v, dtype, device),
+                      write_pos=torch.from_numpy(starts).to(device))
+    ref = O.update_layer_cache(O.LayerKV(k0, v0), k, v, starts, ring, dtype)
+    gk, gv = cache_to_ref(layer)
+    np.testing.assert_array_equal(np_bits(gk, dtype), np_bits(ref.key, dtype))
+    np.testing.assert_array_equal(np_bits(gv, dtype), np_bits(ref.value, dtype))
+    # scalar start (the reference's single `length`)
+    kernels.kv_append(layer, to_dev(k, dtype, device), to_dev(v, dtype, device), write_pos=int(starts[0]))
+    ref = O.update_layer_cache(ref, k, v, int(starts[0]), ring, dtype)
+    gk, gv = cache_to_ref(layer)
+    np.testing.assert_array_equal(np_bits(gk, dtype), np_bits(ref.key, dtype))
+    np.testing.assert_array_equal(np_bits(gv, dtype), np_bits(ref.value, dtype))
+
+
+@pytest.mark.parametrize("dtype", [O.BF16, O.F32])
+@pytest.mark.parametrize("D", [64, 256])
+def test_append_fused_rope_is_bit_exact(device, dtype, D):
+    """RoPE'd K append (model.py:309-317 + 368-390) with the oracle's rounding order."""
+
+    rng = np.random.default_rng(D)
+    B, S, H, cap = 2, 7, 2, 32
+    layer = new_layer_cache(B, H, D, cap, False, __import__("gpu_util").TORCH_DTYPE[dtype], device)
+    k, v = _rand(rng, (B, S, H, D), dtype), _rand(rng, (B, S, H, D), dtype)
+    pos = rng.integers(0, 5000, (B, S)).astype(np.int32)
+    inv = O.rope_inv_freq(O.config_from_hf(dict(
+        vocab_size=8, hidden_size=8, intermediate_size=8, num_hidden_layers=1, num_attention_heads=2,
+        num_key_value_heads=1, head_dim=D, global_head_dim=D, layer_types=["sliding_attention"])))[O.FULL]
+    cos, sin = O.rotary_values(inv, pos)
+    kernels.kv_append(layer, to_dev(k, dtype, device), to_dev(v, dtype, device), write_pos=3,
+                      flags=_lib.G4_APPEND_ROPE_K, rope_cos=torch.from_numpy(cos).to(device),
+                      rope_sin=torch.from_numpy(sin).to(device))
+    ref = O.update_layer_cache(O.LayerKV(np.zeros((B, cap, H, D), np.float32), np.zeros((B, cap, H, D), np.float32)),
+                               O.rope(k, cos, sin, dtype), v, 3, False, dtype)
+    gk, gv = cache_to_ref(layer)
+    np.testing.assert_array_equal(np_bits(gk, dtype), np_bits(ref.key, dtype))
+    np.testing.assert_array_equal(np_bits(gv, dtype), np_bits(ref.value, dtype))
+
+
+@pytest.mark.parametrize("dtype", [O.BF16, O.F32])
+def test_append_with_norms_and_q_matches_oracle(device, dtype):
+    """q/k norm + RoPE, unscaled v norm, prefill chunk outputs (model.py:463-482)."""
+
+    rng = np.random.default_rng(3)
+    B, S, H, R, D, cap = 2, 9, 2, 4, 128, 64
+    width = (H * R + 2 * H) * D
+    rows = _rand(rng, (B, S, width), dtype)
+    qn, kn = O.cast(1 + 0.3 * rng.standard_normal(D), dtype), O.cast(1 + 0.3 * rng.standard_normal(D), dtype)
+    pos = np.tile(np.arange(S, dtype=np.int32), (B, 1))
+    cos, sin = O.rotary_values(np.float32(1) / np.power(np.float32(1e4), np.arange(0, D, 2, dtype=np.float32) / D), pos)
+    layer = new_layer_cache(B, H, D, cap, True, __import__("gpu_util").TORCH_DTYPE[dtype], device)
+    rows_d = to_dev(rows, dtype, device)
+    q = rows_d[:, :, : H * R * D].view(B, S, H, R, D)
+    k = rows_d[:, :, H * R * D: (H * R + H) * D].view(B, S, H, D)
+    v = rows_d[:, :, (H * R + H) * D:].view(B, S, H, D)
+    q_out = torch.empty((B, S, H, R, D), dtype=q.dtype, device=device)
+    k_out = torch.empty((B, H, 64, D), dtype=q.dtype, device=device)
+    vt_out = torch.empty((B, H, D, 64), dtype=q.dtype, device=device)
+    flags = (_lib.G4_APPEND_NORM_Q | _lib.G4_APPEND_ROPE_Q | _lib.G4_APPEND_NORM_K | _lib.G4_APPEND_ROPE_K
+             | _lib.G4_APPEND_NORM_V)
+    kernels.kv_append(layer, k, v, write_pos=0, flags=flags, eps=1e-6, q=q, q_out=q_out,
+                      q_norm_weight=to_dev(qn, dtype, device), k_norm_weight=to_dev(kn, dtype, device),
+                      rope_cos=torch.from_numpy(cos).to(device), rope_sin=torch.from_numpy(sin).to(device),
+                      k_out=k_out, vt_out=vt_out)
+    qr = rows[:, :, : H * R * D].reshape(B, S, H, R, D)
+    kr = rows[:, :, H * R * D: (H * R + H) * D].reshape(B, S, H, D)
+    vr = rows[:, :, (H * R + H) * D:].reshape(B, S, H, D)
+    q_ref = O.rope(O.rms_norm(qn, qr, 1e-6, dtype), cos, sin, dtype)
+    k_ref = O.rope(O.rms_norm(kn, kr, 1e-6, dtype), cos, sin, dtype)
+    v_ref = O.rms_norm(None, vr, 1e-6, dtype)
+    tol = TOL[dtype]
+    np.testing.assert_allclose(to_np(q_out), q_ref, atol=tol, rtol=0)
+    np.testing.assert_allclose(to_np(k_out[:, :, :S]).transpose(0, 2, 1, 3), k_ref, atol=tol, rtol=0)
+    np.testing.assert_allclose(to_np(vt_out[:, :, :, :S]).transpose(0, 3, 1, 2), v_ref, atol=tol, rtol=0)
+    ref = O.update_layer_cache(O.LayerKV(np.zeros((B, cap, H, D), np.float32), np.zeros((B, cap, H, D), np.float32)),
+                               k_ref, v_ref, 0, True, dtype)
+    gk, gv = cache_to_ref(layer)
+    np.testing.assert_allclose(gk, ref.key, atol=tol, rtol=0)
+    np.testing.assert_allclose(gv, ref.value, atol=tol, rtol=0)
+
+
+# --- decode attention -----------------------------------------------------------------------------
+
+
+def _decode_case(device, dtype, *, B, H, R, D, cap, ring, window, q_pos, key_mask, fused, seed):
+    rng = np.random.default_rng(seed)
+    td = __import__("gpu_util").TORCH_DTYPE[dtype]
+    layer = new_layer_cache(B, H, D, cap, ring, td, device)
+    k0, v0 = _rand(rng, (B, cap, H, D), dtype), _rand(rng, (B, cap, H, D), dtype)
+    ref_to_cache(layer, k0, v0, dtype)
+    q = _rand(rng, (B, H, R, D), dtype)
+    nk, nv = _rand(rng, (B, H, D), dtype), _rand(rng, (B, H, D), dtype)
+    qp = torch.from_numpy(q_pos.astype(np.int32)).to(device)
+    km = torch.from_numpy(key_mask).to(device)
+    if fused:
+        out = kernels.decode_attention(layer, to_dev(q, dtype, device), km, q_pos=qp, window=window,
+                                       new_k=to_dev(nk, dtype, device), new_v=to_dev(nv, dtype, device))
+        ref_kv = O.update_layer_cache(O.LayerKV(k0, v0), nk[:, None], nv[:, None], q_pos, ring, dtype)
+    else:
+        out = kernels.decode_attention(layer, to_dev(q, dtype, device), km, q_pos=qp, window=window)
+        ref_kv = O.LayerKV(k0, v0)
+    masks = O.make_cached_qk_masks(key_mask, window if ring else 1 << 30, q_pos, 1)
+    mask = masks[O.SLIDING] if ring else masks[O.FULL]
+    q_ref = q.transpose(0, 2, 1, 3)[:, None]  # [B, 1, R, H, D]
+    o_ref = O.attention_core(q_ref, ref_kv.key, ref_kv.value, mask, dtype)[:, 0].transpose(0, 2, 1, 3)
+    got = to_np(out)
+    err = np.abs(got - o_ref).max()
+    assert err <= TOL[dtype], f"max |out - oracle| = {err}"
+    if fused:
+        gk, gv = cache_to_ref(layer)
+        np.testing.assert_array_equal(np_bits(gk, dtype), np_bits(ref_kv.key, dtype))
+        np.testing.assert_array_equal(np_bits(gv, dtype), np_bits(ref_kv.value, dtype))
+    return err
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_ring_config2_shape(device, fused):
+    """B64, Hq8/Hkv2, D256, W512 ring that has wrapped several times;
+    per-row write positions U[1536, 2048)."""
+
+    rng = np.random.default_rng(2)
+    B, H, R, D, W = 64, 2, 4, 256, 512
+    q_pos = rng.integers(1536, 2048, B)
+    key_mask = np.ones((B, 2048), bool)
+    _decode_case(device, O.BF16, B=B, H=H, R=R, D=D, cap=W, ring=True, window=W, q_pos=q_pos, key_mask=key_mask,
+                 fused=fused, seed=20)
+
+
+@pytest.mark.parametrize("dtype", [O.BF16, O.F32])
+def test_decode_ring_partial_and_masked_rows(device, dtype):
+    """Ring not yet full, left padding, a finished row and a fully masked row (uniform average)."""
+
+    B, H, R, D, W = 4, 2, 4, 64, 16
+    q_pos = np.array([5, 20, 40, 33])
+    key_mask = np.ones((B, 48), bool)
+    key_mask[1, :3] = False
+    key_mask[2, 30:] = False  # finished row: positions after 29 are pads
+    key_mask[3, :] = False  # every key masked
+    _decode_case(device, dtype, B=B, H=H, R=R, D=D, cap=W, ring=True, window=W, q_pos=q_pos, key_mask=key_mask,
+                 fused=True, seed=21)
+
+
+@pytest.mark.parametrize("dtype", [O.BF16, O.F32])
+def test_decode_linear_ragged(device, dtype):
+    """Global-layer linear cache, ragged lengths, left padding, a fully masked row."""
+
+    rng = np.random.default_rng(4)
+    B, H, R, D, C = 5, 2, 4, 128 if dtype == O.BF16 else 64, 1000
+    q_pos = rng.integers(0, C, B)
+    q_pos[0] = C - 1
+    key_mask = np.ones((B, C), bool)
+    key_mask[1, :17] = False
+    key_mask[2, :] = False
+    _decode_case(device, dtype, B=B, H=H, R=R, D=D, cap=C, ring=False, window=0, q_pos=q_pos, key_mask=key_mask,
+                 fused=True, seed=22)
+
+
+def test_decode_is_deterministic(device):
+    rng = np.random.default_rng(9)
+    B, H, R, D, W = 8, 2, 4, 256, 512
+    layer = new_layer_cache(B, H, D, W, True, torch.bfloat16, device)
+    layer.key.normal_()
+    layer.value_t.normal_()
+    q = torch.randn((B, H, R, D), device=device).to(torch.bfloat16)
+    km = torch.ones((B, 4096), dtype=torch.bool, device=device)
+    qp = torch.from_numpy(rng.integers(600, 4000, B).astype(np.int32)).to(device)
+    a = kernels.decode_attention(layer, q, km, q_pos=qp, window=W)
+    b = kernels.decode_attention(layer, q, km, q_pos=qp, window=W)
+    assert torch.equal(a, b)
+
+
+# --- prefill attention ----------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype,D", [(O.BF16, 256), (O.BF16, 64), (O.F32, 64)])
+@pytest.mark.parametrize("window", [0, 48])
+def test_prefill_matches_oracle(device, dtype, D, window):
+    """Causal + sliding-window prefill with left padding (fully masked pad queries)."""
+
+    rng = np.random.default_rng(D + window)
+    B, S, H, R = 2, 150, 2, 4
+    Sp = (S + 63) // 64 * 64
+    q = _rand(rng, (B, S, H, R, D), dtype)
+    k = _rand(rng, (B, S, H, D), dtype)
+    v = _rand(rng, (B, S, H, D), dtype)
+    key_mask = np.ones((B, S), bool)
+    key_mask[1, :11] = False
+    td = __import__("gpu_util").TORCH_DTYPE[dtype]
+    kd = torch.zeros((B, H, Sp, D), dtype=td, device=device)
+    vtd = torch.zeros((B, H, D, Sp), dtype=td, device=device)
+    kd[:, :, :S] = to_dev(k, dtype, device).permute(0, 2, 1, 3)
+    vtd[:, :, :, :S] = to_dev(v, dtype, device).permute(0, 2, 3, 1)
+    out = kernels.prefill_attention(to_dev(q, dtype, device), kd, vtd, torch.from_numpy(key_mask).to(device),
+                                    window=window)
+    masks = O.make_qk_masks(key_mask, window if window else 1 << 30, 0, S)
+    q_ref = q.transpose(0, 1, 3, 2, 4)  # [B, S, R, H, D]
+    o_ref = O.attention_core(q_ref, k, v, masks[O.SLIDING], dtype).transpose(0, 1, 3, 2, 4)
+    err = np.abs(to_np(out) - o_ref).max()
+    assert err <= TOL[dtype], f"max |out - oracle| = {err}"
