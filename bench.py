@@ -1,0 +1,350 @@
+"""Benchmark of the Gemma 4 rollout decode hot path on one MI355X.
+
+Headline (BASELINE.json ``configs[1]``): sliding-window decode attention, B=64, Hq=8/Hkv=2,
+D=256, W=512 bf16 ring already holding 2048 tokens (per-row write positions U[1536, 2048)); a
+step appends one token per row and attends (one launch of the fused append + decode kernel).
+``value`` = algorithmic bytes per step / time per step, in GB/s. Steps are replayed from a HIP
+graph so the timed region holds only GPU work.
+
+Also reported: ``decode_tok_s_b256`` — full decode steps (30-layer E2B-like model, B=256, T=1
+sampling, BASELINE ``configs[4]``) per second x 256, and the oracle's CPU time for the same step.
+
+Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2b] [--no-cpu]``.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+# configs[1]
+B, HQ, HKV, D, W = 64, 8, 2, 256, 512
+R = HQ // HKV
+CTX = 2048
+NCACHE = 8
+
+
+def algorithmic_bytes_per_step() -> int:
+    """K+V of every valid slot once, Q in, O out, the new token's K/V read and written."""
+
+    kv = B * HKV * W * D * 2 * 2
+    q = B * HQ * D * 2
+    o = B * HQ * D * 2
+    new_kv = B * HKV * D * 2 * 2 * 2
+    return kv + q + o + new_kv
+
+
+def cpu_info() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def bench_decode_attention(steps: int, warmup: int) -> dict:
+    import torch
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    from gemma4_posttrain_jax_amd import kernels
+    from gemma4_posttrain_jax_amd.kvcache import new_layer_cache
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    # NCACHE independent config-2 ring caches (64 MiB each), used round-robin: a step reads a
+    # cache last touched NCACHE steps earlier, so the 256 MB Infinity Cache cannot serve it from a
+    # previous step -- as in the full model, where ~12 GB of other layers' KV and weights stream
+    # between two visits of one layer's cache.
+    layers = []
+    for _ in range(NCACHE):
+        layer = new_layer_cache(B, HKV, D, W, True, torch.bfloat16, dev)
+        layer.key.normal_(generator=g)
+        layer.value_t.normal_(generator=g)
+        layers.append(layer)
+    rng = np.random.default_rng(0)
+    pos0 = rng.integers(1536, 2048, B).astype(np.int32)
+    total = warmup + steps
+    # per-step query positions, new K/V rows, queries and outputs (separate buffers per step so
+    # the graph replays exactly the K distinct steps)
+    q_pos = torch.from_numpy(pos0[None, :] + np.arange(total, dtype=np.int32)[:, None]).to(dev).contiguous()
+    key_mask = torch.ones((B, CTX + total + 64), dtype=torch.bool, device=dev)
+    q = torch.randn((total, B, HKV, R, D), device=dev, generator=g).to(torch.bfloat16)
+    nk = torch.randn((total, B, HKV, D), device=dev, generator=g).to(torch.bfloat16)
+    nv = torch.randn((total, B, HKV, D), device=dev, generator=g).to(torch.bfloat16)
+    out = torch.empty((total, B, HKV, R, D), device=dev, dtype=torch.bfloat16)
+
+    def step(i):
+        kernels.decode_attention(layers[i % NCACHE], q[i], key_mask, q_pos=q_pos[i], window=W, out=out[i],
+                                 new_k=nk[i], new_v=nv[i])
+
+    # eager warmup (also compiles nothing: the library is prebuilt)
+    for i in range(min(total, 3)):
+        step(i)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g_warm, g_timed = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g_warm, stream=s):
+            for i in range(warmup):
+                step(i)
+        with torch.cuda.graph(g_timed, stream=s):
+            for i in range(warmup, total):
+                step(i)
+    torch.cuda.synchronize()
+    if warmup:
+        g_warm.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    g_timed.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    # second replay, eager launches, for reference (host launch overhead included)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(warmup, total):
+        step(i)
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3
+    return {"ms_total": ms, "ms_per_step": ms / steps, "eager_ms_per_step": eager_ms / steps}
+
+
+def cpu_baseline_decode_attention(target_s: float = 12.0) -> dict:
+    """The oracle's decode attention (reference semantics: dense masked softmax over all W ring
+    slots, bf16 rounding emulated) on the host, for the same config-2 step."""
+
+    from oracle import g4_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    rng = np.random.default_rng(0)
+    k = O.bf16_round(rng.standard_normal((B, W, HKV, D), dtype=np.float32))
+    v = O.bf16_round(rng.standard_normal((B, W, HKV, D), dtype=np.float32))
+    key_mask = np.ones((B, CTX + 64), bool)
+    pos = rng.integers(1536, 2048, B)
+    times = []
+    t_begin = time.perf_counter()
+    n = 0
+    while True:
+        q = O.bf16_round(rng.standard_normal((B, 1, R, HKV, D), dtype=np.float32))
+        nk = O.bf16_round(rng.standard_normal((B, 1, HKV, D), dtype=np.float32))
+        t0 = time.perf_counter()
+        with O.inplace_cache_updates():
+            layer = O.update_layer_cache(O.LayerKV(k, v), nk, nk, pos + n, True, O.BF16)
+        mask = O.make_cached_qk_masks(key_mask, W, pos + n, 1)[O.SLIDING]
+        O.attention_core(q, layer.key, layer.value, mask, O.BF16)
+        times.append(time.perf_counter() - t0)
+        n += 1
+        if time.perf_counter() - t_begin > target_s and n >= 3:
+            break
+    sec = float(np.median(times[1:])) if len(times) > 1 else times[0]
+    return {
+        "value": algorithmic_bytes_per_step() / sec / 1e9,
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{n} config-2 decode steps (append + attention over the 512-slot ring) through the numpy oracle; "
+                  f"median {sec * 1e3:.1f} ms/step on {cpu_info()}",
+        "s_per_step": sec,
+    }
+
+
+E2B = dict(
+    vocab_size=262144, hidden_size=2048, intermediate_size=8192, num_hidden_layers=30, num_attention_heads=8,
+    num_key_value_heads=2, head_dim=256, global_head_dim=256,
+    layer_types=(["sliding_attention"] * 4 + ["full_attention"]) * 6, sliding_window=512, num_kv_shared_layers=10,
+    hidden_size_per_layer_input=0, final_logit_softcapping=30.0,
+)
+
+
+def random_params(cfg, dev, seed=0):
+    """Random-init E2B-like bf16 weights ~N(0, 0.02), norms 1, layer_scalar 1 (on the GPU)."""
+
+    import torch
+
+    from gemma4_posttrain_jax_amd import model as M
+    from gemma4_posttrain_jax_amd.config import (
+        is_kv_shared, layer_has_v_proj, layer_head_dim, layer_intermediate_size, layer_kv_heads)
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def w(*shape):
+        return (torch.randn(shape, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+
+    def n(dim):
+        return M.RMSNormParams(torch.ones(dim, device=dev, dtype=torch.bfloat16))
+
+    Mh = cfg.hidden_size
+    layers = []
+    for i in range(cfg.num_hidden_layers):
+        Dh, H = layer_head_dim(cfg, i), layer_kv_heads(cfg, i)
+        Rr = cfg.num_attention_heads // H
+        sh = is_kv_shared(cfg, i)
+        att = M.AttentionParams(w(Mh, Rr, H, Dh), None if sh else w(Mh, H, Dh),
+                                None if sh or not layer_has_v_proj(cfg, i) else w(Mh, H, Dh), w(Rr, H, Dh, Mh), n(Dh),
+                                None if sh else n(Dh))
+        F = layer_intermediate_size(cfg, i)
+        layers.append(M.DecoderLayerParams(n(Mh), att, n(Mh), n(Mh), M.MLPParams(w(Mh, F), w(Mh, F), w(F, Mh)), n(Mh),
+                                           None, torch.ones((), device=dev, dtype=torch.bfloat16)))
+    return M.Gemma4TextParams(w(cfg.vocab_size, Mh), None, None, None, tuple(layers), n(Mh))
+
+
+def bench_e2b_decode(steps: int, warmup: int, batch: int = 256, prompt: int = 256, new_tokens: int = 512) -> dict:
+    """Full decode steps (sample at T=1 + one-token forward of all 30 layers + LM head) at B=256."""
+
+    import torch
+
+    from gemma4_posttrain_jax_amd import config as C
+    from gemma4_posttrain_jax_amd import sampler as SMP
+
+    dev = torch.device("cuda:0")
+    cfg = C.config_from_hf(E2B)
+    params = random_params(cfg, dev)
+    g = torch.Generator(device=dev).manual_seed(1)
+    ids = torch.randint(0, cfg.vocab_size, (batch, prompt), device=dev, generator=g, dtype=torch.int32)
+    mask = torch.ones_like(ids, dtype=torch.bool)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = SMP.prefill(params, cfg, ids, mask, max_new_tokens=new_tokens)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    cache = out.kv_cache
+    logits = out.logits[:, -1].float()
+    gen = torch.Generator(device=dev).manual_seed(2)
+    lengths = torch.full((batch,), prompt, dtype=torch.int32, device=dev)
+    times = []
+    for i in range(warmup + steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        tok, _ = SMP._sample_token(logits, gen, temperature=1.0, top_k=0, top_p=1.0)
+        dec = SMP.decode_step(params, cfg, tok, lengths + i, cache)
+        logits = dec.logits[:, -1].float()
+        cache = dec.kv_cache
+        torch.cuda.synchronize()
+        if i >= warmup:
+            times.append(time.perf_counter() - t0)
+    s = float(np.mean(times))
+    return {"decode_s_per_step": s, "decode_tok_s": batch / s, "prefill_s": prefill_s, "params": params, "cfg": cfg,
+            "cache": cache, "logits": logits}
+
+
+def cpu_baseline_e2b_decode(gpu: dict, steps: int = 2) -> dict:
+    """The oracle's full decode step at B=256 on the host (weights copied from the GPU as f32)."""
+
+    import torch
+
+    from oracle import g4_oracle as O
+
+    cfg, params = gpu["cfg"], gpu["params"]
+
+    def a(t):
+        return None if t is None else t.float().cpu().numpy()
+
+    def nw(p):
+        return None if p is None else a(p.weight)
+
+    layers = []
+    for lp in params.layers:
+        at = lp.attention
+        layers.append(O.LayerParams(nw(lp.input_norm), O.AttnParams(a(at.q_proj), a(at.k_proj), a(at.v_proj),
+                                                                    a(at.o_proj), nw(at.q_norm), nw(at.k_norm)),
+                                    nw(lp.post_attention_norm), nw(lp.pre_feedforward_norm),
+                                    O.MLPParams(a(lp.mlp.gate_proj), a(lp.mlp.up_proj), a(lp.mlp.down_proj)),
+                                    nw(lp.post_feedforward_norm), None, np.float32(1.0)))
+    op = O.Params(a(params.embed_tokens), None, None, None, tuple(layers), nw(params.final_norm))
+    ocfg = O.config_from_hf(E2B)
+    Bsz = gpu["logits"].shape[0]
+    length = gpu["cache"].length
+    cap = gpu["cache"].key_mask.shape[1]
+    cache = O.init_kv_cache(ocfg, Bsz, cap, O.BF16)
+    km = np.zeros((Bsz, cap), bool)
+    km[:, :length] = True
+    cache = cache._replace(key_mask=km, length=length)
+    torch.cuda.empty_cache()
+    tok = np.zeros(Bsz, np.int32)
+    times = []
+    with O.inplace_cache_updates():
+        for i in range(steps):
+            t0 = time.perf_counter()
+            logits, _, cache = O.decode_step(op, ocfg, tok, np.full(Bsz, length + i, np.int32), cache, dtype=O.BF16)
+            O.log_softmax_f32(logits[:, -1])
+            times.append(time.perf_counter() - t0)
+    return {"s_per_step": float(np.median(times)), "steps": steps, "cores": len(os.sched_getaffinity(0))}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--e2b-steps", type=int, default=8)
+    ap.add_argument("--no-e2b", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every box here has one GPU)",
+              file=sys.stderr)
+        return 2
+
+    res = bench_decode_attention(args.steps, args.warmup)
+    bytes_step = algorithmic_bytes_per_step()
+    gbs = bytes_step / (res["ms_per_step"] * 1e-3) / 1e9
+    line = {
+        "metric": "decode-attn HBM GB/s (% of peak) + decode tokens/sec at batch 256, 1 GPU",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "configs[1]: sliding-window decode attention, 1-token append + attend per step",
+                   "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "window": W, "ring_context": CTX,
+                   "bytes_per_step": bytes_step, "caches_round_robin": NCACHE},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+        "eager_ms_per_step": round(res["eager_ms_per_step"], 4),
+    }
+    if not args.no_e2b:
+        e2b = bench_e2b_decode(args.e2b_steps, 2)
+        line["decode_tok_s_b256"] = round(e2b["decode_tok_s"], 1)
+        line["decode_ms_per_step_b256"] = round(e2b["decode_s_per_step"] * 1e3, 3)
+        line["prefill_s_b256_p256"] = round(e2b["prefill_s"], 3)
+        if not args.no_cpu:
+            cpu5 = cpu_baseline_e2b_decode(e2b)
+            line["cpu_decode_s_per_step_b256"] = round(cpu5["s_per_step"], 3)
+            line["decode_speedup_vs_cpu"] = round(cpu5["s_per_step"] / e2b["decode_s_per_step"], 1)
+        del e2b
+    if not args.no_cpu:
+        cpu = cpu_baseline_decode_attention()
+        line["cpu_baseline"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()
+                                if k != "s_per_step"}
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

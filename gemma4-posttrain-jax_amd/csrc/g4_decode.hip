@@ -81,171 +81,9 @@ __device__ __forceinline__ void fused_append(const G4DecodeArgs& a, int pair, co
   }
 }
 
-// ----------------------------------------------------------------------------------------------
-// bf16, MFMA
-// ----------------------------------------------------------------------------------------------
-
-template <int D>
-__global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_kernel(G4DecodeArgs a, int t_alloc) {
-  constexpr int NW = kDecodeWaves;
-  constexpr int KS = D / 32;  // MFMA k-steps over the head dim
-  constexpr int DB = D / 16;  // 16-row blocks of d for the value product
-  extern __shared__ float smem[];
-  const int R = a.group;
-  float* sc = smem;                      // [R][t_alloc] rounded, masked scores
-  float* wmax = smem + R * t_alloc;      // [NW][16]
-  float* wsum = wmax + NW * 16;          // [NW][16]
-  float* red = smem;                     // [NW][R][D] value partials (aliases sc after a barrier)
-
-  const int pair = blockIdx.x;
-  const int b = pair / a.kv_heads;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
-  const int col = lane & 15, grp = lane >> 4;
-  const KeyRange kr = key_range(a, b);
-  fused_append<true, D>(a, pair, kr);
-
-  const uint16_t* qh = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)pair * R * D;
-  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.cache_k) + (int64_t)pair * a.slot_stride * D;
-  const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
-  const uint16_t* newk = kr.new_slot >= 0 ? reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D : nullptr;
-  const uint16_t* newv = kr.new_slot >= 0 ? reinterpret_cast<const uint16_t*>(a.new_v) + (int64_t)pair * D : nullptr;
-
-  bf16x8 qop[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (col < R) v = load16(qh + col * D + 32 * s + 8 * grp);
-    qop[s] = as_bf16x8(v);
-  }
-
-  // ---- phase 1: scores for every scanned slot -------------------------------------------------
-  const int n_chunks = (kr.n_keys + 31) >> 5;
-  float mx = kBf16Min;
-  for (int c = w; c < n_chunks; c += NW) {
-    const int c0 = c << 5;
-    const bool valid = key_valid(a, b, kr, c0 + (lane & 31));
-    const uint64_t vbits = __ballot(valid);
-    floatx4 acc[2];
-#pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
-      const int kslot = c0 + 8 * (col >> 2) + 4 * bb + (col & 3);
-      const uint16_t* kp = (kslot == kr.new_slot) ? newk : kbase + (int64_t)kslot * D;
-      u32x4 kv[KS];
-#pragma unroll
-      for (int s = 0; s < KS; ++s) kv[s] = load16(kp + 32 * s + 8 * grp);
-      floatx4 acc_b = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KS; ++s) acc_b = mfma16x16x32(as_bf16x8(kv[s]), qop[s], acc_b);
-      acc[bb] = acc_b;
-    }
-#pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int kk = 8 * grp + 4 * bb + j;
-        const float s = ((vbits >> kk) & 1ull) ? round_bf16(acc[bb][j]) : kBf16Min;
-        if (col < R) sc[col * t_alloc + c0 + kk] = s;
-        mx = fmaxf(mx, s);
-      }
-    }
-  }
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  if (grp == 0) wmax[w * 16 + col] = mx;
-  __syncthreads();
-  float m = kBf16Min;
-#pragma unroll
-  for (int ww = 0; ww < NW; ++ww) m = fmaxf(m, wmax[ww * 16 + col]);
-  const bool all_masked = wmax[0] == kBf16Min && [&] {
-    for (int ww = 1; ww < NW; ++ww)
-      if (wmax[ww * 16] != kBf16Min) return false;
-    return true;
-  }();
-
-  float l = 0.f;
-  if (col < R) {
-    for (int c = w; c < n_chunks; c += NW) {
-      const float* sp = sc + col * t_alloc + (c << 5) + 8 * grp;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) l += expf(sp[e] - m);
-    }
-  }
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
-  if (grp == 0) wsum[w * 16 + col] = l;
-  __syncthreads();
-  float lsum = 0.f;
-#pragma unroll
-  for (int ww = 0; ww < NW; ++ww) lsum += wsum[ww * 16 + col];
-
-  // ---- phase 2: exact probabilities, value product ---------------------------------------------
-  // A row with no valid key is the reference's softmax over all-equal fills: 1/T on every slot.
-  const int n_keys2 = all_masked ? a.capacity : kr.n_keys;
-  const int n_chunks2 = (n_keys2 + 31) >> 5;
-  const float p_uniform = round_bf16(1.0f / (float)a.capacity);
-  floatx4 oacc[DB];
-#pragma unroll
-  for (int i = 0; i < DB; ++i) oacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int c = w; c < n_chunks2; c += NW) {
-    const int c0 = c << 5;
-    const int kb = c0 + 8 * grp;
-    u32x4 vv[DB];
-#pragma unroll
-    for (int i = 0; i < DB; ++i) vv[i] = load16(vbase + (int64_t)(16 * i + col) * a.slot_stride + kb);
-    uint32_t pw[4];
-#pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) {
-      uint32_t lo = 0, hi = 0;
-      if (col < R) {
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          const int key = kb + 2 * e2 + h2;
-          float p;
-          if (all_masked) {
-            p = key < a.capacity ? p_uniform : 0.f;
-          } else {
-            p = round_bf16(expf(sc[col * t_alloc + key] - m) / lsum);
-          }
-          const uint32_t bits = f32_to_bf16_bits(p);
-          if (h2 == 0) lo = bits; else hi = bits;
-        }
-      }
-      pw[e2] = lo | (hi << 16);
-    }
-    const bf16x8 pop = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
-    const int64_t off = kr.new_slot - kb;
-    if (off >= 0 && off < 8) {
-#pragma unroll
-      for (int i = 0; i < DB; ++i) {
-        const uint32_t nvb = newv[16 * i + col];
-        uint32_t word = vv[i][off >> 1];
-        word = (off & 1) ? ((word & 0x0000ffffu) | (nvb << 16)) : ((word & 0xffff0000u) | nvb);
-        vv[i][off >> 1] = word;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < DB; ++i) oacc[i] = mfma16x16x32(as_bf16x8(vv[i]), pop, oacc[i]);
-  }
-
-  // ---- cross-wave reduction of O^T partials -----------------------------------------------------
-  __syncthreads();  // every wave is done with sc before red (aliasing it) is written
-  if (col < R) {
-#pragma unroll
-    for (int i = 0; i < DB; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) red[(w * R + col) * D + 16 * i + 4 * grp + j] = oacc[i][j];
-    }
-  }
-  __syncthreads();
-  uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + (int64_t)pair * R * D;
-  for (int idx = tid; idx < R * D; idx += NW * 64) {
-    float o = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < NW; ++ww) o += red[ww * R * D + idx];
-    out[idx] = (uint16_t)f32_to_bf16_bits(o);
-  }
-}
+#include "g4_decode_bf16.h"
+#include "g4_decode_dsplit.h"
+#include "g4_decode_stream.h"
 
 // ----------------------------------------------------------------------------------------------
 // f32, VALU
@@ -309,13 +147,38 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(G4DecodeArgs a, int t_a
   }
 }
 
-size_t lds_bytes_bf16(const G4DecodeArgs& a, int t_alloc) {
-  const size_t scores = (size_t)a.group * t_alloc * 4 + 2 * kDecodeWaves * 16 * 4;
-  const size_t red = (size_t)kDecodeWaves * a.group * a.head_dim * 4;
+// LDS: scores f32 | wave max/sum | q bf16 | new K, V rows bf16 | probabilities bf16, and for the
+// key-split kernel (head dims below 128) the O partials [NW][R][D] f32 aliasing from 0.
+size_t lds_bytes_bf16(const G4DecodeArgs& a, int t_alloc, bool with_partials) {
+  const size_t scores = (size_t)a.group * t_alloc * 4 + 2 * kDecodeWaves * 16 * 4 + (size_t)a.group * a.head_dim * 2 +
+                        (size_t)2 * a.head_dim * 2 + (size_t)a.group * t_alloc * 2;
+  const size_t red = with_partials ? (size_t)kDecodeWaves * a.group * a.head_dim * 4 : 0;
   return scores > red ? scores : red;
 }
 
 constexpr size_t kMaxLds = 64 * 1024;
+constexpr size_t kMaxLdsStream = 160 * 1024;  // gfx950: 160 KiB of LDS per workgroup
+
+// The stream kernel's LDS: the two-phase regions, 1 KiB alignment, and the staged V tiles.
+size_t lds_bytes_stream(const G4DecodeArgs& a, int t_alloc) {
+  const int dpw = a.head_dim / 16 / kDecodeWaves;
+  return lds_bytes_bf16(a, t_alloc, false) + 1024 + (size_t)kDecodeWaves * 8 * dpw * 1024;
+}
+
+template <int D>
+int launch_stream(const G4DecodeArgs& a, int t_alloc, hipStream_t st) {
+  const size_t lds = lds_bytes_stream(a, t_alloc);
+  static bool attr_set = false;  // raise the dynamic-LDS limit once per instantiation
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)decode_bf16_stream_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)kMaxLdsStream) != hipSuccess)
+      return fail(G4_ERR_LAUNCH, "g4_decode_attention: cannot raise the LDS limit");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(decode_bf16_stream_kernel<D>, dim3((unsigned)((int64_t)a.batch * a.kv_heads)),
+                     dim3(kDecodeWaves * 64), lds, st, a, t_alloc);
+  return G4_OK;
+}
 
 }  // namespace
 }  // namespace g4
@@ -352,7 +215,16 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
   const int t_alloc = (a.capacity + 31) / 32 * 32;
   const dim3 grid((unsigned)((int64_t)a.batch * a.kv_heads));
   if (a.dtype == G4_DTYPE_BF16) {
-    const size_t lds = lds_bytes_bf16(a, t_alloc);
+    // rows of <= 16 chunks, head dims 128/256: everything requested up front (stream kernel)
+    if ((a.head_dim == 128 || a.head_dim == 256) && a.capacity <= 16 * 32 &&
+        lds_bytes_stream(a, t_alloc) <= kMaxLdsStream) {
+      const int rc = a.head_dim == 256 ? launch_stream<256>(a, t_alloc, st) : launch_stream<128>(a, t_alloc, st);
+      if (rc != G4_OK) return rc;
+      return check_launch("g4_decode_attention");
+    }
+    // head dims >= 128: key-split scores + head-dim-split values; smaller (test) dims: key split
+    const bool dsplit = a.head_dim >= 128;
+    const size_t lds = lds_bytes_bf16(a, t_alloc, !dsplit);
     if (lds > kMaxLds)
       return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: capacity %d x group %d needs %zu B of LDS (> %zu)",
                   a.capacity, a.group, lds, kMaxLds);
@@ -360,8 +232,8 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
     switch (a.head_dim) {
       case 32: hipLaunchKernelGGL(decode_bf16_kernel<32>, grid, block, lds, st, a, t_alloc); break;
       case 64: hipLaunchKernelGGL(decode_bf16_kernel<64>, grid, block, lds, st, a, t_alloc); break;
-      case 128: hipLaunchKernelGGL(decode_bf16_kernel<128>, grid, block, lds, st, a, t_alloc); break;
-      case 256: hipLaunchKernelGGL(decode_bf16_kernel<256>, grid, block, lds, st, a, t_alloc); break;
+      case 128: hipLaunchKernelGGL(decode_bf16_dsplit_kernel<128>, grid, block, lds, st, a, t_alloc); break;
+      case 256: hipLaunchKernelGGL(decode_bf16_dsplit_kernel<256>, grid, block, lds, st, a, t_alloc); break;
       default: return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: bf16 head_dim %d", a.head_dim);
     }
   } else {

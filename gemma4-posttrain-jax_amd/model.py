@@ -238,13 +238,16 @@ def forward_gemma4_text(
     attention_mask: torch.Tensor | None = None,
     kv_cache: KVCache | None = None,
     cache_mode: Literal["prefill", "append"] = "prefill",
+    layer_outputs: list | None = None,
     lora=None,
 ) -> tuple[torch.Tensor, KVCache | None]:
     """model.py:571-673: hidden after the final norm and the updated cache.
 
     Without a cache the forward runs in prefill form over a scratch cache (the reference's
-    cache-less path computes the same attention). ``lora`` must be None: the rollout path runs
-    without adapters (the reference applies LoRA inside the projections, lora.py:107-113)."""
+    cache-less path computes the same attention). ``layer_outputs`` collects every decoder
+    layer's output (the reference's parity hook, model.py:580). ``lora`` must be None: the
+    rollout path runs without adapters (the reference applies LoRA inside the projections,
+    lora.py:107-113)."""
 
     if lora is not None:
         raise NotImplementedError("LoRA adapters are not supported by the native rollout path")
@@ -339,6 +342,8 @@ def forward_gemma4_text(
             g = rms_norm(g, lp.per_layer_input.post_norm.weight, eps)
             x = x + g
         x = (x.float() * lp.layer_scalar.float()).to(x.dtype)
+        if layer_outputs is not None:
+            layer_outputs.append(x)
     hidden = rms_norm(x, params.final_norm.weight, eps)
     if scratch_cache:
         return hidden, None

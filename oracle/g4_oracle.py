@@ -456,6 +456,20 @@ def init_kv_cache(cfg: Config, batch: int, capacity: int, dtype: str) -> KVCache
     return KVCache(tuple(layers), np.zeros((batch, capacity), bool), 0)
 
 
+_INPLACE = [False]
+
+
+class inplace_cache_updates:
+    """Context manager: cache appends write into the existing arrays instead of copying them
+    (what XLA does inside the reference's while_loop); used when the oracle is timed."""
+
+    def __enter__(self):
+        _INPLACE.append(True)
+
+    def __exit__(self, *exc):
+        _INPLACE.pop()
+
+
 def append_slots(start: int, num_new: int, capacity: int, circular: bool) -> tuple[np.ndarray, np.ndarray]:
     """Destination slots and source rows of one ``_update_layer_cache`` call (model.py:368-390).
     Linear: rows ``0..S-1`` -> slots ``start..start+S-1``. Ring: the last ``keep = min(S, Wc)`` rows
@@ -474,7 +488,10 @@ def update_layer_cache(layer: LayerKV, k: np.ndarray, v: np.ndarray, start, circ
 
     k = cast(k, dtype)
     v = cast(v, dtype)
-    ck, cv = layer.key.copy(), layer.value.copy()
+    if _INPLACE[-1]:
+        ck, cv = layer.key, layer.value
+    else:
+        ck, cv = layer.key.copy(), layer.value.copy()
     C = ck.shape[1]
     starts = np.broadcast_to(np.asarray(start, dtype=np.int64), (ck.shape[0],))
     S = k.shape[1]

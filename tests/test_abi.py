@@ -1,0 +1,140 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol include/g4_rollout.h declares,
+its host-side functions match the oracle, and invalid arguments are rejected with an error
+code and message before any launch (no GPU needed: validation precedes every HIP call)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import hf_util as H
+from oracle import g4_oracle as O
+
+from gemma4_posttrain_jax_amd import _lib
+from gemma4_posttrain_jax_amd import config as C
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "g4_rollout.h"
+
+
+def declared_functions() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(g4_\w+)\s*\(", text))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = declared_functions()
+    assert names == set(_lib.PROTOTYPES), "ctypes prototypes and header declarations differ"
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.g4_version().startswith(b"g4rollout")
+
+
+def test_ctypes_structs_match_the_compiled_header(tmp_path):
+    """Size and every field offset of the ctypes mirrors equal what a C compiler lays out."""
+
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for st in (_lib.G4AppendArgs, _lib.G4DecodeArgs, _lib.G4PrefillArgs):
+        lines.append(f'printf("{st.__name__} size %zu\\n", sizeof({st.__name__}));')
+        for f, _ in st._fields_:
+            lines.append(f'printf("{st.__name__} {f} %zu\\n", offsetof({st.__name__}, {f}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([cc, str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    for line in filter(None, out):
+        name, field, value = line.split()
+        st = getattr(_lib, name)
+        got = ctypes.sizeof(st) if field == "size" else getattr(st, field).offset
+        assert got == int(value), f"{name}.{field}: ctypes {got} != C {value}"
+
+
+@pytest.mark.parametrize("name", ["TINY_A", "TINY_B", "CFG1"])
+def test_native_kv_source_layers_match_oracle(name):
+    kw = getattr(H, name)
+    ocfg, cfg = O.config_from_hf(kw), C.config_from_hf(kw)
+    assert C.kv_source_layers(cfg) == [O.kv_source_layer(ocfg, i) for i in range(ocfg.num_hidden_layers)]
+
+
+def test_native_kv_source_layers_e2b_like():
+    types = [0, 0, 0, 0, 1] * 6
+    got = _lib.kv_source_layers(types, 10)
+    assert got[:20] == list(range(20))
+    assert got[20:] == [18, 18, 18, 18, 19, 18, 18, 18, 18, 19]
+
+
+def test_native_kv_source_layers_rejects_missing_source():
+    with pytest.raises(_lib.G4Error, match="no non-shared layer"):
+        _lib.kv_source_layers([1, 0, 0], 2)
+
+
+@pytest.mark.parametrize("wc", [1, 7, 16, 512])
+def test_native_ring_slot_positions_match_oracle(wc):
+    for last in [-3, 0, 5, wc - 1, wc, 3 * wc + 1, 2047]:
+        np.testing.assert_array_equal(_lib.ring_slot_positions(last, wc), O.ring_slot_positions(last, wc))
+
+
+def _decode_args(**kw):
+    base = dict(dtype=_lib.G4_DTYPE_BF16, kind=_lib.G4_CACHE_RING, batch=2, kv_heads=2, group=4, head_dim=256,
+                capacity=512, slot_stride=512, window=512, q_pos_scalar=0, q_pos=None, key_mask=1,
+                key_mask_stride=2048, q=1, cache_k=1, cache_vt=1, cache_k_w=1, new_k=None, new_v=None, out=1,
+                workspace=None, workspace_bytes=0, num_splits=0)
+    base.update(kw)
+    return _lib.G4DecodeArgs(**base)
+
+
+@pytest.mark.parametrize("override,match", [
+    (dict(dtype=7), "dtype"),
+    (dict(kind=5), "kind"),
+    (dict(group=17), "group"),
+    (dict(head_dim=96), "head_dim"),
+    (dict(slot_stride=500), "slot_stride"),
+    (dict(window=0), "window"),
+    (dict(q=None), "NULL"),
+    (dict(new_k=1), "together"),
+    (dict(kind=_lib.G4_CACHE_LINEAR, key_mask_stride=100), "key_mask_stride"),
+    (dict(capacity=8192, slot_stride=8192, kind=_lib.G4_CACHE_LINEAR, key_mask_stride=8192, group=8), "LDS"),
+])
+def test_decode_rejects_invalid_arguments(override, match):
+    a = _decode_args(**override)
+    rc = _lib.lib().g4_decode_attention(ctypes.byref(a), None)
+    assert rc in (-1, -2)
+    assert re.search(match, _lib.lib().g4_last_error().decode())
+
+
+def test_append_and_prefill_reject_invalid_arguments():
+    L = _lib.lib()
+    a = _lib.G4AppendArgs(dtype=_lib.G4_DTYPE_BF16, kind=_lib.G4_CACHE_LINEAR, batch=1, seq=10, kv_heads=1, group=0,
+                          head_dim=64, capacity=8, slot_stride=64, k=1, v=1, cache_k=1, cache_vt=1, in_row_stride=64)
+    assert L.g4_kv_append(ctypes.byref(a), None) == -1
+    assert b"do not fit" in L.g4_last_error()
+    a.seq, a.flags = 1, _lib.G4_APPEND_ROPE_K
+    assert L.g4_kv_append(ctypes.byref(a), None) == -1
+    assert b"RoPE" in L.g4_last_error()
+    assert L.g4_kv_append(None, None) == -1
+    p = _lib.G4PrefillArgs(dtype=_lib.G4_DTYPE_BF16, batch=1, seq=100, kv_heads=1, group=4, head_dim=64, window=0,
+                           key_mask=1, key_mask_stride=100, q=1, k=1, vt=1, k_stride=100, out=1)
+    assert L.g4_prefill_attention(ctypes.byref(p), None) == -1
+    assert b"k_stride" in L.g4_last_error()
+    p.k_stride, p.group = 128, 3
+    assert L.g4_prefill_attention(ctypes.byref(p), None) == -2
+    assert b"group" in L.g4_last_error()
+
+
+def test_python_wrappers_fail_loudly_without_the_library(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "missing.so")
+    with pytest.raises(_lib.G4Error, match="missing"):
+        _lib.lib()

@@ -91,7 +91,10 @@ def test_bf16_prefill_and_decode_calls_match_oracle(device, seed):
     writes must match the oracle's to the same bar."""
 
     ocfg = O.config_from_hf(SMALL_BF16)
-    oparams = O.init_params(ocfg, seed=seed, dtype=O.BF16, std=0.05, norm_std=0.2, layer_scalar_min=0.5)
+    # the reference's well-conditioned recipe (grad_tiny, tests/conftest.py:112-125): random bf16
+    # models with larger norm spreads are chaotic, so a last-bit GEMM difference in layer 0 grows
+    # by 2-4x per layer for any two implementations, the oracle against itself included
+    oparams = O.init_params(ocfg, seed=seed, dtype=O.BF16, std=0.03, norm_std=0.05, layer_scalar_min=0.8)
     cfg = C.config_from_hf(SMALL_BF16)
     params = M.params_from_numpy(oparams, cfg, dtype=torch.bfloat16, device=device)
     rng = np.random.default_rng(7 + seed)
