@@ -57,7 +57,7 @@ def cpu_info() -> str:
     return platform.processor() or "unknown"
 
 
-def bench_decode_attention(steps: int, warmup: int) -> dict:
+def bench_decode_attention(steps: int, warmup: int, num_splits: int = 0) -> dict:
     import torch
 
     import __graft_entry__
@@ -92,7 +92,7 @@ def bench_decode_attention(steps: int, warmup: int) -> dict:
 
     def step(i):
         kernels.decode_attention(layers[i % NCACHE], q[i], key_mask, q_pos=q_pos[i], window=W, out=out[i],
-                                 new_k=nk[i], new_v=nv[i])
+                                 new_k=nk[i], new_v=nv[i], num_splits=num_splits)
 
     # eager warmup (also compiles nothing: the library is prebuilt)
     for i in range(min(total, 3)):
@@ -298,13 +298,15 @@ def main() -> int:
     ap.add_argument("--e2b-steps", type=int, default=8)
     ap.add_argument("--no-e2b", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--num-splits", type=int, default=0,
+                    help="workgroups per (b, kv head) for decode attention (0: library default)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every box here has one GPU)",
               file=sys.stderr)
         return 2
 
-    res = bench_decode_attention(args.steps, args.warmup)
+    res = bench_decode_attention(args.steps, args.warmup, args.num_splits)
     bytes_step = algorithmic_bytes_per_step()
     gbs = bytes_step / (res["ms_per_step"] * 1e-3) / 1e9
     line = {
@@ -322,7 +324,7 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "configs[1]: sliding-window decode attention, 1-token append + attend per step",
                    "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "window": W, "ring_context": CTX,
-                   "bytes_per_step": bytes_step, "caches_round_robin": NCACHE},
+                   "bytes_per_step": bytes_step, "caches_round_robin": NCACHE, "num_splits": args.num_splits},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),

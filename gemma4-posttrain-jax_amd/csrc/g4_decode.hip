@@ -82,8 +82,7 @@ __device__ __forceinline__ void fused_append(const G4DecodeArgs& a, int pair, co
 }
 
 #include "g4_decode_bf16.h"
-#include "g4_decode_dsplit.h"
-#include "g4_decode_stream.h"
+#include "g4_decode_fast.h"
 
 // ----------------------------------------------------------------------------------------------
 // f32, VALU
@@ -156,27 +155,22 @@ size_t lds_bytes_bf16(const G4DecodeArgs& a, int t_alloc, bool with_partials) {
   return scores > red ? scores : red;
 }
 
-constexpr size_t kMaxLds = 64 * 1024;
-constexpr size_t kMaxLdsStream = 160 * 1024;  // gfx950: 160 KiB of LDS per workgroup
+constexpr size_t kMaxLds = 64 * 1024;       // default dynamic-LDS limit
+constexpr size_t kMaxLdsFast = 160 * 1024;  // gfx950: 160 KiB of LDS per workgroup
 
-// The stream kernel's LDS: the two-phase regions, 1 KiB alignment, and the staged V tiles.
-size_t lds_bytes_stream(const G4DecodeArgs& a, int t_alloc) {
-  const int dpw = a.head_dim / 16 / kDecodeWaves;
-  return lds_bytes_bf16(a, t_alloc, false) + 1024 + (size_t)kDecodeWaves * 8 * dpw * 1024;
-}
-
-template <int D>
-int launch_stream(const G4DecodeArgs& a, int t_alloc, hipStream_t st) {
-  const size_t lds = lds_bytes_stream(a, t_alloc);
+template <int D, int NSPLIT, bool LONG>
+int launch_fast(const G4DecodeArgs& a, int t_alloc, size_t lds, hipStream_t st) {
   static bool attr_set = false;  // raise the dynamic-LDS limit once per instantiation
   if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)decode_bf16_stream_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)kMaxLdsStream) != hipSuccess)
+    if (hipFuncSetAttribute((const void*)decode_bf16_fast_kernel<D, NSPLIT, LONG>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLdsFast) != hipSuccess)
       return fail(G4_ERR_LAUNCH, "g4_decode_attention: cannot raise the LDS limit");
     attr_set = true;
   }
-  hipLaunchKernelGGL(decode_bf16_stream_kernel<D>, dim3((unsigned)((int64_t)a.batch * a.kv_heads)),
-                     dim3(kDecodeWaves * 64), lds, st, a, t_alloc);
+  const int64_t npairs = (int64_t)a.batch * a.kv_heads;
+  const int64_t blocks = NSPLIT == 1 ? npairs : (npairs + 7) / 8 * 8 * NSPLIT;
+  hipLaunchKernelGGL((decode_bf16_fast_kernel<D, NSPLIT, LONG>), dim3((unsigned)blocks), dim3(kDecodeWaves * 64), lds, st,
+                     a, t_alloc);
   return G4_OK;
 }
 
@@ -215,16 +209,30 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
   const int t_alloc = (a.capacity + 31) / 32 * 32;
   const dim3 grid((unsigned)((int64_t)a.batch * a.kv_heads));
   if (a.dtype == G4_DTYPE_BF16) {
-    // rows of <= 16 chunks, head dims 128/256: everything requested up front (stream kernel)
-    if ((a.head_dim == 128 || a.head_dim == 256) && a.capacity <= 16 * 32 &&
-        lds_bytes_stream(a, t_alloc) <= kMaxLdsStream) {
-      const int rc = a.head_dim == 256 ? launch_stream<256>(a, t_alloc, st) : launch_stream<128>(a, t_alloc, st);
+    if (a.head_dim == 128 || a.head_dim == 256) {
+      // num_splits: workgroups per (b, kv head), each owning a slice of the value dims
+      // (0 = automatic: 2 for head dim 256, else 1)
+      const int splits = a.num_splits == 0 ? (a.head_dim == 256 ? 2 : 1) : a.num_splits;
+      if (splits != 1 && !(splits == 2 && a.head_dim == 256))
+        return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: num_splits %d with head_dim %d", a.num_splits,
+                    a.head_dim);
+      const size_t lds = fast_lds_bytes(a.group, a.head_dim, t_alloc);
+      if (lds > kMaxLdsFast)
+        return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: capacity %d x group %d needs %zu B of LDS (> %zu)",
+                    a.capacity, a.group, lds, kMaxLdsFast);
+      const bool long_rows = t_alloc > 2 * kDecodeWaves * 32;
+      int rc;
+      if (a.head_dim == 128)
+        rc = long_rows ? launch_fast<128, 1, true>(a, t_alloc, lds, st) : launch_fast<128, 1, false>(a, t_alloc, lds, st);
+      else if (splits == 2)
+        rc = long_rows ? launch_fast<256, 2, true>(a, t_alloc, lds, st) : launch_fast<256, 2, false>(a, t_alloc, lds, st);
+      else
+        rc = long_rows ? launch_fast<256, 1, true>(a, t_alloc, lds, st) : launch_fast<256, 1, false>(a, t_alloc, lds, st);
       if (rc != G4_OK) return rc;
       return check_launch("g4_decode_attention");
     }
-    // head dims >= 128: key-split scores + head-dim-split values; smaller (test) dims: key split
-    const bool dsplit = a.head_dim >= 128;
-    const size_t lds = lds_bytes_bf16(a, t_alloc, !dsplit);
+    // smaller (test) head dims: key-split kernel with a cross-wave reduction of O
+    const size_t lds = lds_bytes_bf16(a, t_alloc, true);
     if (lds > kMaxLds)
       return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: capacity %d x group %d needs %zu B of LDS (> %zu)",
                   a.capacity, a.group, lds, kMaxLds);
@@ -232,8 +240,6 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
     switch (a.head_dim) {
       case 32: hipLaunchKernelGGL(decode_bf16_kernel<32>, grid, block, lds, st, a, t_alloc); break;
       case 64: hipLaunchKernelGGL(decode_bf16_kernel<64>, grid, block, lds, st, a, t_alloc); break;
-      case 128: hipLaunchKernelGGL(decode_bf16_dsplit_kernel<128>, grid, block, lds, st, a, t_alloc); break;
-      case 256: hipLaunchKernelGGL(decode_bf16_dsplit_kernel<256>, grid, block, lds, st, a, t_alloc); break;
       default: return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: bf16 head_dim %d", a.head_dim);
     }
   } else {

@@ -156,9 +156,11 @@ def decode_attention(
     out: torch.Tensor | None = None,
     new_k: torch.Tensor | None = None,
     new_v: torch.Tensor | None = None,
+    num_splits: int = 0,
 ) -> torch.Tensor:
     """g4_decode_attention: q ``[B, Hkv, R, D]`` against ``layer``; returns ``[B, Hkv, R, D]``.
-    With ``new_k``/``new_v`` (``[B, Hkv, D]``) the token's K/V is stored at ``q_pos`` first."""
+    With ``new_k``/``new_v`` (``[B, Hkv, D]``) the token's K/V is stored at ``q_pos`` first.
+    ``num_splits``: workgroups per (b, kv head); 0 lets the library choose."""
 
     B, H, R, D = q.shape
     if not q.is_contiguous() or q.dtype != layer.key.dtype:
@@ -185,7 +187,8 @@ def decode_attention(
         group=R, head_dim=D, capacity=layer.capacity, slot_stride=layer.slot_stride, window=window,
         q_pos_scalar=qp_scalar, q_pos=qp_ptr, key_mask=_ptr(key_mask), key_mask_stride=key_mask.stride(0),
         q=_ptr(q), cache_k=_ptr(layer.key), cache_vt=_ptr(layer.value_t), cache_k_w=_ptr(layer.key),
-        new_k=_ptr(new_k), new_v=_ptr(new_v), out=_ptr(out), workspace=None, workspace_bytes=0, num_splits=0,
+        new_k=_ptr(new_k), new_v=_ptr(new_v), out=_ptr(out), workspace=None, workspace_bytes=0,
+        num_splits=num_splits,
     )
     _lib.check(_lib.lib().g4_decode_attention(ctypes.byref(a), _stream()), "g4_decode_attention")
     return out

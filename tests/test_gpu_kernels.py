@@ -123,7 +123,7 @@ def test_append_with_norms_and_q_matches_oracle(device, dtype):
 # --- decode attention -----------------------------------------------------------------------------
 
 
-def _decode_case(device, dtype, *, B, H, R, D, cap, ring, window, q_pos, key_mask, fused, seed):
+def _decode_case(device, dtype, *, B, H, R, D, cap, ring, window, q_pos, key_mask, fused, seed, num_splits=0):
     rng = np.random.default_rng(seed)
     td = __import__("gpu_util").TORCH_DTYPE[dtype]
     layer = new_layer_cache(B, H, D, cap, ring, td, device)
@@ -135,10 +135,12 @@ def _decode_case(device, dtype, *, B, H, R, D, cap, ring, window, q_pos, key_mas
     km = torch.from_numpy(key_mask).to(device)
     if fused:
         out = kernels.decode_attention(layer, to_dev(q, dtype, device), km, q_pos=qp, window=window,
-                                       new_k=to_dev(nk, dtype, device), new_v=to_dev(nv, dtype, device))
+                                       new_k=to_dev(nk, dtype, device), new_v=to_dev(nv, dtype, device),
+                                       num_splits=num_splits)
         ref_kv = O.update_layer_cache(O.LayerKV(k0, v0), nk[:, None], nv[:, None], q_pos, ring, dtype)
     else:
-        out = kernels.decode_attention(layer, to_dev(q, dtype, device), km, q_pos=qp, window=window)
+        out = kernels.decode_attention(layer, to_dev(q, dtype, device), km, q_pos=qp, window=window,
+                                       num_splits=num_splits)
         ref_kv = O.LayerKV(k0, v0)
     masks = O.make_cached_qk_masks(key_mask, window if ring else 1 << 30, q_pos, 1)
     mask = masks[O.SLIDING] if ring else masks[O.FULL]
@@ -154,17 +156,34 @@ def _decode_case(device, dtype, *, B, H, R, D, cap, ring, window, q_pos, key_mas
     return err
 
 
-@pytest.mark.parametrize("fused", [False, True])
-def test_decode_ring_config2_shape(device, fused):
+@pytest.mark.parametrize("fused,num_splits", [(False, 0), (True, 0), (True, 1), (True, 2)])
+def test_decode_ring_config2_shape(device, fused, num_splits):
     """BASELINE config 2: B64, Hq8/Hkv2, D256, W512 ring that has wrapped several times;
-    per-row write positions U[1536, 2048)."""
+    per-row write positions U[1536, 2048). num_splits 1/2: one or two workgroups per (b, kv head)."""
 
     rng = np.random.default_rng(2)
     B, H, R, D, W = 64, 2, 4, 256, 512
     q_pos = rng.integers(1536, 2048, B)
     key_mask = np.ones((B, 2048), bool)
     _decode_case(device, O.BF16, B=B, H=H, R=R, D=D, cap=W, ring=True, window=W, q_pos=q_pos, key_mask=key_mask,
-                 fused=fused, seed=20)
+                 fused=fused, seed=20, num_splits=num_splits)
+
+
+@pytest.mark.parametrize("D,num_splits", [(128, 1), (256, 1), (256, 2)])
+def test_decode_linear_long_rows(device, D, num_splits):
+    """Rows longer than one round of chunks (capacity 768, the E2B global-layer cache): the
+    appended slot falls in the first round for some rows and in later rounds for others;
+    batch*heads not a multiple of 8 (padding workgroups of the two-split grid); a fully masked
+    row; rows shorter than one round."""
+
+    rng = np.random.default_rng(7)
+    B, H, R, C = 5, 3, 4, 768
+    q_pos = np.array([767, 600, 100, 20, 700])
+    key_mask = np.ones((B, C), bool)
+    key_mask[1, :40] = False
+    key_mask[4, :] = False
+    _decode_case(device, O.BF16, B=B, H=H, R=R, D=D, cap=C, ring=False, window=0, q_pos=q_pos, key_mask=key_mask,
+                 fused=True, seed=23, num_splits=num_splits)
 
 
 @pytest.mark.parametrize("dtype,D", [(O.BF16, 64), (O.BF16, 256), (O.F32, 64)])
