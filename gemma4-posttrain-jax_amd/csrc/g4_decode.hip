@@ -83,6 +83,7 @@ __device__ __forceinline__ void fused_append(const G4DecodeArgs& a, int pair, co
 
 #include "g4_decode_bf16.h"
 #include "g4_decode_fast.h"
+#include "g4_decode_stage.h"
 
 // ----------------------------------------------------------------------------------------------
 // f32, VALU
@@ -158,6 +159,26 @@ size_t lds_bytes_bf16(const G4DecodeArgs& a, int t_alloc, bool with_partials) {
 constexpr size_t kMaxLds = 64 * 1024;       // default dynamic-LDS limit
 constexpr size_t kMaxLdsFast = 160 * 1024;  // gfx950: 160 KiB of LDS per workgroup
 
+// Dynamic LDS of the staged kernel: scores/probabilities bf16 [R][512 + 32] | wave maxima [NW][16] |
+// block sums [R][2] (the V^T tiles and the new K row are static).
+size_t stage_lds_bytes(int R) { return (size_t)R * kStageStride * 2 + (size_t)kDecodeWaves * 16 * 4 + (size_t)R * 2 * 4; }
+
+template <int D, int NSPLIT>
+int launch_stage(const G4DecodeArgs& a, hipStream_t st) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)decode_bf16_stage_kernel<D, NSPLIT>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)stage_lds_bytes(16)) != hipSuccess)
+      return fail(G4_ERR_LAUNCH, "g4_decode_attention: cannot raise the LDS limit");
+    attr_set = true;
+  }
+  const int64_t npairs = (int64_t)a.batch * a.kv_heads;
+  const int64_t blocks = NSPLIT == 1 ? npairs : (npairs + 7) / 8 * 8 * NSPLIT;
+  hipLaunchKernelGGL((decode_bf16_stage_kernel<D, NSPLIT>), dim3((unsigned)blocks), dim3(kDecodeWaves * 64),
+                     stage_lds_bytes(a.group), st, a);
+  return G4_OK;
+}
+
 template <int D, int NSPLIT, bool LONG>
 int launch_fast(const G4DecodeArgs& a, int t_alloc, size_t lds, hipStream_t st) {
   static bool attr_set = false;  // raise the dynamic-LDS limit once per instantiation
@@ -222,6 +243,11 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
                     a.capacity, a.group, lds, kMaxLdsFast);
       const bool long_rows = t_alloc > 2 * kDecodeWaves * 32;
       int rc;
+      if (!long_rows && splits == a.head_dim / 128) {  // V^T slice of 128 dims x 512 slots staged in LDS
+        rc = a.head_dim == 128 ? launch_stage<128, 1>(a, st) : launch_stage<256, 2>(a, st);
+        if (rc != G4_OK) return rc;
+        return check_launch("g4_decode_attention");
+      }
       if (a.head_dim == 128)
         rc = long_rows ? launch_fast<128, 1, true>(a, t_alloc, lds, st) : launch_fast<128, 1, false>(a, t_alloc, lds, st);
       else if (splits == 2)

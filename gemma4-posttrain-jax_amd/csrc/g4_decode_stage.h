@@ -1,0 +1,230 @@
+// bf16 decode attention for rows of at most 512 slots (the sliding-window ring) with
+// D / NSPLIT = 128 value dims per workgroup; included by g4_decode.hip after g4_decode_fast.h.
+//
+// Everything a workgroup reads is requested in its first instructions: q (straight into MFMA
+// operand registers), the key-mask bytes, two 32-slot K chunks per wave (registers) and the
+// workgroup's whole V^T slice, DMA'd into LDS (buffer_load ... lds, 128 KiB): wave w stages the
+// tiles of its own 16-row d-block for every chunk, each tile lane-ordered so that it is read
+// back as that lane's MFMA operand. A wave scores once its requests are queued (its K, queued
+// first, has landed by then); the softmax barriers wait only for LDS traffic (a __syncthreads()
+// fence would also wait for the DMA, which writes LDS), and a wave waits for its own DMA right
+// before its value MFMAs.
+//
+// The appended token: the wave that scores the chunk holding the slot stages the new K row in
+// LDS for itself (no barrier) and substitutes it into that chunk's K operand registers; every
+// wave writes the new V value into its own staged tile once its DMA has landed. The cache
+// itself is written last (after every load of the workgroup).
+//
+// The softmax runs on all 512 threads: thread t owns 4 consecutive (head, slot) entries of the
+// [R][512] score array, so no lanes sit idle behind the R <= 16 MFMA columns.
+
+constexpr int kStageSlots = 2 * NW * 32;  // slots per row handled here (16 chunks)
+// LDS row stride of the score/probability array: 64 bytes of padding put the rows of heads
+// 0..3 on different banks for the 16-byte MFMA-operand accesses (lane (grp, col) -> row col).
+constexpr int kStageStride = kStageSlots + 32;
+
+__device__ __forceinline__ void wg_barrier() {
+  // LDS writes of this wave complete, then the workgroup barrier; no wait for vector memory
+  __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+template <int D, int NSPLIT>
+__global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_stage_kernel(G4DecodeArgs a) {
+  static_assert(D / NSPLIT == 16 * NW, "one 16-row d-block of V^T per wave");
+  __shared__ __attribute__((aligned(1024))) unsigned char vt_tiles[NW][2 * NW][1024];  // [wave][chunk][lane*16]
+  __shared__ __attribute__((aligned(16))) uint16_t nk_lds[D];
+  extern __shared__ float smem[];
+  const int R = a.group;
+  uint16_t* sp = reinterpret_cast<uint16_t*>(smem);                // [R][stride] scores, then probabilities
+  float* wmax = reinterpret_cast<float*>(sp + R * kStageStride);  // [NW][16] wave maxima
+  float* bsum = wmax + NW * 16;                                   // [R][2] sums of 256-slot blocks
+
+  const int npairs = a.batch * a.kv_heads;
+  int pair, h;
+  if (NSPLIT == 1) {
+    pair = blockIdx.x;
+    h = 0;
+  } else {  // the two workgroups of a pair share blockIdx.x mod 8, i.e. one XCD
+    pair = (int)(blockIdx.x >> 4) * 8 + (int)(blockIdx.x & 7);
+    h = (int)(blockIdx.x >> 3) & 1;
+  }
+  if (pair >= npairs) return;  // padding workgroups of the NSPLIT = 2 grid (whole workgroup)
+  const int b = pair / a.kv_heads;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const int db = h * NW + w;  // this wave's d-block: value dims [16*db, 16*db + 16)
+  const KeyRange kr = key_range(a, b);
+  const int64_t ss = a.slot_stride;
+  const uint32_t pair_bytes = (uint32_t)a.slot_stride * D * 2u;
+  const __amdgpu_buffer_rsrc_t rk =
+      make_rsrc(reinterpret_cast<const uint16_t*>(a.cache_k) + (int64_t)pair * a.slot_stride * D, pair_bytes);
+  const __amdgpu_buffer_rsrc_t rv =
+      make_rsrc(reinterpret_cast<const uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride, pair_bytes);
+  const int n_chunks = (kr.n_keys + 31) >> 5;  // <= 2*NW: capacity <= 512 is checked on the host
+  const bool has_new = kr.new_slot >= 0;
+  const bool owner = has_new && (int)((kr.new_slot >> 5) & (NW - 1)) == w;  // scores the appended slot's chunk
+
+  // ---- requests: small rows, q operands, mask bytes, K, then the V^T slice into LDS -------------
+  u32x4 nkv = {0u, 0u, 0u, 0u};
+  if (owner && lane < D / 8) nkv = load16(reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D + 8 * lane);
+  uint32_t nvb = 0;  // new V value of this lane's d row (16*db + col)
+  if (has_new) nvb = reinterpret_cast<const uint16_t*>(a.new_v)[(int64_t)pair * D + 16 * db + col];
+  bf16x8 qop[D / 32];
+  {
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)pair * R + (col < R ? col : 0)) * D;
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (col < R) v = load16(qrow + 32 * s + 8 * grp);
+      qop[s] = as_bf16x8(v);
+    }
+  }
+  const int c0 = w << 5, c1 = (w + NW) << 5;
+  uint8_t mb0, mb1;
+  const bool ok0 = slot_valid_flat(a, b, kr, c0 + (lane & 31), mb0);
+  const bool ok1 = slot_valid_flat(a, b, kr, c1 + (lane & 31), mb1);
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 k0[2][D / 32], k1[2][D / 32];
+  load_k_chunk<D>(k0, rk, c0, col, grp);
+  load_k_chunk<D>(k1, rk, c1, col, grp);
+  // Every byte is requested before any compute: a wave stalled on a full memory queue cannot
+  // compute anyway, and its K (requested first) has landed by the time its last DMA is queued.
+  const uint32_t soff = (uint32_t)(16 * db * ss) * 2u;
+  auto dma_v = [&](int c) {
+    if (c < n_chunks) {
+      const uint32_t voff = (uint32_t)(col * ss + (c << 5) + 8 * grp) * 2u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&vt_tiles[w][c][0], 16,
+                                               voff, soff, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int c = 0; c < 2 * NW; ++c) dma_v(c);
+  __builtin_amdgcn_sched_barrier(0);
+  if (owner && lane < D / 8) reinterpret_cast<u32x4*>(nk_lds)[lane] = nkv;  // read back by this wave only
+  const uint64_t vb0 = __ballot(ok0 && mb0 != 0);
+  const uint64_t vb1 = __ballot(ok1 && mb1 != 0);
+
+  // ---- scores (each wave: chunks w and w + NW) --------------------------------------------------
+  float mx = kBf16Min;
+  if (w < n_chunks) {
+    patch_k_sel<D>(k0, nk_lds, kr.new_slot, c0, col, grp);
+    mx = score_to_lds<D>(k0, qop, vb0, sp, kStageStride, c0, R, col, grp, mx);
+  }
+  if (w + NW < n_chunks) {
+    patch_k_sel<D>(k1, nk_lds, kr.new_slot, c1, col, grp);
+    mx = score_to_lds<D>(k1, qop, vb1, sp, kStageStride, c1, R, col, grp, mx);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (grp == 0) wmax[w * 16 + col] = mx;
+  wg_barrier();  // scores and wave maxima are in LDS
+
+  // ---- softmax over all threads: thread t owns entries [4t, 4t + 4) of each 2048-entry slice ----
+  // (entry e = head * 512 + slot; a wave's 256 entries lie in one head)
+  bool all_masked = true;
+#pragma unroll
+  for (int ww = 0; ww < NW; ++ww) all_masked = all_masked && wmax[ww * 16] == kBf16Min;  // per-slot validity
+  const int n_scanned = n_chunks << 5;
+  const int slot = 256 * (w & 1) + 4 * lane;
+  float ev[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // heads 4i + w/2 (R <= 16)
+    const int hh = 4 * i + (w >> 1);
+    if (hh < R && !all_masked) {
+      float m = kBf16Min;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) m = fmaxf(m, wmax[ww * 16 + hh]);
+      const uint2 sv = *reinterpret_cast<const uint2*>(sp + hh * kStageStride + slot);
+      const float s4[4] = {bf16_lo(sv.x), bf16_hi(sv.x), bf16_lo(sv.y), bf16_hi(sv.y)};
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        ev[i][j] = slot + j < n_scanned ? expf(s4[j] - m) : 0.f;
+        part += ev[i][j];
+      }
+      part = wave_sum64(part);
+      if (lane == 0) bsum[2 * hh + (w & 1)] = part;
+    }
+  }
+  wg_barrier();  // block sums are in LDS
+  const float pu = round_bf16(1.0f / (float)a.capacity);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int hh = 4 * i + (w >> 1);
+    if (hh < R) {
+      float p[4];
+      if (all_masked) {  // no valid slot: uniform bf16(1/capacity) over the capacity
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[j] = slot + j < a.capacity ? pu : 0.f;
+      } else {
+        const float l = bsum[2 * hh] + bsum[2 * hh + 1];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[j] = ev[i][j] / l;
+      }
+      const uint2 pw = make_uint2(f32_to_bf16_bits(p[0]) | (f32_to_bf16_bits(p[1]) << 16),
+                                  f32_to_bf16_bits(p[2]) | (f32_to_bf16_bits(p[3]) << 16));
+      *reinterpret_cast<uint2*>(sp + hh * kStageStride + slot) = pw;
+    }
+  }
+  wg_barrier();  // probabilities are in LDS
+
+  // ---- values: this wave's d-block over every chunk ---------------------------------------------
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's V^T tiles have landed
+  if (has_new) {  // the appended slot's value into the staged tile (lanes of the slot's 8-slot group)
+    const int cn = (int)(kr.new_slot >> 5), gn = (int)(kr.new_slot & 31) >> 3, e = (int)(kr.new_slot & 7);
+    if (grp == gn) *reinterpret_cast<uint16_t*>(&vt_tiles[w][cn][16 * lane + 2 * e]) = (uint16_t)nvb;
+  }
+  const int n_chunks2 = all_masked ? (a.capacity + 31) >> 5 : n_chunks;
+  floatx4 oacc = {0.f, 0.f, 0.f, 0.f}, oacc1 = {0.f, 0.f, 0.f, 0.f};  // even / odd chunks
+  {
+    u32x4 vt[2 * NW];  // every operand read before the MFMA chain (LDS latency paid once)
+    bf16x8 pp[2 * NW];
+#pragma unroll
+    for (int c = 0; c < 2 * NW; ++c) {
+      if (c < n_chunks) {
+        vt[c] = *reinterpret_cast<const u32x4*>(&vt_tiles[w][c][16 * lane]);
+        pp[c] = prob_operand(sp, kStageStride, (c << 5) + 8 * grp, R, col);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 2 * NW; c += 2) {
+      if (c < n_chunks) oacc = mfma16x16x32(as_bf16x8(vt[c]), pp[c], oacc);
+      if (c + 1 < n_chunks) oacc1 = mfma16x16x32(as_bf16x8(vt[c + 1]), pp[c + 1], oacc1);
+    }
+  }
+  oacc += oacc1;
+  for (int c = n_chunks; c < n_chunks2; ++c) {  // fully masked linear row: slots never scanned
+    const uint32_t voff = (uint32_t)(col * ss + (c << 5) + 8 * grp) * 2u;
+    const u32x4 v = buffer_load16(rv, voff, (uint32_t)(16 * db * ss) * 2u);
+    oacc = mfma16x16x32(as_bf16x8(v), prob_operand(sp, kStageStride, (c << 5) + 8 * grp, R, col), oacc);
+  }
+
+  // ---- the fused append's cache write (after every cache load of this workgroup) ---------------
+  // Workgroup h writes K row elements [h*D/NSPLIT, (h+1)*D/NSPLIT) and its own V^T rows. The
+  // other workgroup of the pair may still read that K row; it substitutes the staged row for
+  // it, so what it reads does not matter.
+  if (has_new) {
+    constexpr int DS = D / NSPLIT;  // K row elements [h*DS, (h+1)*DS): lanes holding 8 of them each
+    uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
+    if (owner && lane >= h * DS / 8 && lane < (h + 1) * DS / 8) *reinterpret_cast<u32x4*>(ck + 8 * lane) = nkv;
+    if (grp == 0) {
+      uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride + kr.new_slot;
+      cv[(int64_t)(16 * db + col) * a.slot_stride] = (uint16_t)nvb;
+    }
+  }
+  // lane (grp, col < R) holds O^T[d = 16*db + 4*grp + j][head col]
+  if (col < R) {
+    uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)pair * R + col) * D;
+    const uint32_t w0 = f32_to_bf16_bits(oacc[0]) | (f32_to_bf16_bits(oacc[1]) << 16);
+    const uint32_t w1 = f32_to_bf16_bits(oacc[2]) | (f32_to_bf16_bits(oacc[3]) << 16);
+    *reinterpret_cast<uint2*>(orow + 16 * db + 4 * grp) = make_uint2(w0, w1);
+  }
+}
