@@ -105,7 +105,7 @@ def _decode_args(**kw):
     (dict(q=None), "NULL"),
     (dict(new_k=1), "together"),
     (dict(kind=_lib.G4_CACHE_LINEAR, key_mask_stride=100), "key_mask_stride"),
-    (dict(capacity=8192, slot_stride=8192, kind=_lib.G4_CACHE_LINEAR, key_mask_stride=8192, group=8), "LDS"),
+    (dict(capacity=32768, slot_stride=32768, kind=_lib.G4_CACHE_LINEAR, key_mask_stride=32768, group=8), "LDS"),
 ])
 def test_decode_rejects_invalid_arguments(override, match):
     a = _decode_args(**override)
