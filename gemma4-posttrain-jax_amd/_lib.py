@@ -22,6 +22,8 @@ G4_APPEND_NORM_V = 2
 G4_APPEND_ROPE_K = 4
 G4_APPEND_NORM_Q = 8
 G4_APPEND_ROPE_Q = 16
+G4_DECODE_SPLIT_KEYS = -1
+G4_ERR_WORKSPACE = -4
 
 
 class G4AppendArgs(ctypes.Structure):

@@ -84,6 +84,7 @@ __device__ __forceinline__ void fused_append(const G4DecodeArgs& a, int pair, co
 #include "g4_decode_bf16.h"
 #include "g4_decode_fast.h"
 #include "g4_decode_stage.h"
+#include "g4_decode_splitk.h"
 
 // ----------------------------------------------------------------------------------------------
 // f32, VALU
@@ -198,9 +199,53 @@ int launch_fast(const G4DecodeArgs& a, int t_alloc, size_t lds, hipStream_t st) 
 }  // namespace
 }  // namespace g4
 
+namespace g4 {
+namespace {
+
+// Whether the call takes the split-K path (bf16, head dims 128/256, rows longer than one split).
+bool use_split_keys(const G4DecodeArgs& a) {
+  if (a.dtype != G4_DTYPE_BF16 || (a.head_dim != 128 && a.head_dim != 256)) return false;
+  const int t_alloc = (a.capacity + 31) / 32 * 32;
+  if (t_alloc <= kSplitSlots) return false;
+  if (a.num_splits == G4_DECODE_SPLIT_KEYS) return true;
+  if (a.num_splits != 0) return false;
+  const int64_t npairs = (int64_t)a.batch * a.kv_heads;
+  return npairs < 256 || fast_lds_bytes(a.group, a.head_dim, t_alloc) > kMaxLdsFast;
+}
+
+template <int D>
+int launch_split_keys(const G4DecodeArgs& a, hipStream_t st) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)decode_bf16_splitk_scores_kernel<D>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)stage_lds_bytes(16)) != hipSuccess ||
+        hipFuncSetAttribute((const void*)decode_bf16_splitk_values_kernel<D>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)stage_lds_bytes(16)) != hipSuccess)
+      return fail(G4_ERR_LAUNCH, "g4_decode_attention: cannot raise the LDS limit");
+    attr_set = true;
+  }
+  const int64_t npairs = (int64_t)a.batch * a.kv_heads;
+  SplitKWorkspace ws;
+  ws.n_splits = (a.capacity + kSplitSlots - 1) / kSplitSlots;
+  ws.c_pad = ws.n_splits * kSplitSlots;
+  ws.scores = reinterpret_cast<uint16_t*>(a.workspace);
+  ws.stats = reinterpret_cast<float*>(ws.scores + npairs * a.group * ws.c_pad);
+  ws.partials = ws.stats + npairs * ws.n_splits * a.group * 2;
+  const dim3 grid((unsigned)(npairs * ws.n_splits)), block(kDecodeWaves * 64);
+  const size_t lds = stage_lds_bytes(a.group);
+  hipLaunchKernelGGL(decode_bf16_splitk_scores_kernel<D>, grid, block, lds, st, a, ws);
+  hipLaunchKernelGGL(decode_bf16_splitk_values_kernel<D>, grid, block, lds, st, a, ws);
+  hipLaunchKernelGGL(decode_splitk_combine_kernel, dim3((unsigned)npairs), dim3(256), 0, st, a, ws);
+  return G4_OK;
+}
+
+}  // namespace
+}  // namespace g4
+
 extern "C" size_t g4_decode_workspace_size(const G4DecodeArgs* args) {
-  (void)args;
-  return 0;
+  using namespace g4;
+  if (!args || !use_split_keys(*args)) return 0;
+  return splitk_workspace_bytes(args->batch * args->kv_heads, args->group, args->head_dim, args->capacity);
 }
 
 extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
@@ -229,6 +274,20 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int t_alloc = (a.capacity + 31) / 32 * 32;
   const dim3 grid((unsigned)((int64_t)a.batch * a.kv_heads));
+  if (a.num_splits < G4_DECODE_SPLIT_KEYS || a.num_splits > 2)
+    return fail(G4_ERR_INVALID, "g4_decode_attention: num_splits %d", a.num_splits);
+  if (use_split_keys(a)) {
+    const size_t need = splitk_workspace_bytes(a.batch * a.kv_heads, a.group, a.head_dim, a.capacity);
+    if (!a.workspace || a.workspace_bytes < need)
+      return fail(G4_ERR_WORKSPACE, "g4_decode_attention: split-K needs %zu B of workspace (have %zu)", need,
+                  a.workspace ? a.workspace_bytes : (size_t)0);
+    const int rc = a.head_dim == 256 ? launch_split_keys<256>(a, st) : launch_split_keys<128>(a, st);
+    if (rc != G4_OK) return rc;
+    return check_launch("g4_decode_attention");
+  }
+  if (a.num_splits == G4_DECODE_SPLIT_KEYS)
+    return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: split-K needs bf16, head_dim 128/256, capacity > %d",
+                kSplitSlots);
   if (a.dtype == G4_DTYPE_BF16) {
     if (a.head_dim == 128 || a.head_dim == 256) {
       // num_splits: workgroups per (b, kv head), each owning a slice of the value dims

@@ -1,0 +1,280 @@
+// bf16 decode attention over long rows, split over 512-slot key ranges (flash-decoding style):
+// the global-layer linear cache of a long context, where a few (b, kv head) pairs hold tens of
+// thousands of slots. Included by g4_decode.hip after g4_decode_stage.h.
+//
+// Three launches, one workgroup per (pair, split) in the first two:
+//   scores   K of the split -> bf16-rounded masked scores (workspace) and, per head, the split's
+//            max m_s and l_s = sum exp(s - m_s). Also the fused append: the split holding the
+//            appended slot substitutes the new K row and writes the slot (K row and V^T column)
+//            back to the cache after its loads.
+//   values   V^T loads of the split are issued first; meanwhile the row statistics
+//            m = max m_s, l = sum_s l_s * exp(m_s - m) are formed (fixed split order), then the
+//            exact probabilities bf16(exp(s - m) / l) of the split and its f32 partial of O.
+//   combine  O = sum of the partials in split order, rounded to bf16.
+// The probabilities are rounded exactly as the single-pass kernels round them (after the
+// division by the full-row sum), so the result differs from theirs only in f32 summation order.
+//
+// Workspace: scores bf16 [pairs][R][C32] | stats f32 [pairs][splits][R][2] |
+//            partials f32 [pairs][splits][R][D]      (C32 = capacity rounded up to 32 * 16).
+
+constexpr int kSplitSlots = 2 * NW * 32;  // slots per split (16 chunks)
+
+struct SplitKWorkspace {
+  uint16_t* scores;
+  float* stats;
+  float* partials;
+  int n_splits;  // splits per pair: ceil(capacity / kSplitSlots)
+  int c_pad;     // row length of the score array: n_splits * kSplitSlots
+};
+
+__host__ __device__ inline size_t splitk_workspace_bytes(int npairs, int R, int D, int capacity) {
+  const size_t n_splits = (size_t)(capacity + kSplitSlots - 1) / kSplitSlots;
+  return (size_t)npairs * R * n_splits * kSplitSlots * 2 + (size_t)npairs * n_splits * R * 2 * 4 +
+         (size_t)npairs * n_splits * R * D * 4;
+}
+
+__device__ __forceinline__ bf16x8 q_operand_global(const G4DecodeArgs& a, int pair, int R, int D, int col, int grp,
+                                                   int s) {
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (col < R)
+    v = load16(reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)pair * R + col) * D + 32 * s + 8 * grp);
+  return as_bf16x8(v);
+}
+
+template <int D>
+__global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_scores_kernel(G4DecodeArgs a,
+                                                                                       SplitKWorkspace ws) {
+  __shared__ __attribute__((aligned(16))) uint16_t nk_lds[D];
+  extern __shared__ float smem[];
+  const int R = a.group;
+  uint16_t* sp = reinterpret_cast<uint16_t*>(smem);                // [R][stride] scores of the split
+  float* wmax = reinterpret_cast<float*>(sp + R * kStageStride);  // [NW][16]
+  float* bsum = wmax + NW * 16;                                    // [R][2]
+  const int pair = blockIdx.x / ws.n_splits, split = blockIdx.x % ws.n_splits;
+  const int b = pair / a.kv_heads;
+  const KeyRange kr = key_range(a, b);
+  const int n_chunks = (kr.n_keys + 31) >> 5;
+  const int cbase = split * 2 * NW;  // first chunk of the split
+  if (cbase >= n_chunks) return;     // the split lies beyond the row (whole workgroup)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const __amdgpu_buffer_rsrc_t rk =
+      make_rsrc(reinterpret_cast<const uint16_t*>(a.cache_k) + (int64_t)pair * a.slot_stride * D,
+                (uint32_t)a.slot_stride * D * 2u);
+  const bool has_new = kr.new_slot >= 0 && (kr.new_slot >> 5) >= cbase && (kr.new_slot >> 5) < cbase + 2 * NW;
+  const bool owner = has_new && (int)((kr.new_slot >> 5) & (NW - 1)) == w;
+
+  u32x4 nkv = {0u, 0u, 0u, 0u};
+  if (owner && lane < D / 8) nkv = load16(reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D + 8 * lane);
+  bf16x8 qop[D / 32];
+#pragma unroll
+  for (int s = 0; s < D / 32; ++s) qop[s] = q_operand_global(a, pair, R, D, col, grp, s);
+  const int cc0 = cbase + w, cc1 = cbase + w + NW;  // this wave's chunks
+  const int c0 = cc0 << 5, c1 = cc1 << 5;
+  uint8_t mb0, mb1;
+  const bool ok0 = slot_valid_flat(a, b, kr, c0 + (lane & 31), mb0);
+  const bool ok1 = slot_valid_flat(a, b, kr, c1 + (lane & 31), mb1);
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 k0[2][D / 32], k1[2][D / 32];
+  load_k_chunk<D>(k0, rk, c0, col, grp);
+  load_k_chunk<D>(k1, rk, c1, col, grp);
+  __builtin_amdgcn_sched_barrier(0);
+  if (owner && lane < D / 8) reinterpret_cast<u32x4*>(nk_lds)[lane] = nkv;  // read back by this wave only
+  const uint64_t vb0 = __ballot(ok0 && mb0 != 0);
+  const uint64_t vb1 = __ballot(ok1 && mb1 != 0);
+
+  // scores of the split at local slots [0, 512): chunk cc at local offset 32 * (cc - cbase)
+  float mx = kBf16Min;
+  if (cc0 < n_chunks) {
+    patch_k_sel<D>(k0, nk_lds, kr.new_slot, c0, col, grp);
+    mx = score_to_lds<D>(k0, qop, vb0, sp, kStageStride, 32 * w, R, col, grp, mx);
+  }
+  if (cc1 < n_chunks) {
+    patch_k_sel<D>(k1, nk_lds, kr.new_slot, c1, col, grp);
+    mx = score_to_lds<D>(k1, qop, vb1, sp, kStageStride, 32 * (w + NW), R, col, grp, mx);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (grp == 0) wmax[w * 16 + col] = mx;
+  __syncthreads();
+
+  // split statistics on all threads (thread t: local slots 256*(w&1) + 4*lane .. +3 of head 4i + w/2)
+  const int n_local = (n_chunks - cbase < 2 * NW ? n_chunks - cbase : 2 * NW) << 5;  // slots scored here
+  const int slot = 256 * (w & 1) + 4 * lane;
+  float msplit[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int hh = 4 * i + (w >> 1);
+    msplit[i] = kBf16Min;
+    if (hh < R) {
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) msplit[i] = fmaxf(msplit[i], wmax[ww * 16 + hh]);
+      const uint2 sv = *reinterpret_cast<const uint2*>(sp + hh * kStageStride + slot);
+      const float s4[4] = {bf16_lo(sv.x), bf16_hi(sv.x), bf16_lo(sv.y), bf16_hi(sv.y)};
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) part += slot + j < n_local ? expf(s4[j] - msplit[i]) : 0.f;
+      part = wave_sum64(part);
+      if (lane == 0) bsum[2 * hh + (w & 1)] = part;
+      // the split's scores to the workspace (slots beyond n_local are never read)
+      *reinterpret_cast<uint2*>(ws.scores + ((int64_t)pair * R + hh) * ws.c_pad + split * kSplitSlots + slot) = sv;
+    }
+  }
+  __syncthreads();
+  if (tid < R) {
+    float m = kBf16Min;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) m = fmaxf(m, wmax[ww * 16 + tid]);
+    float* st = ws.stats + (((int64_t)pair * ws.n_splits + split) * R + tid) * 2;
+    st[0] = m;
+    st[1] = bsum[2 * tid] + bsum[2 * tid + 1];
+  }
+
+  // the fused append's cache write, after this workgroup's loads; the values launch (next in
+  // stream order) reads the V^T column from the cache
+  if (has_new) {
+    uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
+    if (owner && lane < D / 8) *reinterpret_cast<u32x4*>(ck + 8 * lane) = nkv;
+    uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride + kr.new_slot;
+    const uint16_t* nv = reinterpret_cast<const uint16_t*>(a.new_v) + (int64_t)pair * D;
+    for (int d = tid; d < D; d += blockDim.x) cv[(int64_t)d * a.slot_stride] = nv[d];
+  }
+}
+
+// Row statistics from the per-split ones (fixed split order): m, l per head into LDS; returns
+// whether the row has no valid slot.
+__device__ __forceinline__ bool splitk_row_stats(const SplitKWorkspace& ws, int pair, int R, int n_splits_row,
+                                                  float* mh, float* lh, int w, int n_waves, int lane) {
+  const float* st = ws.stats + (int64_t)pair * ws.n_splits * R * 2;
+  for (int hh = w; hh < R; hh += n_waves) {  // one wave per head
+    float m = kBf16Min;
+    for (int s = lane; s < n_splits_row; s += 64) m = fmaxf(m, st[(s * R + hh) * 2]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    // l = sum_s l_s * exp(m_s - m), per lane in split order, then across lanes in a fixed tree
+    float l = 0.f;
+    for (int s = lane; s < n_splits_row; s += 64) l += st[(s * R + hh) * 2 + 1] * expf(st[(s * R + hh) * 2] - m);
+    l = wave_sum64(l);
+    if (lane == 0) {
+      mh[hh] = m;
+      lh[hh] = l;
+    }
+  }
+  __syncthreads();
+  return mh[0] == kBf16Min;  // head 0's max (key validity does not depend on the head)
+}
+
+template <int D>
+__global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_kernel(G4DecodeArgs a,
+                                                                                       SplitKWorkspace ws) {
+  constexpr int DPW = D / 16 / NW;  // d-blocks per wave (all of D in one workgroup)
+  __shared__ float mh[16], lh[16];
+  extern __shared__ float smem[];
+  const int R = a.group;
+  uint16_t* sp = reinterpret_cast<uint16_t*>(smem);  // [R][stride] probabilities of the split
+  const int pair = blockIdx.x / ws.n_splits, split = blockIdx.x % ws.n_splits;
+  const int b = pair / a.kv_heads;
+  const KeyRange kr = key_range(a, b);
+  const int n_chunks = (kr.n_keys + 31) >> 5;
+  const int n_splits_row = (n_chunks + 2 * NW - 1) / (2 * NW);
+  const int cbase = split * 2 * NW;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const int64_t ss = a.slot_stride;
+  const __amdgpu_buffer_rsrc_t rv =
+      make_rsrc(reinterpret_cast<const uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride,
+                (uint32_t)a.slot_stride * D * 2u);
+  const int n_chunks_cap = (a.capacity + 31) >> 5;
+  if (cbase >= n_chunks_cap) return;  // beyond the capacity (whole workgroup)
+
+  // V^T of the split's scanned chunks, requested before anything else
+  const int n_here = cbase < n_chunks ? (n_chunks - cbase < 2 * NW ? n_chunks - cbase : 2 * NW) : 0;
+  u32x4 vv[2 * NW][DPW];
+#pragma unroll
+  for (int i = 0; i < 2 * NW; ++i) {
+    if (i < n_here) {
+      const uint32_t voff = (uint32_t)(col * ss + ((cbase + i) << 5) + 8 * grp) * 2u;
+#pragma unroll
+      for (int ii = 0; ii < DPW; ++ii) vv[i][ii] = buffer_load16(rv, voff, (uint32_t)(16 * (w * DPW + ii) * ss) * 2u);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const bool all_masked = splitk_row_stats(ws, pair, R, n_splits_row, mh, lh, w, NW, lane);
+  if (!all_masked && split >= n_splits_row) return;  // nothing of the row here (whole workgroup)
+  // a row without any valid slot: uniform bf16(1/capacity) over every slot below the capacity
+  const int n_mine = all_masked ? (n_chunks_cap - cbase < 2 * NW ? n_chunks_cap - cbase : 2 * NW) : n_here;
+  const int slot = 256 * (w & 1) + 4 * lane;
+  const float pu = round_bf16(1.0f / (float)a.capacity);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int hh = 4 * i + (w >> 1);
+    if (hh < R) {
+      float p[4];
+      const int gslot = split * kSplitSlots + slot;  // row slot of entry j = 0
+      if (all_masked) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[j] = gslot + j < a.capacity ? pu : 0.f;
+      } else {
+        const uint2 sv =
+            *reinterpret_cast<const uint2*>(ws.scores + ((int64_t)pair * R + hh) * ws.c_pad + gslot);
+        const float s4[4] = {bf16_lo(sv.x), bf16_hi(sv.x), bf16_lo(sv.y), bf16_hi(sv.y)};
+        const float m = mh[hh], l = lh[hh];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[j] = slot + j < (n_here << 5) ? expf(s4[j] - m) / l : 0.f;
+      }
+      *reinterpret_cast<uint2*>(sp + hh * kStageStride + slot) =
+          make_uint2(f32_to_bf16_bits(p[0]) | (f32_to_bf16_bits(p[1]) << 16),
+                     f32_to_bf16_bits(p[2]) | (f32_to_bf16_bits(p[3]) << 16));
+    }
+  }
+  __syncthreads();
+
+  floatx4 oacc[DPW];
+#pragma unroll
+  for (int ii = 0; ii < DPW; ++ii) oacc[ii] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 2 * NW; ++i) {
+    if (i < n_here) {
+      const bf16x8 pop = prob_operand(sp, kStageStride, (i << 5) + 8 * grp, R, col);
+#pragma unroll
+      for (int ii = 0; ii < DPW; ++ii) oacc[ii] = mfma16x16x32(as_bf16x8(vv[i][ii]), pop, oacc[ii]);
+    }
+  }
+  for (int i = n_here; i < n_mine; ++i) {  // fully masked row: slots never scanned
+    const uint32_t voff = (uint32_t)(col * ss + ((cbase + i) << 5) + 8 * grp) * 2u;
+    const bf16x8 pop = prob_operand(sp, kStageStride, (i << 5) + 8 * grp, R, col);
+#pragma unroll
+    for (int ii = 0; ii < DPW; ++ii)
+      oacc[ii] = mfma16x16x32(as_bf16x8(buffer_load16(rv, voff, (uint32_t)(16 * (w * DPW + ii) * ss) * 2u)), pop,
+                              oacc[ii]);
+  }
+  // lane (grp, col < R) holds O^T[d = 16*(w*DPW + ii) + 4*grp + j][head col]
+  if (col < R) {
+    float* o = ws.partials + (((int64_t)pair * ws.n_splits + split) * R + col) * D;
+#pragma unroll
+    for (int ii = 0; ii < DPW; ++ii)
+      *reinterpret_cast<floatx4*>(o + 16 * (w * DPW + ii) + 4 * grp) = oacc[ii];
+  }
+}
+
+// O = sum of the split partials (split order), bf16. One workgroup of 256 threads per pair.
+__global__ __launch_bounds__(256) void decode_splitk_combine_kernel(G4DecodeArgs a, SplitKWorkspace ws) {
+  __shared__ float mh[16], lh[16];
+  const int R = a.group, D = a.head_dim;
+  const int pair = blockIdx.x;
+  const int b = pair / a.kv_heads;
+  const KeyRange kr = key_range(a, b);
+  const int n_chunks = (kr.n_keys + 31) >> 5;
+  const int n_splits_row = (n_chunks + 2 * NW - 1) / (2 * NW);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const bool all_masked = splitk_row_stats(ws, pair, R, n_splits_row, mh, lh, w, (int)(blockDim.x >> 6), lane);
+  const int n = all_masked ? ws.n_splits : n_splits_row;
+  uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + (int64_t)pair * R * D;
+  for (int idx = tid; idx < R * D; idx += blockDim.x) {
+    float o = 0.f;
+    for (int s = 0; s < n; ++s) o += ws.partials[((int64_t)pair * ws.n_splits + s) * R * D + idx];
+    out[idx] = (uint16_t)f32_to_bf16_bits(o);
+  }
+}

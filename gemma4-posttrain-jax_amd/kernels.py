@@ -160,7 +160,9 @@ def decode_attention(
 ) -> torch.Tensor:
     """g4_decode_attention: q ``[B, Hkv, R, D]`` against ``layer``; returns ``[B, Hkv, R, D]``.
     With ``new_k``/``new_v`` (``[B, Hkv, D]``) the token's K/V is stored at ``q_pos`` first.
-    ``num_splits``: workgroups per (b, kv head); 0 lets the library choose."""
+    ``num_splits``: 0 lets the library choose; 1 or 2 workgroups per (b, kv head) in one pass;
+    ``_lib.G4_DECODE_SPLIT_KEYS`` splits the key range (long rows). A workspace of the size the
+    library asks for is allocated from torch's caching allocator on the current stream."""
 
     B, H, R, D = q.shape
     if not q.is_contiguous() or q.dtype != layer.key.dtype:
@@ -190,6 +192,11 @@ def decode_attention(
         new_k=_ptr(new_k), new_v=_ptr(new_v), out=_ptr(out), workspace=None, workspace_bytes=0,
         num_splits=num_splits,
     )
+    need = _lib.lib().g4_decode_workspace_size(ctypes.byref(a))
+    ws = None
+    if need:
+        ws = torch.empty(need, dtype=torch.uint8, device=q.device)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), need
     _lib.check(_lib.lib().g4_decode_attention(ctypes.byref(a), _stream()), "g4_decode_attention")
     return out
 

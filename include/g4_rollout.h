@@ -135,9 +135,19 @@ typedef struct G4DecodeArgs {
   void* out;            /* [B, Hkv, R, D] */
   void* workspace;      /* split-K scratch, >= g4_decode_workspace_size(args) bytes */
   size_t workspace_bytes;
-  int32_t num_splits;   /* 0 = choose automatically; 1 = one workgroup per (b, h) */
+  int32_t num_splits;   /* 0 = choose automatically; 1 or 2 = workgroups per (b, kv head), one
+                           pass, each owning a slice of the head dim (2: head dim 256);
+                           G4_DECODE_SPLIT_KEYS = split the key range (bf16, head dims 128/256) */
 } G4DecodeArgs;
 
+/* num_splits value: split-K over 512-slot key ranges in three launches (scores, values,
+ * combine), for long rows over few (b, kv head) pairs. Uses the workspace. The automatic
+ * choice takes it for bf16 rows longer than 512 slots when B * Hkv < 256 or when a one-pass
+ * row does not fit in LDS. */
+#define G4_DECODE_SPLIT_KEYS (-1)
+
+/* Bytes of workspace the call described by args needs (0 when the chosen path uses none). The
+ * workspace is plain scratch: no state is kept in it between calls. */
 size_t g4_decode_workspace_size(const G4DecodeArgs* args);
 int g4_decode_attention(const G4DecodeArgs* args, void* stream);
 

@@ -105,13 +105,36 @@ def _decode_args(**kw):
     (dict(q=None), "NULL"),
     (dict(new_k=1), "together"),
     (dict(kind=_lib.G4_CACHE_LINEAR, key_mask_stride=100), "key_mask_stride"),
-    (dict(capacity=32768, slot_stride=32768, kind=_lib.G4_CACHE_LINEAR, key_mask_stride=32768, group=8), "LDS"),
+    (dict(capacity=32768, slot_stride=32768, kind=_lib.G4_CACHE_LINEAR, key_mask_stride=32768,
+          dtype=_lib.G4_DTYPE_F32), "too large"),
+    (dict(num_splits=3), "num_splits"),
+    (dict(num_splits=_lib.G4_DECODE_SPLIT_KEYS), "split-K needs"),
+    (dict(num_splits=2, head_dim=128), "num_splits 2 with head_dim 128"),
 ])
 def test_decode_rejects_invalid_arguments(override, match):
     a = _decode_args(**override)
     rc = _lib.lib().g4_decode_attention(ctypes.byref(a), None)
     assert rc in (-1, -2)
     assert re.search(match, _lib.lib().g4_last_error().decode())
+
+
+def test_decode_split_keys_workspace():
+    """Long rows over few pairs take the split-K path: the library reports its workspace and
+    refuses to run without it."""
+
+    L = _lib.lib()
+    long_rows = dict(capacity=32768, slot_stride=32768, kind=_lib.G4_CACHE_LINEAR, key_mask_stride=32768, batch=16)
+    a = _decode_args(**long_rows)
+    need = L.g4_decode_workspace_size(ctypes.byref(a))
+    n_splits = 32768 // 512
+    assert need == 32 * 4 * 32768 * 2 + 32 * n_splits * 4 * 2 * 4 + 32 * n_splits * 4 * 256 * 4
+    assert L.g4_decode_attention(ctypes.byref(a), None) == _lib.G4_ERR_WORKSPACE
+    assert re.search("workspace", L.g4_last_error().decode())
+    a = _decode_args(**long_rows, workspace=1, workspace_bytes=need - 1)
+    assert L.g4_decode_attention(ctypes.byref(a), None) == _lib.G4_ERR_WORKSPACE
+    # ring rows of 512 slots and one-pass choices need none
+    assert L.g4_decode_workspace_size(ctypes.byref(_decode_args())) == 0
+    assert L.g4_decode_workspace_size(ctypes.byref(_decode_args(**long_rows, num_splits=1))) == 0
 
 
 def test_append_and_prefill_reject_invalid_arguments():

@@ -186,6 +186,37 @@ def test_decode_linear_long_rows(device, D, num_splits):
                  fused=True, seed=23, num_splits=num_splits)
 
 
+@pytest.mark.parametrize("D", [128, 256])
+def test_decode_split_keys_long_context(device, D):
+    """BASELINE config 3 shape at reduced capacity: global-layer linear cache with ragged
+    lengths over few (b, kv head) pairs, so the library splits the key range (scores / values /
+    combine launches). Rows end mid-split, one row is shorter than a split, one is fully masked,
+    one is left-padded; the appended slot lands in different splits."""
+
+    rng = np.random.default_rng(9)
+    B, H, R, C = 4, 2, 4, 4096
+    q_pos = np.array([4095, 2600, 300, 1500])
+    key_mask = np.ones((B, C), bool)
+    key_mask[2, :] = False
+    key_mask[3, :700] = False
+    _decode_case(device, O.BF16, B=B, H=H, R=R, D=D, cap=C, ring=False, window=0, q_pos=q_pos, key_mask=key_mask,
+                 fused=True, seed=24)
+
+
+@pytest.mark.parametrize("D", [128, 256])
+def test_decode_split_keys_forced_matches_one_pass(device, D):
+    """num_splits = G4_DECODE_SPLIT_KEYS on a 768-slot cache (where the one-pass kernel also
+    applies) against the oracle; unfused (no append)."""
+
+    rng = np.random.default_rng(10)
+    B, H, R, C = 3, 2, 4, 768
+    q_pos = np.array([767, 513, 100])
+    key_mask = np.ones((B, C), bool)
+    key_mask[1, 500:520] = False
+    _decode_case(device, O.BF16, B=B, H=H, R=R, D=D, cap=C, ring=False, window=0, q_pos=q_pos, key_mask=key_mask,
+                 fused=False, seed=25, num_splits=_lib.G4_DECODE_SPLIT_KEYS)
+
+
 @pytest.mark.parametrize("dtype,D", [(O.BF16, 64), (O.BF16, 256), (O.F32, 64)])
 def test_decode_ring_partial_and_masked_rows(device, dtype, D):
     """Ring not yet full, left padding, a finished row and a fully masked row (uniform average)."""
