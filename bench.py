@@ -9,7 +9,10 @@ graph so the timed region holds only GPU work.
 Also reported: ``decode_tok_s_b256`` — full decode steps (30-layer E2B-like model, B=256, T=1
 sampling, BASELINE ``configs[4]``) per second x 256, and the oracle's CPU time for the same step.
 
-Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2b] [--no-cpu]``.
+Also: ``long_context_decode`` (``configs[2]``, split-K decode over a 32768-slot linear cache,
+HBM-bound) and ``prefill_attention`` (``configs[3]``, causal / sliding attention on MFMA).
+
+Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2b] [--no-cpu] [--no-extra]``.
 """
 
 from __future__ import annotations
@@ -126,6 +129,113 @@ def bench_decode_attention(steps: int, warmup: int, num_splits: int = 0) -> dict
     torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - t0) * 1e3
     return {"ms_total": ms, "ms_per_step": ms / steps, "eager_ms_per_step": eager_ms / steps}
+
+
+def _graph_time(step, n_warm: int, n_timed: int) -> float:
+    """ms per step of `step(i)` replayed from a HIP graph (steps n_warm .. n_warm + n_timed - 1)."""
+
+    import torch
+
+    for i in range(min(n_warm, 2)):
+        step(i)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    gw, gt = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(gw, stream=s):
+            for i in range(n_warm):
+                step(i)
+        with torch.cuda.graph(gt, stream=s):
+            for i in range(n_warm, n_warm + n_timed):
+                step(i)
+    torch.cuda.synchronize()
+    gw.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    gt.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n_timed
+
+
+def bench_long_context_decode(steps: int = 16, warmup: int = 4) -> dict:
+    """global-layer decode over a linear cache, B=16, Hq=8/Hkv=2, D=256,
+    capacity 32768, per-row lengths U[1024, 32768] growing by one per step (split-K path).
+    Algorithmic bytes: K+V of every valid slot once, Q in, O out, the new K/V row."""
+
+    import torch
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    from gemma4_posttrain_jax_amd import kernels
+    from gemma4_posttrain_jax_amd.kvcache import new_layer_cache
+
+    Bq, C = 16, 32768
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(3)
+    layer = new_layer_cache(Bq, HKV, D, C, False, torch.bfloat16, dev)
+    layer.key.normal_(generator=g)
+    layer.value_t.normal_(generator=g)
+    rng = np.random.default_rng(0)
+    total = warmup + steps
+    len0 = rng.integers(1024, C - total, Bq).astype(np.int32)
+    q_pos = torch.from_numpy(len0[None, :] + np.arange(total, dtype=np.int32)[:, None]).to(dev).contiguous()
+    key_mask = torch.ones((Bq, C), dtype=torch.bool, device=dev)
+    q = torch.randn((total, Bq, HKV, R, D), device=dev, generator=g).to(torch.bfloat16)
+    nk = torch.randn((total, Bq, HKV, D), device=dev, generator=g).to(torch.bfloat16)
+    nv = torch.randn((total, Bq, HKV, D), device=dev, generator=g).to(torch.bfloat16)
+    out = torch.empty((total, Bq, HKV, R, D), device=dev, dtype=torch.bfloat16)
+
+    def step(i):
+        kernels.decode_attention(layer, q[i], key_mask, q_pos=q_pos[i], window=0, out=out[i], new_k=nk[i],
+                                 new_v=nv[i])
+
+    ms = _graph_time(step, warmup, steps)
+    lens = len0[None, :] + np.arange(warmup, total)[:, None] + 1  # valid slots incl. the appended one
+    kv_bytes = float(lens.sum(axis=1).mean()) * HKV * D * 2 * 2
+    small = Bq * HQ * D * 2 * 2 + Bq * HKV * D * 2 * 2 * 2
+    gbs = (kv_bytes + small) / (ms * 1e-3) / 1e9
+    return {"ms_per_step": ms, "gbs": gbs, "bytes_per_step": kv_bytes + small}
+
+
+def bench_prefill(reps: int = 5) -> dict:
+    """chunked-prefill attention, B=8, S=4096, Hq=8/Hkv=2, D=256 bf16, one
+    global (causal) and one sliding-window (512) layer. Algorithmic flops = 4 * B * Hq * D *
+    (valid (query, key) pairs per (b, h))."""
+
+    import torch
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    from gemma4_posttrain_jax_amd import kernels
+
+    Bp, S = 8, 4096
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(4)
+    q = torch.randn((Bp, S, HKV, R, D), device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn((Bp, HKV, S, D), device=dev, generator=g).to(torch.bfloat16)
+    vt = torch.randn((Bp, HKV, D, S), device=dev, generator=g).to(torch.bfloat16)
+    key_mask = torch.ones((Bp, S), dtype=torch.bool, device=dev)
+    out = torch.empty_like(q)
+    res = {}
+    for name, win in (("global", 0), ("sliding", W)):
+        pairs = S * (S + 1) // 2 if win == 0 else win * (win + 1) // 2 + (S - win) * win
+        flops = 4.0 * Bp * HQ * D * pairs
+        kernels.prefill_attention(q, k, vt, key_mask, window=win, out=out)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            kernels.prefill_attention(q, k, vt, key_mask, window=win, out=out)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        res[name] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12}
+    return res
 
 
 def cpu_baseline_decode_attention(target_s: float = 12.0) -> dict:
@@ -298,6 +408,7 @@ def main() -> int:
     ap.add_argument("--e2b-steps", type=int, default=8)
     ap.add_argument("--no-e2b", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the configs[2]/[3] lines")
     ap.add_argument("--num-splits", type=int, default=0,
                     help="workgroups per (b, kv head) for decode attention (0: library default)")
     args = ap.parse_args()
@@ -330,6 +441,17 @@ def main() -> int:
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "eager_ms_per_step": round(res["eager_ms_per_step"], 4),
     }
+    if not args.no_extra:
+        lc = bench_long_context_decode()
+        line["long_context_decode"] = {"workload": "configs[2]: B16 Hq8/Hkv2 D256, linear cache 32768, ragged "
+                                       "lengths U[1024,32768], split-K", "ms_per_step": round(lc["ms_per_step"], 4),
+                                       "GB/s": round(lc["gbs"], 1), "frac_hbm_peak": round(lc["gbs"] / HBM_PEAK_GBS, 4)}
+        pf = bench_prefill()
+        line["prefill_attention"] = {
+            "workload": "configs[3]: B8 S4096 Hq8/Hkv2 D256 bf16 attention, per layer",
+            **{f"{k}_ms": round(v["ms"], 3) for k, v in pf.items()},
+            **{f"{k}_TFLOP/s": round(v["tflops"], 1) for k, v in pf.items()},
+            **{f"{k}_frac_mfma_peak": round(v["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4) for k, v in pf.items()}}
     if not args.no_e2b:
         e2b = bench_e2b_decode(args.e2b_steps, 2)
         line["decode_tok_s_b256"] = round(e2b["decode_tok_s"], 1)
