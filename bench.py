@@ -340,20 +340,21 @@ def bench_e2b_decode(steps: int, warmup: int, batch: int = 256, prompt: int = 25
     logits = out.logits[:, -1].float()
     gen = torch.Generator(device=dev).manual_seed(2)
     lengths = torch.full((batch,), prompt, dtype=torch.int32, device=dev)
-    times = []
-    for i in range(warmup + steps):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
+    active = torch.ones(batch, dtype=torch.bool, device=dev)
+    engine = SMP.GraphedDecodeStep(params, cfg, cache)  # what generate() replays per token
+    torch.cuda.synchronize()
+    for i in range(warmup):
         tok, _ = SMP._sample_token(logits, gen, temperature=1.0, top_k=0, top_p=1.0)
-        dec = SMP.decode_step(params, cfg, tok, lengths + i, cache)
-        logits = dec.logits[:, -1].float()
-        cache = dec.kv_cache
-        torch.cuda.synchronize()
-        if i >= warmup:
-            times.append(time.perf_counter() - t0)
-    s = float(np.mean(times))
+        logits = engine.step(tok, lengths + i, active)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(warmup, warmup + steps):  # sample + decode, as generate()'s loop body
+        tok, _ = SMP._sample_token(logits, gen, temperature=1.0, top_k=0, top_p=1.0)
+        logits = engine.step(tok, lengths + i, active)
+    torch.cuda.synchronize()
+    s = (time.perf_counter() - t0) / steps
     return {"decode_s_per_step": s, "decode_tok_s": batch / s, "prefill_s": prefill_s, "params": params, "cfg": cfg,
-            "cache": cache, "logits": logits}
+            "cache": engine.kv_cache, "logits": logits}
 
 
 def cpu_baseline_e2b_decode(gpu: dict, steps: int = 2) -> dict:

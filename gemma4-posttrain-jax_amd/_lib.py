@@ -65,6 +65,10 @@ PROTOTYPES = {
     "g4_prefill_attention": (c_int32, [POINTER(G4PrefillArgs), c_void_p]),
     "g4_kv_source_layers": (c_int32, [c_int32, c_int32, POINTER(c_int32), POINTER(c_int32)]),
     "g4_ring_slot_positions": (c_int32, [c_int32, c_int32, POINTER(c_int32)]),
+    "g4_rms_norm": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_float, c_void_p, c_void_p]),
+    "g4_residual_norm": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                   c_float, c_void_p, c_void_p, c_void_p]),
+    "g4_gelu_mul": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "g4_last_error": (c_char_p, []),
     "g4_version": (c_char_p, []),
 }

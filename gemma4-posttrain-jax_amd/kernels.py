@@ -229,3 +229,59 @@ def prefill_attention(
     )
     _lib.check(_lib.lib().g4_prefill_attention(ctypes.byref(a), _stream()), "g4_prefill_attention")
     return out
+
+
+# --- fused decoder-layer glue ------------------------------------------------------------------------
+
+
+def _rows(x: torch.Tensor) -> tuple[int, int]:
+    if not x.is_contiguous():
+        raise ValueError("expected a contiguous tensor")
+    return x.numel() // x.shape[-1], x.shape[-1]
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """g4_rms_norm over the last dim: ``cast(x * (mean(x^2) + eps)^-0.5 * w)`` (f32 inside)."""
+
+    rows, cols = _rows(x)
+    if weight is not None and (weight.dtype != x.dtype or weight.numel() != cols or not weight.is_contiguous()):
+        raise ValueError("weight must be a contiguous [cols] tensor in x's dtype")
+    out = torch.empty_like(x) if out is None else out
+    _lib.check(_lib.lib().g4_rms_norm(_code(x), rows, cols, _ptr(x), _ptr(weight), eps, _ptr(out), _stream()),
+               "g4_rms_norm")
+    return out
+
+
+def residual_norm(branch: torch.Tensor, branch_weight: torch.Tensor | None, residual: torch.Tensor, *,
+                  scalar: torch.Tensor | None, next_weight: torch.Tensor | None, eps: float,
+                  with_next: bool = True) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """g4_residual_norm: ``x = cast(cast(residual + cast(rms(branch) * w)) * scalar)`` and, with
+    ``with_next``, ``h = cast(rms(x) * next_weight)``; returns ``(x, h)``. ``scalar`` is a one-
+    element f32 tensor (or None)."""
+
+    rows, cols = _rows(branch)
+    if residual.shape != branch.shape or residual.dtype != branch.dtype or not residual.is_contiguous():
+        raise ValueError("residual must match branch")
+    for w in (branch_weight, next_weight):
+        if w is not None and (w.dtype != branch.dtype or w.numel() != cols or not w.is_contiguous()):
+            raise ValueError("norm weights must be contiguous [cols] tensors in the activation dtype")
+    if scalar is not None and (scalar.dtype != torch.float32 or scalar.numel() != 1):
+        raise ValueError("scalar must be a one-element f32 tensor")
+    x = torch.empty_like(branch)
+    h = torch.empty_like(branch) if with_next else None
+    _lib.check(_lib.lib().g4_residual_norm(_code(branch), rows, cols, _ptr(branch), _ptr(branch_weight),
+                                           _ptr(residual), _ptr(scalar), _ptr(next_weight), eps, _ptr(x), _ptr(h),
+                                           _stream()), "g4_residual_norm")
+    return x, h
+
+
+def gelu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    """g4_gelu_mul: ``[rows, 2F] -> [rows, F]``, ``cast(gelu_tanh(g) * u)`` in f32."""
+
+    rows, cols2 = _rows(gate_up)
+    if cols2 % 2:
+        raise ValueError("gate_up must have an even last dim")
+    out = torch.empty(gate_up.shape[:-1] + (cols2 // 2,), dtype=gate_up.dtype, device=gate_up.device)
+    _lib.check(_lib.lib().g4_gelu_mul(_code(gate_up), rows, cols2 // 2, _ptr(gate_up), _ptr(out), _stream()),
+               "g4_gelu_mul")
+    return out

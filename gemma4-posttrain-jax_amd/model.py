@@ -7,8 +7,10 @@ layout (``PackedWeights``): q/k/v projections fused into one ``[M, (H*R + 2H)*D]
 query columns in (kv head, r) order, o_proj rows in the same order, gate|up fused. Per layer the
 forward runs one hipBLASLt GEMM for q/k/v, the native ``g4_kv_append`` (q/k norms, RoPE, v norm,
 cache append), the native prefill or decode attention kernel, and GEMMs for o_proj and the MLP.
-RMSNorm / residual / gelu glue runs as PyTorch-ROCm elementwise ops with the reference's f32
-rounding points.
+The norm / residual / activation glue runs as three fused native kernels per layer with the
+reference's f32 rounding points: ``g4_residual_norm`` (post-attention norm + residual + pre-MLP
+norm, and post-MLP norm + residual + layer scalar + the next layer's input norm) and
+``g4_gelu_mul``; the per-layer-input branch of configs that have one uses PyTorch-ROCm ops.
 """
 
 from __future__ import annotations
@@ -128,6 +130,7 @@ class PackedLayer(NamedTuple):
     head_dim: int
     has_k: bool
     has_v: bool
+    scalar_f32: torch.Tensor  # [1] f32 layer_scalar (model.py:553)
 
 
 class PackedWeights(NamedTuple):
@@ -176,7 +179,8 @@ def pack_weights(params: Gemma4TextParams, config: Gemma4TextConfig) -> PackedWe
         w_qkv = torch.cat(parts, dim=1).contiguous()
         w_o = a.o_proj.permute(1, 0, 2, 3).reshape(H * R * D, M).contiguous()
         w_gu = torch.cat([lp.mlp.gate_proj, lp.mlp.up_proj], dim=1).contiguous()
-        layers.append(PackedLayer(w_qkv, w_o, w_gu, lp.mlp.down_proj.contiguous(), H, R, D, has_k, has_v))
+        layers.append(PackedLayer(w_qkv, w_o, w_gu, lp.mlp.down_proj.contiguous(), H, R, D, has_k, has_v,
+                                  lp.layer_scalar.float().reshape(1).contiguous()))
     dev = params.embed_tokens.device
     dt = params.embed_tokens.dtype
     inv = {k: torch.from_numpy(v).to(dev) for k, v in _rope_inv_freq(config).items()}
@@ -222,7 +226,8 @@ def _per_layer_inputs(params: Gemma4TextParams, config: Gemma4TextConfig, ids: t
     B, S, M = x.shape
     dt = x.dtype
     token = params.embed_tokens_per_layer[ids]  # [B, S, L, P]
-    token = (token.float() * torch.tensor(math.sqrt(P), dtype=dt, device=x.device).float()).to(dt)
+    scale = float(torch.tensor(math.sqrt(P), dtype=dt))  # sqrt(P) rounded to the activation dtype, on the host
+    token = (token.float() * scale).to(dt)
     ctx = (x.reshape(B * S, M) @ params.per_layer_model_projection.reshape(M, L * P)).reshape(B, S, L, P)
     ctx = (ctx.float() * (config.hidden_size ** -0.5)).to(dt)
     ctx = rms_norm(ctx, params.per_layer_projection_norm.weight, config.rms_norm_eps)
@@ -240,6 +245,7 @@ def forward_gemma4_text(
     cache_mode: Literal["prefill", "append"] = "prefill",
     layer_outputs: list | None = None,
     lora=None,
+    write_pos: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, KVCache | None]:
     """model.py:571-673: hidden after the final norm and the updated cache.
 
@@ -247,7 +253,12 @@ def forward_gemma4_text(
     cache-less path computes the same attention). ``layer_outputs`` collects every decoder
     layer's output (the reference's parity hook, model.py:580). ``lora`` must be None: the
     rollout path runs without adapters (the reference applies LoRA inside the projections,
-    lora.py:107-113)."""
+    lora.py:107-113).
+
+    ``write_pos`` (append mode only): int32 ``[B]`` device tensor holding the physical slot of
+    this step (``kv_cache.length``) for every row. The kernels then read the slot on the device
+    and the key mask is updated in place, so the step has no host-side value baked in and can be
+    captured in a HIP graph and replayed."""
 
     if lora is not None:
         raise NotImplementedError("LoRA adapters are not supported by the native rollout path")
@@ -270,8 +281,16 @@ def forward_gemma4_text(
     if cache_mode == "append" and S != 1:
         raise ValueError(f'cache_mode="append" requires one token, got {S}')
     length = int(kv_cache.length)
-    key_mask = kv_cache.key_mask.clone()
-    key_mask[:, length:length + S] = attention_mask
+    if write_pos is not None:
+        if cache_mode != "append":
+            raise ValueError("write_pos is only used in append mode")
+        key_mask = kv_cache.key_mask
+        key_mask.scatter_(1, write_pos[:, None].long(), attention_mask)
+        slot = write_pos
+    else:
+        key_mask = kv_cache.key_mask.clone()
+        key_mask[:, length:length + S] = attention_mask
+        slot = length
     rot = {t: rotary_tables(pw.inv_freq[t], position_ids) for t in (SLIDING, FULL)}
     sources = kv_source_layers(config)
 
@@ -279,12 +298,12 @@ def forward_gemma4_text(
     flags_kv = _lib.G4_APPEND_NORM_K | _lib.G4_APPEND_ROPE_K | _lib.G4_APPEND_NORM_V
     prompt_kv: dict = {}  # layer index -> (k [B,H,Sp,D], vt [B,H,D,Sp]) for prefill attention
     new_layers = []
+    n_layers = len(params.layers)
+    h = kernels.rms_norm(x, params.layers[0].input_norm.weight, eps)  # layer 0's input norm
     for i, (lp, pk) in enumerate(zip(params.layers, pw.layers)):
         lt = config.layer_types[i]
         window = config.sliding_window if lt == SLIDING else 0
         H, R, D = pk.heads, pk.group, pk.head_dim
-        residual = x
-        h = rms_norm(x, lp.input_norm.weight, eps)
         qkv = (h.reshape(B * S, -1) @ pk.w_qkv).reshape(B, S, -1)
         q = qkv[..., : H * R * D].view(B, S, H, R, D)
         q_out = torch.empty((B, S, H, R, D), dtype=x.dtype, device=dev)
@@ -304,7 +323,7 @@ def forward_gemma4_text(
                 sp = slot_stride_for(S)
                 k_out = torch.empty((B, H, sp, D), dtype=x.dtype, device=dev)
                 vt_out = torch.zeros((B, H, D, sp), dtype=x.dtype, device=dev)
-            kernels.kv_append(layer_cache, k, v, write_pos=length, flags=flags_q | flags_kv, eps=eps, q=q,
+            kernels.kv_append(layer_cache, k, v, write_pos=slot, flags=flags_q | flags_kv, eps=eps, q=q,
                               q_out=q_out, q_norm_weight=lp.attention.q_norm.weight,
                               k_norm_weight=lp.attention.k_norm.weight, rope_cos=cos, rope_sin=sin, k_out=k_out,
                               vt_out=vt_out)
@@ -322,29 +341,34 @@ def forward_gemma4_text(
                 kk, vt = src_cache.key, src_cache.value_t
             attn = kernels.prefill_attention(q_out, kk, vt, key_mask, window=window)
         else:
-            attn = kernels.decode_attention(src_cache, q_out.view(B, H, R, D), key_mask, q_pos=length,
+            attn = kernels.decode_attention(src_cache, q_out.view(B, H, R, D), key_mask, q_pos=slot,
                                             window=config.sliding_window).view(B, 1, H, R, D)
         o = (attn.reshape(B * S, H * R * D) @ pk.w_o).reshape(B, S, -1)
-        o = rms_norm(o, lp.post_attention_norm.weight, eps)
-        x = residual + o
-        residual = x
-        h = rms_norm(x, lp.pre_feedforward_norm.weight, eps)
+        # post-attention norm + residual, then the pre-feedforward norm (one pass)
+        x, h = kernels.residual_norm(o, lp.post_attention_norm.weight, x, scalar=None,
+                                     next_weight=lp.pre_feedforward_norm.weight, eps=eps)
         gu = h.reshape(B * S, -1) @ pk.w_gate_up
-        F = gu.shape[1] // 2
-        act = (gelu_tanh_f32(gu[:, :F]) * gu[:, F:].float()).to(x.dtype)
+        act = kernels.gelu_mul(gu)
         d = (act @ pk.w_down).reshape(B, S, -1)
-        d = rms_norm(d, lp.post_feedforward_norm.weight, eps)
-        x = residual + d
-        if lp.per_layer_input is not None:
+        next_w = params.layers[i + 1].input_norm.weight if i + 1 < n_layers else params.final_norm.weight
+        if lp.per_layer_input is None:
+            # post-feedforward norm + residual, layer scalar, then the next layer's input norm
+            # (the final norm after the last layer)
+            x, h = kernels.residual_norm(d, lp.post_feedforward_norm.weight, x, scalar=pk.scalar_f32,
+                                         next_weight=next_w, eps=eps)
+        else:
+            x, _ = kernels.residual_norm(d, lp.post_feedforward_norm.weight, x, scalar=None, next_weight=None,
+                                         eps=eps, with_next=False)
             g = x.reshape(B * S, -1) @ lp.per_layer_input.gate
             g = (gelu_tanh_f32(g) * pli[:, :, i].reshape(B * S, -1).float()).to(x.dtype)
             g = (g @ lp.per_layer_input.projection).reshape(B, S, -1)
             g = rms_norm(g, lp.per_layer_input.post_norm.weight, eps)
             x = x + g
-        x = (x.float() * lp.layer_scalar.float()).to(x.dtype)
+            x = (x.float() * lp.layer_scalar.float()).to(x.dtype)
+            h = kernels.rms_norm(x, next_w, eps)
         if layer_outputs is not None:
             layer_outputs.append(x)
-    hidden = rms_norm(x, params.final_norm.weight, eps)
+    hidden = h
     if scratch_cache:
         return hidden, None
     return hidden, KVCache(tuple(new_layers), key_mask, length + S)
@@ -371,12 +395,13 @@ def forward_gemma4_lm(
     cache_mode: Literal["prefill", "append"] = "prefill",
     logits_to_keep: int = 0,
     lora=None,
+    write_pos: torch.Tensor | None = None,
 ) -> Gemma4Output:
-    """model.py:683-709."""
+    """model.py:683-709 (``write_pos``: see forward_gemma4_text)."""
 
     hidden, cache = forward_gemma4_text(params, input_ids, position_ids, config=config,
                                         attention_mask=attention_mask, kv_cache=kv_cache, cache_mode=cache_mode,
-                                        lora=lora)
+                                        lora=lora, write_pos=write_pos)
     head_in = hidden[:, -logits_to_keep:] if logits_to_keep > 0 else hidden
     return Gemma4Output(forward_lm_head(params.embed_tokens, head_in, config.final_logit_softcapping), hidden, cache)
 

@@ -112,6 +112,60 @@ def decode_step(
                              logits_to_keep=1, lora=lora)
 
 
+class GraphedDecodeStep:
+    """One decode step (append forward + LM head, ``decode_step``'s work) captured in a HIP graph
+    and replayed once per generated token.
+
+    Inputs live in static device buffers (token ids, logical positions, the active mask) and the
+    physical slot is an int32 device counter advanced inside the graph, so a replay launches the
+    whole step (every layer's GEMMs, norms, cache append and decode attention, the LM head) with
+    one call and no host work per layer. The cache is updated in place.
+
+    Capture runs the step once eagerly first (library handles, packed weights); that warm-up
+    writes the cache slot ``cache.length``, which the first replay then overwrites.
+    """
+
+    def __init__(self, params: Gemma4TextParams, config: Gemma4TextConfig, cache: KVCache) -> None:
+        dev = cache.key_mask.device
+        B = cache.key_mask.shape[0]
+        self.params, self.config, self.cache = params, config, cache
+        self.length = int(cache.length)
+        self.tok = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.active = torch.ones(B, dtype=torch.bool, device=dev)
+        self.slot = torch.full((B,), self.length, dtype=torch.int32, device=dev)
+        self._forward()
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side), torch.cuda.graph(self.graph, stream=side):
+            self.logits = self._forward()
+            self.slot.add_(1)
+        torch.cuda.current_stream(dev).wait_stream(side)
+
+    def _forward(self) -> torch.Tensor:
+        out = forward_gemma4_lm(self.params, self.tok[:, None], self.pos[:, None], config=self.config,
+                                attention_mask=self.active[:, None], kv_cache=self.cache, cache_mode="append",
+                                logits_to_keep=1, write_pos=self.slot)
+        return out.logits[:, -1].float()
+
+    def step(self, token_ids: torch.Tensor, position_ids: torch.Tensor, active: torch.Tensor) -> torch.Tensor:
+        """Append ``token_ids`` at the next slot; returns next-token logits ``[B, V]`` f32 (a static
+        buffer, valid until the next call)."""
+
+        self.tok.copy_(token_ids)
+        self.pos.copy_(position_ids)
+        self.active.copy_(active)
+        self.graph.replay()
+        self.length += 1
+        return self.logits
+
+    @property
+    def kv_cache(self) -> KVCache:
+        return self.cache._replace(length=self.length)
+
+
 def _generator(key, device, seed: int) -> torch.Generator:
     if isinstance(key, torch.Generator):
         return key
@@ -192,6 +246,7 @@ def generate(
     eos = torch.tensor(list(sc.eos_ids), dtype=torch.int64, device=dev)
     logits = out.logits[:, -1].float()
     cache = out.kv_cache
+    graphed = GraphedDecodeStep(params, config, cache) if dev.type == "cuda" and N > 1 else None
     step = 0
     while step < N:
         sampled, logp = _sample_token(logits, gen, temperature=sc.temperature, top_k=sc.top_k, top_p=sc.top_p)
@@ -203,10 +258,14 @@ def generate(
         next_active = active & ~torch.isin(token.long(), eos) if len(sc.eos_ids) else active
         any_active = bool(next_active.any())  # the only host sync per step (while_loop's cond)
         if step + 1 < N and any_active:
-            dec = decode_step(params, config, token.to(torch.int32), (prompt_lengths + step).to(torch.int32), cache,
-                              attention_mask=active, lora=lora)
-            logits = dec.logits[:, -1].float()
-            cache = dec.kv_cache
+            pos = (prompt_lengths + step).to(torch.int32)
+            if graphed is not None:
+                logits = graphed.step(token.to(torch.int32), pos, active)
+            else:
+                dec = decode_step(params, config, token.to(torch.int32), pos, cache, attention_mask=active,
+                                  lora=lora)
+                logits = dec.logits[:, -1].float()
+                cache = dec.kv_cache
         active = next_active
         step += 1
         if not any_active:

@@ -190,6 +190,27 @@ int g4_kv_source_layers(int32_t num_layers, int32_t num_kv_shared_layers, const 
  * (negative = never written). */
 int g4_ring_slot_positions(int32_t last_written, int32_t window_capacity, int32_t* out);
 
+/*
+ * Fused elementwise glue of the decoder layer (row-major [rows, cols] arrays, cols <= 4096 for
+ * the norms; one pass each, the reference's rounding points kept). dtype = G4_DTYPE_*.
+ *
+ * g4_rms_norm: out = cast(x * (mean(x^2) + eps)^-0.5 * weight) in f32, weight NULL = no scale.
+ *   Replaces forward_rms_norm (model.py:278-285).
+ * g4_residual_norm: residual_out = cast(cast(residual + cast(rms(branch) * branch_weight)) *
+ *   scalar) (scalar: one f32 value on the device, NULL = none), then, if next_out is given, next_out =
+ *   cast(rms(residual_out) * next_weight). residual_out may alias residual. Replaces the
+ *   post-norm + residual + layer-scalar steps of forward_decoder_layer (model.py:505-554)
+ *   followed by the next pre-norm.
+ * g4_gelu_mul: out[r, c] = cast(gelu_tanh(g) * u) in f32 with gate_up[r] = [g (cols) | u (cols)].
+ *   Replaces the activation of forward_mlp (model.py:393-396).
+ */
+int g4_rms_norm(int dtype, int rows, int cols, const void* x, const void* weight, float eps, void* out,
+                void* stream);
+int g4_residual_norm(int dtype, int rows, int cols, const void* branch, const void* branch_weight,
+                     const void* residual, const float* scalar, const void* next_weight, float eps,
+                     void* residual_out, void* next_out, void* stream);
+int g4_gelu_mul(int dtype, int rows, int cols, const void* gate_up, void* out, void* stream);
+
 const char* g4_last_error(void);
 const char* g4_version(void);
 

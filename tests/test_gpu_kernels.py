@@ -288,3 +288,66 @@ def test_prefill_matches_oracle(device, dtype, D, window):
     o_ref = O.attention_core(q_ref, k, v, masks[O.SLIDING], dtype).transpose(0, 1, 3, 2, 4)
     err = np.abs(to_np(out) - o_ref).max()
     assert err <= TOL[dtype], f"max |out - oracle| = {err}"
+
+
+# --- fused decoder-layer glue ---------------------------------------------------------------------
+
+# one rounding of the activation dtype on either side (the kernels and the oracle sum the mean of
+# squares in different orders, which can move a result across a rounding boundary)
+GLUE_RTOL = {O.BF16: 2.0 ** -7, O.F32: 1e-5}
+# absolute floor for results that cancel to near zero (a residual plus a normed branch; gelu of a
+# very negative gate, where 1 + tanh cancels and tanh implementations differ in the last bits)
+GLUE_ATOL = {O.BF16: 1e-5, O.F32: 1e-6}
+
+
+@pytest.mark.parametrize("dtype", [O.BF16, O.F32])
+@pytest.mark.parametrize("cols", [2048, 200])
+def test_rms_norm_matches_oracle(device, dtype, cols):
+    """g4_rms_norm against the oracle's rms_norm (model.py:278-285); cols not a multiple of the
+    row stride too."""
+
+    rng = np.random.default_rng(cols)
+    x = _rand(rng, (5, 3, cols), dtype) * 3
+    w = O.cast(1 + 0.3 * rng.standard_normal(cols).astype(np.float32), dtype)
+    got = to_np(kernels.rms_norm(to_dev(x, dtype, device), to_dev(w, dtype, device), 1e-6))
+    ref = O.rms_norm(w, x, 1e-6, dtype)
+    np.testing.assert_allclose(got, ref, rtol=GLUE_RTOL[dtype], atol=GLUE_ATOL[dtype])
+    got = to_np(kernels.rms_norm(to_dev(x, dtype, device), None, 1e-6))  # no scale (v_norm)
+    np.testing.assert_allclose(got, O.rms_norm(None, x, 1e-6, dtype), rtol=GLUE_RTOL[dtype], atol=GLUE_ATOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [O.BF16, O.F32])
+def test_residual_norm_matches_oracle_layer_tail(device, dtype):
+    """g4_residual_norm = the oracle's post-norm, residual add, layer scalar and the next norm
+    (forward_decoder_layer, model.py:505-554), each rounded where the oracle rounds."""
+
+    rng = np.random.default_rng(5)
+    M = 2048
+    a = _rand(rng, (4, 1, M), dtype)
+    x = _rand(rng, (4, 1, M), dtype)
+    wa = O.cast(1 + 0.3 * rng.standard_normal(M).astype(np.float32), dtype)
+    wn = O.cast(1 + 0.3 * rng.standard_normal(M).astype(np.float32), dtype)
+    scalar = np.float32(0.8125)
+    xo, ho = kernels.residual_norm(to_dev(a, dtype, device), to_dev(wa, dtype, device), to_dev(x, dtype, device),
+                                   scalar=torch.tensor([scalar], device=device), next_weight=to_dev(wn, dtype, device),
+                                   eps=1e-6)
+    x_ref = O.cast(O.cast(x + O.rms_norm(wa, a, 1e-6, dtype), dtype) * scalar, dtype)
+    np.testing.assert_allclose(to_np(xo), x_ref, rtol=GLUE_RTOL[dtype], atol=GLUE_ATOL[dtype])
+    np.testing.assert_allclose(to_np(ho), O.rms_norm(wn, to_np(xo), 1e-6, dtype), rtol=GLUE_RTOL[dtype], atol=GLUE_ATOL[dtype])
+    xo2, h2 = kernels.residual_norm(to_dev(a, dtype, device), to_dev(wa, dtype, device), to_dev(x, dtype, device),
+                                    scalar=None, next_weight=None, eps=1e-6, with_next=False)
+    assert h2 is None
+    np.testing.assert_allclose(to_np(xo2), O.cast(x + O.rms_norm(wa, a, 1e-6, dtype), dtype),
+                               rtol=GLUE_RTOL[dtype], atol=GLUE_ATOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [O.BF16, O.F32])
+def test_gelu_mul_matches_oracle(device, dtype):
+    """g4_gelu_mul = the oracle's gelu_tanh(gate) * up rounded once (forward_mlp, model.py:393-396)."""
+
+    rng = np.random.default_rng(6)
+    F = 1000
+    gu = _rand(rng, (3, 2, 2 * F), dtype) * 2
+    got = to_np(kernels.gelu_mul(to_dev(gu, dtype, device)))
+    ref = O.cast(O.gelu_tanh(gu[..., :F]) * gu[..., F:], dtype)
+    np.testing.assert_allclose(got, ref, rtol=GLUE_RTOL[dtype], atol=GLUE_ATOL[dtype])

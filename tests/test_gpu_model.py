@@ -132,6 +132,51 @@ def test_bf16_prefill_and_decode_calls_match_oracle(device, seed):
         assert err <= bar, f"call {i}: max |logits - oracle| = {err} > {bar}; all: {results}"
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_graphed_decode_matches_eager_decode(device, dtype):
+    """The HIP-graph decode step (device-side slot counter, in-place key mask, replayed launch
+    sequence) computes exactly what decode_step computes: bitwise-equal logits on every step and
+    bitwise-equal caches and key masks afterwards, with a row that finishes and a left-padded row
+    (kv-shared layers, ring wrap-around)."""
+
+    ocfg = O.config_from_hf(SMALL_BF16)
+    oparams = O.init_params(ocfg, seed=3, dtype=O.BF16 if dtype == torch.bfloat16 else O.F32, std=0.03,
+                            norm_std=0.05, layer_scalar_min=0.8)
+    cfg = C.config_from_hf(SMALL_BF16)
+    params = M.params_from_numpy(oparams, cfg, dtype=dtype, device=device)
+    rng = np.random.default_rng(11)
+    ids = torch.from_numpy(rng.integers(3, 512, (3, 10)).astype(np.int32)).to(device)
+    mask = torch.ones_like(ids, dtype=torch.bool)
+    mask[1, :4] = False
+    runs = []
+    for graphed in (False, True):
+        out = SMP.prefill(params, cfg, ids, mask, max_new_tokens=12)
+        cache = out.kv_cache
+        engine = SMP.GraphedDecodeStep(params, cfg, cache) if graphed else None
+        pos0 = mask.sum(-1, dtype=torch.int32)
+        tok = out.logits[:, -1].argmax(-1).to(torch.int32)
+        logits_seen = []
+        for step in range(11):  # 10 prompt slots + 11 steps: the 8-slot ring wraps
+            active = torch.tensor([True, True, step < 5], device=device)
+            if graphed:
+                logits = engine.step(tok, pos0 + step, active).clone()
+            else:
+                dec = SMP.decode_step(params, cfg, tok, pos0 + step, cache, attention_mask=active)
+                cache = dec.kv_cache
+                logits = dec.logits[:, -1].float()
+            logits_seen.append(logits)
+            tok = logits.argmax(-1).to(torch.int32)
+        runs.append((logits_seen, engine.kv_cache if graphed else cache))
+    (la, ca), (lb, cb) = runs
+    for step, (x, y) in enumerate(zip(la, lb)):
+        assert torch.equal(x, y), f"step {step}: max diff {(x - y).abs().max().item()}"
+    assert ca.length == cb.length
+    assert torch.equal(ca.key_mask, cb.key_mask)
+    for i, (x, y) in enumerate(zip(ca.layers, cb.layers)):
+        if x is not None:
+            assert torch.equal(x.key, y.key) and torch.equal(x.value_t, y.value_t), f"layer {i}"
+
+
 @pytest.mark.parametrize("fixture_name", ["TINY_A", "TINY_B"])
 def test_reference_tiny_configs_match_oracle(device, fixture_name):
     """The reference's own test configs (PLE, kv sharing, double-wide MLP, K=V global layers),
