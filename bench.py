@@ -50,6 +50,18 @@ def algorithmic_bytes_per_step() -> int:
     return kv + q + o + new_kv
 
 
+def measured_traffic() -> int | None:
+    """HBM bytes per launch of the config-2 decode kernel from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the counter's reading on a copy of known
+    size); None when the summary is absent."""
+
+    path = ROOT / "profiles" / "decode_attention_config2_traffic.json"
+    try:
+        return int(json.loads(path.read_text())["hbm_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_info() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -410,6 +422,9 @@ def main() -> int:
     ap.add_argument("--no-e2b", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the configs[2]/[3] lines")
+    ap.add_argument("--pmc-calibration", action="store_true",
+                    help="first copy 256 MiB device-to-device once: the reference kernel whose FETCH_SIZE / "
+                         "WRITE_SIZE counters scale the decode kernel's (see profiles/)")
     ap.add_argument("--num-splits", type=int, default=0,
                     help="workgroups per (b, kv head) for decode attention (0: library default)")
     args = ap.parse_args()
@@ -418,6 +433,14 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    if args.pmc_calibration:
+        import torch
+        src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     res = bench_decode_attention(args.steps, args.warmup, args.num_splits)
     bytes_step = algorithmic_bytes_per_step()
     gbs = bytes_step / (res["ms_per_step"] * 1e-3) / 1e9
@@ -438,7 +461,7 @@ def main() -> int:
                    "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "window": W, "ring_context": CTX,
                    "bytes_per_step": bytes_step, "caches_round_robin": NCACHE, "num_splits": args.num_splits},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "eager_ms_per_step": round(res["eager_ms_per_step"], 4),
     }

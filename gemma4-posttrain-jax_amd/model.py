@@ -4,7 +4,8 @@ generation path (``init_kv_cache``, ``forward_gemma4_text``, ``forward_gemma4_lm
 Parameters use the reference's pytree (``Gemma4TextParams`` and friends, model.py:193-235) with
 torch device tensors. On first use each params object is packed once into the kernel-friendly
 layout (``PackedWeights``): q/k/v projections fused into one ``[M, (H*R + 2H)*D]`` matrix with
-query columns in (kv head, r) order, o_proj rows in the same order, gate|up fused. Per layer the
+query columns in (kv head, r) order, o_proj rows in the same order, gate|up fused; the MLP
+matrices are stored output-major (``[N, K]``), which hipBLASLt runs faster at decode batch sizes. Per layer the
 forward runs one hipBLASLt GEMM for q/k/v, the native ``g4_kv_append`` (q/k norms, RoPE, v norm,
 cache append), the native prefill or decode attention kernel, and GEMMs for o_proj and the MLP.
 The norm / residual / activation glue runs as three fused native kernels per layer with the
@@ -123,8 +124,8 @@ def params_from_numpy(p, config: Gemma4TextConfig, *, dtype=torch.bfloat16, devi
 class PackedLayer(NamedTuple):
     w_qkv: torch.Tensor  # [M, (H*R [+ H [+ H]])*D]: q in (h, r) order, then k, then v
     w_o: torch.Tensor  # [H*R*D, M] rows in (h, r, d) order
-    w_gate_up: torch.Tensor  # [M, 2F]
-    w_down: torch.Tensor  # [F, M]
+    w_gate_up_t: torch.Tensor  # [2F, M]: gate rows then up rows (output-major: a faster GEMM at small M)
+    w_down_t: torch.Tensor  # [M, F]
     heads: int
     group: int
     head_dim: int
@@ -178,8 +179,8 @@ def pack_weights(params: Gemma4TextParams, config: Gemma4TextConfig) -> PackedWe
             parts.append(a.v_proj.reshape(M, H * D))
         w_qkv = torch.cat(parts, dim=1).contiguous()
         w_o = a.o_proj.permute(1, 0, 2, 3).reshape(H * R * D, M).contiguous()
-        w_gu = torch.cat([lp.mlp.gate_proj, lp.mlp.up_proj], dim=1).contiguous()
-        layers.append(PackedLayer(w_qkv, w_o, w_gu, lp.mlp.down_proj.contiguous(), H, R, D, has_k, has_v,
+        w_gu_t = torch.cat([lp.mlp.gate_proj, lp.mlp.up_proj], dim=1).t().contiguous()
+        layers.append(PackedLayer(w_qkv, w_o, w_gu_t, lp.mlp.down_proj.t().contiguous(), H, R, D, has_k, has_v,
                                   lp.layer_scalar.float().reshape(1).contiguous()))
     dev = params.embed_tokens.device
     dt = params.embed_tokens.dtype
@@ -347,9 +348,9 @@ def forward_gemma4_text(
         # post-attention norm + residual, then the pre-feedforward norm (one pass)
         x, h = kernels.residual_norm(o, lp.post_attention_norm.weight, x, scalar=None,
                                      next_weight=lp.pre_feedforward_norm.weight, eps=eps)
-        gu = h.reshape(B * S, -1) @ pk.w_gate_up
+        gu = h.reshape(B * S, -1) @ pk.w_gate_up_t.t()
         act = kernels.gelu_mul(gu)
-        d = (act @ pk.w_down).reshape(B, S, -1)
+        d = (act @ pk.w_down_t.t()).reshape(B, S, -1)
         next_w = params.layers[i + 1].input_norm.weight if i + 1 < n_layers else params.final_norm.weight
         if lp.per_layer_input is None:
             # post-feedforward norm + residual, layer scalar, then the next layer's input norm
