@@ -1,14 +1,17 @@
 // bf16 decode attention for rows of at most 512 slots (the sliding-window ring) with
 // D / NSPLIT = 128 value dims per workgroup; included by g4_decode.hip after g4_decode_fast.h.
 //
-// Everything a workgroup reads is requested in its first instructions: q (straight into MFMA
-// operand registers), the key-mask bytes, two 32-slot K chunks per wave (registers) and the
-// workgroup's whole V^T slice, DMA'd into LDS (buffer_load ... lds, 128 KiB): wave w stages the
-// tiles of its own 16-row d-block for every chunk, each tile lane-ordered so that it is read
-// back as that lane's MFMA operand. A wave scores once its requests are queued (its K, queued
-// first, has landed by then); the softmax barriers wait only for LDS traffic (a __syncthreads()
-// fence would also wait for the DMA, which writes LDS), and a wave waits for its own DMA right
-// before its value MFMAs.
+// Requests: q (straight into MFMA operand registers), the key-mask bytes and two 32-slot K
+// chunks per wave (registers) go out first, with the first half of the workgroup's V^T slice
+// DMA'd into LDS (buffer_load ... lds); the second half (chunks 8..15) is queued after the
+// softmax's second barrier. Wave w stages the tiles of its own 16-row d-block, each tile
+// lane-ordered so that it is read back as that lane's MFMA operand. The split keeps the memory
+// queue busy through the scores and the softmax without making the barriers wait for the whole
+// V issue (a wave blocked on a full queue reaches no barrier), and the value MFMAs of the first
+// half run while the second half lands. The barriers wait only for LDS traffic (a
+// __syncthreads() fence would also wait for the DMA, which writes LDS); each wave waits for its
+// own DMA right before the value MFMAs that read it (the two halves are separate LDS arrays, so
+// the compiler's wait for the first does not include the second).
 //
 // The appended token: the wave that scores the chunk holding the slot stages the new K row in
 // LDS for itself (no barrier) and substitutes it into that chunk's K operand registers; every
@@ -37,7 +40,8 @@ __device__ __forceinline__ float wave_sum64(float v) {
 template <int D, int NSPLIT>
 __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_stage_kernel(G4DecodeArgs a) {
   static_assert(D / NSPLIT == 16 * NW, "one 16-row d-block of V^T per wave");
-  __shared__ __attribute__((aligned(1024))) unsigned char vt_tiles[NW][2 * NW][1024];  // [wave][chunk][lane*16]
+  __shared__ __attribute__((aligned(1024))) unsigned char vt_lo[NW][NW][1024];  // chunks 0..7: [wave][chunk][lane*16]
+  __shared__ __attribute__((aligned(1024))) unsigned char vt_hi[NW][NW][1024];  // chunks 8..15
   __shared__ __attribute__((aligned(16))) uint16_t nk_lds[D];
   extern __shared__ float smem[];
   const int R = a.group;
@@ -98,15 +102,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_stage_kernel(G4
   // Every byte is requested before any compute: a wave stalled on a full memory queue cannot
   // compute anyway, and its K (requested first) has landed by the time its last DMA is queued.
   const uint32_t soff = (uint32_t)(16 * db * ss) * 2u;
-  auto dma_v = [&](int c) {
+  auto dma_v = [&](unsigned char (&tiles)[NW][NW][1024], int c) {
     if (c < n_chunks) {
       const uint32_t voff = (uint32_t)(col * ss + (c << 5) + 8 * grp) * 2u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&vt_tiles[w][c][0], 16,
-                                               voff, soff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&tiles[w][c & (NW - 1)][0],
+                                               16, voff, soff, 0, 0);
     }
   };
 #pragma unroll
-  for (int c = 0; c < 2 * NW; ++c) dma_v(c);
+  for (int c = 0; c < NW; ++c) dma_v(vt_lo, c);
   __builtin_amdgcn_sched_barrier(0);
   if (owner && lane < D / 8) reinterpret_cast<u32x4*>(nk_lds)[lane] = nkv;  // read back by this wave only
   const uint64_t vb0 = __ballot(ok0 && mb0 != 0);
@@ -155,6 +159,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_stage_kernel(G4
     }
   }
   wg_barrier();  // block sums are in LDS
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int c = NW; c < 2 * NW; ++c) dma_v(vt_hi, c);
+  __builtin_amdgcn_sched_barrier(0);
   const float pu = round_bf16(1.0f / (float)a.capacity);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -177,29 +185,31 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_stage_kernel(G4
   wg_barrier();  // probabilities are in LDS
 
   // ---- values: this wave's d-block over every chunk ---------------------------------------------
-  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's V^T tiles have landed
-  if (has_new) {  // the appended slot's value into the staged tile (lanes of the slot's 8-slot group)
-    const int cn = (int)(kr.new_slot >> 5), gn = (int)(kr.new_slot & 31) >> 3, e = (int)(kr.new_slot & 7);
-    if (grp == gn) *reinterpret_cast<uint16_t*>(&vt_tiles[w][cn][16 * lane + 2 * e]) = (uint16_t)nvb;
-  }
+  // (the compiler waits for a half's DMA before the first LDS access to that half)
+  const int cn = (int)(kr.new_slot >> 5), gn = (int)(kr.new_slot & 31) >> 3, en = (int)(kr.new_slot & 7);
   const int n_chunks2 = all_masked ? (a.capacity + 31) >> 5 : n_chunks;
   floatx4 oacc = {0.f, 0.f, 0.f, 0.f}, oacc1 = {0.f, 0.f, 0.f, 0.f};  // even / odd chunks
-  {
-    u32x4 vt[2 * NW];  // every operand read before the MFMA chain (LDS latency paid once)
-    bf16x8 pp[2 * NW];
+  auto value_half = [&](unsigned char (&tiles)[NW][NW][1024], int c_first) {
+    // the appended slot's value into the staged tile (the lanes of the slot's 8-slot group)
+    if (has_new && cn >= c_first && cn < c_first + NW && grp == gn)
+      *reinterpret_cast<uint16_t*>(&tiles[w][cn - c_first][16 * lane + 2 * en]) = (uint16_t)nvb;
+    u32x4 vt[NW];  // every operand read before the MFMA chain (LDS latency paid once)
+    bf16x8 pp[NW];
 #pragma unroll
-    for (int c = 0; c < 2 * NW; ++c) {
-      if (c < n_chunks) {
-        vt[c] = *reinterpret_cast<const u32x4*>(&vt_tiles[w][c][16 * lane]);
-        pp[c] = prob_operand(sp, kStageStride, (c << 5) + 8 * grp, R, col);
+    for (int i = 0; i < NW; ++i) {
+      if (c_first + i < n_chunks) {
+        vt[i] = *reinterpret_cast<const u32x4*>(&tiles[w][i][16 * lane]);
+        pp[i] = prob_operand(sp, kStageStride, ((c_first + i) << 5) + 8 * grp, R, col);
       }
     }
 #pragma unroll
-    for (int c = 0; c < 2 * NW; c += 2) {
-      if (c < n_chunks) oacc = mfma16x16x32(as_bf16x8(vt[c]), pp[c], oacc);
-      if (c + 1 < n_chunks) oacc1 = mfma16x16x32(as_bf16x8(vt[c + 1]), pp[c + 1], oacc1);
+    for (int i = 0; i < NW; i += 2) {
+      if (c_first + i < n_chunks) oacc = mfma16x16x32(as_bf16x8(vt[i]), pp[i], oacc);
+      if (c_first + i + 1 < n_chunks) oacc1 = mfma16x16x32(as_bf16x8(vt[i + 1]), pp[i + 1], oacc1);
     }
-  }
+  };
+  value_half(vt_lo, 0);
+  value_half(vt_hi, NW);
   oacc += oacc1;
   for (int c = n_chunks; c < n_chunks2; ++c) {  // fully masked linear row: slots never scanned
     const uint32_t voff = (uint32_t)(col * ss + (c << 5) + 8 * grp) * 2u;
