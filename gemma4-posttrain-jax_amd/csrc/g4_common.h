@@ -75,6 +75,10 @@ __host__ __device__ __forceinline__ int64_t floor_mod(int64_t a, int64_t m) {
   return r < 0 ? r + m : r;
 }
 
+// Workgroup barrier after this wave's LDS writes complete, without waiting for vector memory:
+// __syncthreads()'s release fence would also wait for in-flight LDS DMA (buffer_load ... lds).
+__device__ __forceinline__ void wg_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // 16-byte global load / store of 8 bf16 values (raw bits).
 __device__ __forceinline__ u32x4 load16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 

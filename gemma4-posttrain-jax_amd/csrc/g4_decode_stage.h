@@ -26,11 +26,6 @@ constexpr int kStageSlots = 2 * NW * 32;  // slots per row handled here (16 chun
 // 0..3 on different banks for the 16-byte MFMA-operand accesses (lane (grp, col) -> row col).
 constexpr int kStageStride = kStageSlots + 32;
 
-__device__ __forceinline__ void wg_barrier() {
-  // LDS writes of this wave complete, then the workgroup barrier; no wait for vector memory
-  __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 __device__ __forceinline__ float wave_sum64(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -1,0 +1,228 @@
+// bf16 prefill attention with the key / value chunks staged through LDS (head dims 128, 256);
+// included by g4_prefill.hip after prefill_bf16_kernel.
+//
+// A workgroup of 8 waves owns 8 * 16/R consecutive query positions of one (b, kv head); each
+// wave owns 16 query rows (16/R positions x R heads), the MFMA column block. The key range is
+// walked in 32-key chunks: every chunk's K and V^T are DMA'd into LDS once per workgroup
+// (buffer_load ... lds, double-buffered, each wave issuing an equal share) as lane-ordered
+// MFMA operand tiles, and all 8 waves read them from there — against 1 KiB of global loads per
+// MFMA when each wave loads its own operands. The key-mask bytes of the row are staged in LDS
+// once, so a chunk's validity bits are one LDS byte per lane and a ballot.
+//
+// Same two passes as prefill_bf16_kernel (the reference rounds probabilities after the full-row
+// softmax): pass 1 streams K for each row's max and sum, pass 2 streams K and V and forms exact
+// bf16 probabilities exp(s - m) * (1/l) for the value product. Workgroups are launched heaviest
+// (latest positions, longest causal key range) first.
+
+constexpr int kPfWaves = 8;
+constexpr int kPfMaxSeq = 32768;  // key-mask bytes staged in LDS
+
+template <int D>
+struct PfShape {
+  static constexpr int KT = 2 * (D / 32);  // K operand tiles per chunk: (bb, s)
+  static constexpr int VT = D / 16;        // V^T operand tiles per chunk: d-blocks
+  static constexpr int KT_W = KT / kPfWaves;
+  static constexpr int VT_W = VT / kPfWaves;
+  static_assert(KT % kPfWaves == 0 && VT % kPfWaves == 0, "tiles split evenly over the waves");
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int D>
+__global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4PrefillArgs a) {
+  using S_ = PfShape<D>;
+  constexpr int KS = D / 32;
+  __shared__ __attribute__((aligned(1024))) unsigned char kb0[S_::KT][1024];
+  __shared__ __attribute__((aligned(1024))) unsigned char vb0[S_::VT][1024];
+  __shared__ __attribute__((aligned(1024))) unsigned char kb1[S_::KT][1024];
+  __shared__ __attribute__((aligned(1024))) unsigned char vb1[S_::VT][1024];
+  extern __shared__ float smem[];
+  uint8_t* km_lds = reinterpret_cast<uint8_t*>(smem);  // key_mask[b, 0:S]
+
+  const int R = a.group;
+  const int ppw = 16 / R;              // positions per wave
+  const int ppb = kPfWaves * ppw;      // positions per workgroup
+  const int S = a.seq, H = a.kv_heads;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int nblk = (S + ppb - 1) / ppb;
+  const int blk = nblk - 1 - (int)blockIdx.x;  // heaviest first
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const int p0 = blk * ppb;                       // first position of the workgroup
+  const int my_pos = p0 + w * ppw + col / R;      // this lane's query row (column col)
+  const int r = col - (col / R) * R;
+  const bool row_ok = my_pos < S;
+  const int64_t bh = (int64_t)b * H + h;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(reinterpret_cast<const uint16_t*>(a.k) + bh * a.k_stride * D,
+                                              (uint32_t)a.k_stride * D * 2u);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(reinterpret_cast<const uint16_t*>(a.vt) + bh * D * a.k_stride,
+                                              (uint32_t)a.k_stride * D * 2u);
+
+  // q operands (registers) and the row's key-mask bytes (LDS)
+  bf16x8 qop[KS];
+  {
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + ((((int64_t)b * S + my_pos) * H + h) * R + r) * D;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (row_ok) v = load16(qrow + 32 * s + 8 * grp);
+      qop[s] = as_bf16x8(v);
+    }
+  }
+  const uint8_t* km = a.key_mask + (int64_t)b * a.key_mask_stride;
+  for (int i = tid; i < S; i += blockDim.x) km_lds[i] = km[i];
+
+  const int pos_last = min(p0 + ppb - 1, S - 1);
+  const int kmin = a.window > 0 ? max(0, p0 - a.window + 1) : 0;
+  const int c_begin = kmin >> 5, c_end = pos_last >> 5;
+
+  // this wave's share of a chunk's operand tiles into LDS
+  auto issue = [&](int c, unsigned char (&kt)[S_::KT][1024], unsigned char (&vt)[S_::VT][1024], bool with_v) {
+    const int c0 = c << 5;
+#pragma unroll
+    for (int i = 0; i < S_::KT_W; ++i) {
+      const int t = w * S_::KT_W + i, bb = t / KS, s = t - bb * KS;
+      const int key = c0 + 8 * (col >> 2) + 4 * bb + (col & 3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)&kt[t][0], 16,
+                                               (uint32_t)(key * D + 32 * s + 8 * grp) * 2u, 0, 0, 0);
+    }
+    if (with_v) {
+#pragma unroll
+      for (int i = 0; i < S_::VT_W; ++i) {
+        const int t = w * S_::VT_W + i;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rv, (__attribute__((address_space(3))) void*)&vt[t][0], 16,
+            (uint32_t)((int64_t)(16 * t + col) * a.k_stride + c0 + 8 * grp) * 2u, 0, 0, 0);
+      }
+    }
+  };
+  // validity bits of the chunk's 32 keys for this lane's row: bit e <-> key c0 + 8*grp + e
+  auto valid_bits = [&](int c) -> uint32_t {
+    const int c0 = c << 5;
+    const int key = c0 + (lane & 31);
+    const uint64_t mb = __ballot(key < S && km_lds[key < S ? key : 0] != 0);
+    uint32_t bits = (uint32_t)(mb >> (8 * grp)) & 0xffu;
+    // causal: key <= my_pos; window: key > my_pos - window
+    const int lo = c0 + 8 * grp;
+    const int hi_ok = my_pos - lo;  // keys lo + e valid for e <= hi_ok
+    bits &= hi_ok >= 7 ? 0xffu : (hi_ok < 0 ? 0u : (0xffu >> (7 - hi_ok)));
+    if (a.window > 0) {
+      const int lo_ok = my_pos - a.window + 1 - lo;  // need e >= lo_ok
+      bits &= lo_ok <= 0 ? 0xffu : (lo_ok > 7 ? 0u : (0xffu << lo_ok) & 0xffu);
+    }
+    return row_ok ? bits : 0u;
+  };
+  auto qk = [&](unsigned char (&kt)[S_::KT][1024], floatx4 (&acc)[2]) {
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+      floatx4 x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        x = mfma16x16x32(as_bf16x8(*reinterpret_cast<const u32x4*>(&kt[bb * KS + s][16 * lane])), qop[s], x);
+      acc[bb] = x;
+    }
+  };
+
+  // ---- pass 1: row max and sum --------------------------------------------------------------------
+  float m = kBf16Min, l = 0.f;
+  auto stats = [&](int c, unsigned char (&kt)[S_::KT][1024]) {
+    floatx4 acc[2];
+    qk(kt, acc);
+    const uint32_t bits = valid_bits(c);
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 4 * bb + j;
+        const float s = ((bits >> e) & 1u) ? round_bf16(acc[bb][j]) : kBf16Min;
+        if (s > m) {
+          l = l * __expf(m - s) + 1.f;
+          m = s;
+        } else {
+          l += __expf(s - m);
+        }
+      }
+    }
+  };
+  __syncthreads();  // key-mask bytes in LDS (no DMA in flight yet)
+  issue(c_begin, kb0, vb0, false);
+  for (int c = c_begin; c <= c_end; c += 2) {
+    wait_vmcnt<0>();
+    wg_barrier();
+    if (c + 1 <= c_end) issue(c + 1, kb1, vb1, false);
+    stats(c, kb0);
+    if (c + 1 > c_end) break;
+    wait_vmcnt<0>();
+    wg_barrier();
+    if (c + 2 <= c_end) issue(c + 2, kb0, vb0, false);
+    stats(c + 1, kb1);
+  }
+#pragma unroll
+  for (int msk = 16; msk <= 32; msk <<= 1) {
+    const float m2 = __shfl_xor(m, msk, 64);
+    const float l2 = __shfl_xor(l, msk, 64);
+    const float mm = fmaxf(m, m2);
+    l = l * __expf(m - mm) + l2 * __expf(m2 - mm);
+    m = mm;
+  }
+  // A row with no valid key is the reference's softmax over S equal fills: 1/S on every key.
+  const bool row_masked = row_ok && m == kBf16Min;
+  const bool any_masked = __syncthreads_or(row_masked);  // (also: every wave is done with pass 1's LDS)
+  const float p_uniform = round_bf16(1.0f / (float)S);
+  const float rl = 1.0f / l;
+  const int c2_begin = any_masked ? 0 : c_begin;
+  const int c2_end = any_masked ? (S - 1) >> 5 : c_end;
+
+  // ---- pass 2: exact probabilities and O^T = V^T P^T -------------------------------------------------
+  floatx4 oacc[S_::VT];
+#pragma unroll
+  for (int i = 0; i < S_::VT; ++i) oacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  auto values = [&](int c, unsigned char (&kt)[S_::KT][1024], unsigned char (&vt)[S_::VT][1024]) {
+    floatx4 acc[2];
+    qk(kt, acc);
+    const uint32_t bits = valid_bits(c);
+    const int kb = (c << 5) + 8 * grp;
+    uint32_t pw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 4 * bb + j;
+        float p;
+        if (row_masked) p = kb + e < S ? p_uniform : 0.f;
+        else p = ((bits >> e) & 1u) ? __expf(round_bf16(acc[bb][j]) - m) * rl : 0.f;
+        pw[e >> 1] |= f32_to_bf16_bits(p) << (16 * (e & 1));
+      }
+    }
+    const bf16x8 pop = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
+#pragma unroll
+    for (int i = 0; i < S_::VT; ++i)
+      oacc[i] = mfma16x16x32(as_bf16x8(*reinterpret_cast<const u32x4*>(&vt[i][16 * lane])), pop, oacc[i]);
+  };
+  issue(c2_begin, kb0, vb0, true);
+  for (int c = c2_begin; c <= c2_end; c += 2) {
+    wait_vmcnt<0>();
+    wg_barrier();
+    if (c + 1 <= c2_end) issue(c + 1, kb1, vb1, true);
+    values(c, kb0, vb0);
+    if (c + 1 > c2_end) break;
+    wait_vmcnt<0>();
+    wg_barrier();
+    if (c + 2 <= c2_end) issue(c + 2, kb0, vb0, true);
+    values(c + 1, kb1, vb1);
+  }
+
+  if (row_ok) {
+    uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((((int64_t)b * S + my_pos) * H + h) * R + r) * D;
+#pragma unroll
+    for (int i = 0; i < S_::VT; ++i) {
+      const uint32_t w0 = f32_to_bf16_bits(oacc[i][0]) | (f32_to_bf16_bits(oacc[i][1]) << 16);
+      const uint32_t w1 = f32_to_bf16_bits(oacc[i][2]) | (f32_to_bf16_bits(oacc[i][3]) << 16);
+      *reinterpret_cast<uint2*>(orow + 16 * i + 4 * grp) = make_uint2(w0, w1);
+    }
+  }
+}

@@ -263,10 +263,11 @@ def test_decode_is_deterministic(device):
 # --- prefill attention ----------------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("dtype,D", [(O.BF16, 256), (O.BF16, 64), (O.F32, 64)])
+@pytest.mark.parametrize("dtype,D", [(O.BF16, 256), (O.BF16, 128), (O.BF16, 64), (O.F32, 64)])
 @pytest.mark.parametrize("window", [0, 48])
 def test_prefill_matches_oracle(device, dtype, D, window):
-    """Causal + sliding-window prefill with left padding (fully masked pad queries)."""
+    """Causal + sliding-window prefill with left padding (fully masked pad queries); S not a
+    multiple of the 32-key chunk nor of a workgroup's 32 positions."""
 
     rng = np.random.default_rng(D + window)
     B, S, H, R = 2, 150, 2, 4
@@ -288,6 +289,31 @@ def test_prefill_matches_oracle(device, dtype, D, window):
     o_ref = O.attention_core(q_ref, k, v, masks[O.SLIDING], dtype).transpose(0, 1, 3, 2, 4)
     err = np.abs(to_np(out) - o_ref).max()
     assert err <= TOL[dtype], f"max |out - oracle| = {err}"
+
+
+@pytest.mark.parametrize("R", [1, 2, 8])
+def test_prefill_group_sizes(device, R):
+    """Other GQA group sizes (16/R positions per wave) on the LDS-staged bf16 kernel, a longer row
+    (several workgroups of positions, heaviest launched first) and a sliding window."""
+
+    rng = np.random.default_rng(30 + R)
+    B, S, H, D, window = 1, 300, 2, 128, 100
+    q = _rand(rng, (B, S, H, R, D), O.BF16)
+    k = _rand(rng, (B, S, H, D), O.BF16)
+    v = _rand(rng, (B, S, H, D), O.BF16)
+    key_mask = np.ones((B, S), bool)
+    key_mask[0, 120:125] = False
+    Sp = (S + 63) // 64 * 64
+    kd = torch.zeros((B, H, Sp, D), dtype=torch.bfloat16, device=device)
+    vtd = torch.zeros((B, H, D, Sp), dtype=torch.bfloat16, device=device)
+    kd[:, :, :S] = to_dev(k, O.BF16, device).permute(0, 2, 1, 3)
+    vtd[:, :, :, :S] = to_dev(v, O.BF16, device).permute(0, 2, 3, 1)
+    out = kernels.prefill_attention(to_dev(q, O.BF16, device), kd, vtd, torch.from_numpy(key_mask).to(device),
+                                    window=window)
+    masks = O.make_qk_masks(key_mask, window, 0, S)
+    o_ref = O.attention_core(q.transpose(0, 1, 3, 2, 4), k, v, masks[O.SLIDING], O.BF16).transpose(0, 1, 3, 2, 4)
+    err = np.abs(to_np(out) - o_ref).max()
+    assert err <= TOL[O.BF16], f"max |out - oracle| = {err}"
 
 
 # --- fused decoder-layer glue ---------------------------------------------------------------------
