@@ -200,20 +200,33 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(G4PrefillArgs a, int t
 
 #include "g4_prefill_lds.h"
 
+constexpr int kLdsBytes = 160 * 1024;  // gfx950 LDS per workgroup
+
+// Largest key-mask row the LDS-staged kernel can hold next to its static tile buffers (bytes;
+// 0 when the limit cannot be raised). Queried and set once per instantiation.
 template <int D>
-int launch_prefill_lds(const G4PrefillArgs& a, hipStream_t st) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)prefill_bf16_lds_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            kPfMaxSeq) != hipSuccess)
-      return fail(G4_ERR_LAUNCH, "g4_prefill_attention: cannot raise the LDS limit");
-    attr_set = true;
+int prefill_lds_max_seq() {
+  static int max_seq = -1;
+  if (max_seq < 0) {
+    hipFuncAttributes attr;
+    max_seq = 0;
+    if (hipFuncGetAttributes(&attr, (const void*)prefill_bf16_lds_kernel<D>) == hipSuccess) {
+      const int room = (kLdsBytes - (int)attr.sharedSizeBytes) / 16 * 16;
+      const int cap = room < kPfMaxSeq ? room : kPfMaxSeq;
+      if (cap > 0 && hipFuncSetAttribute((const void*)prefill_bf16_lds_kernel<D>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, cap) == hipSuccess)
+        max_seq = cap;
+    }
   }
+  return max_seq;
+}
+
+template <int D>
+void launch_prefill_lds(const G4PrefillArgs& a, hipStream_t st) {
   const int ppb = kPfWaves * (16 / a.group);
   const dim3 grid((unsigned)((a.seq + ppb - 1) / ppb), a.kv_heads, a.batch);
   const size_t lds = ((size_t)a.seq + 15) / 16 * 16;
   hipLaunchKernelGGL(prefill_bf16_lds_kernel<D>, grid, dim3(kPfWaves * 64), lds, st, a);
-  return G4_OK;
 }
 
 }  // namespace
@@ -236,9 +249,13 @@ extern "C" int g4_prefill_attention(const G4PrefillArgs* args, void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (a.dtype == G4_DTYPE_BF16) {
     if (16 % a.group) return fail(G4_ERR_UNSUPPORTED, "g4_prefill_attention: bf16 needs group dividing 16");
-    if ((a.head_dim == 128 || a.head_dim == 256) && a.seq <= kPfMaxSeq) {  // K/V chunks staged through LDS
-      const int rc = a.head_dim == 256 ? launch_prefill_lds<256>(a, st) : launch_prefill_lds<128>(a, st);
-      if (rc != G4_OK) return rc;
+    // head dims 128/256: K/V chunks staged through LDS, when the row's key mask fits next to them
+    if (a.head_dim == 256 && a.seq <= prefill_lds_max_seq<256>()) {
+      launch_prefill_lds<256>(a, st);
+      return check_launch("g4_prefill_attention");
+    }
+    if (a.head_dim == 128 && a.seq <= prefill_lds_max_seq<128>()) {
+      launch_prefill_lds<128>(a, st);
       return check_launch("g4_prefill_attention");
     }
     const int rows_per_block = kPrefillWaves * (16 / a.group);

@@ -4,7 +4,8 @@
 // A workgroup of 8 waves owns 8 * 16/R consecutive query positions of one (b, kv head); each
 // wave owns 16 query rows (16/R positions x R heads), the MFMA column block. The key range is
 // walked in 32-key chunks: every chunk's K and V^T are DMA'd into LDS once per workgroup
-// (buffer_load ... lds, double-buffered, each wave issuing an equal share) as lane-ordered
+// (buffer_load ... lds through a ring of 4 buffers, three chunks in flight ahead of the one being
+// computed, each wave issuing an equal share) as lane-ordered
 // MFMA operand tiles, and all 8 waves read them from there — against 1 KiB of global loads per
 // MFMA when each wave loads its own operands. The key-mask bytes of the row are staged in LDS
 // once, so a chunk's validity bits are one LDS byte per lane and a ballot.
@@ -35,10 +36,16 @@ template <int D>
 __global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4PrefillArgs a) {
   using S_ = PfShape<D>;
   constexpr int KS = D / 32;
+  // four buffers as separate arrays, so the compiler's wait before reading one does not include
+  // the DMA still in flight into the others
   __shared__ __attribute__((aligned(1024))) unsigned char kb0[S_::KT][1024];
   __shared__ __attribute__((aligned(1024))) unsigned char vb0[S_::VT][1024];
   __shared__ __attribute__((aligned(1024))) unsigned char kb1[S_::KT][1024];
   __shared__ __attribute__((aligned(1024))) unsigned char vb1[S_::VT][1024];
+  __shared__ __attribute__((aligned(1024))) unsigned char kb2[S_::KT][1024];
+  __shared__ __attribute__((aligned(1024))) unsigned char vb2[S_::VT][1024];
+  __shared__ __attribute__((aligned(1024))) unsigned char kb3[S_::KT][1024];
+  __shared__ __attribute__((aligned(1024))) unsigned char vb3[S_::VT][1024];
   extern __shared__ float smem[];
   uint8_t* km_lds = reinterpret_cast<uint8_t*>(smem);  // key_mask[b, 0:S]
 
@@ -116,7 +123,9 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4Prefi
     }
     return row_ok ? bits : 0u;
   };
+  // (the scheduling barriers bound how many operand tiles are read ahead into registers)
   auto qk = [&](unsigned char (&kt)[S_::KT][1024], floatx4 (&acc)[2]) {
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb) {
       floatx4 x = {0.f, 0.f, 0.f, 0.f};
@@ -124,6 +133,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4Prefi
       for (int s = 0; s < KS; ++s)
         x = mfma16x16x32(as_bf16x8(*reinterpret_cast<const u32x4*>(&kt[bb * KS + s][16 * lane])), qop[s], x);
       acc[bb] = x;
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -148,18 +158,48 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4Prefi
       }
     }
   };
+  // One pipeline step: wait for this wave's DMA of chunk c (chunks c+1, c+2 may stay in flight),
+  // barrier (every wave's share of chunk c has landed, and every wave is done with chunk c-1, whose
+  // buffer the DMA of chunk c+3 reuses), queue chunk c+3, compute chunk c.
+  auto wait_chunk = [&](int c, int c_last, bool with_v) {
+    const int ahead = min(c_last - c, 2);  // chunks queued after c
+    if (with_v) {
+      constexpr int n = S_::KT_W + S_::VT_W;
+      if (ahead >= 2) wait_vmcnt<2 * n>();
+      else if (ahead == 1) wait_vmcnt<n>();
+      else wait_vmcnt<0>();
+    } else {
+      constexpr int n = S_::KT_W;
+      if (ahead >= 2) wait_vmcnt<2 * n>();
+      else if (ahead == 1) wait_vmcnt<n>();
+      else wait_vmcnt<0>();
+    }
+    wg_barrier();
+  };
   __syncthreads();  // key-mask bytes in LDS (no DMA in flight yet)
   issue(c_begin, kb0, vb0, false);
-  for (int c = c_begin; c <= c_end; c += 2) {
-    wait_vmcnt<0>();
-    wg_barrier();
-    if (c + 1 <= c_end) issue(c + 1, kb1, vb1, false);
+  if (c_begin + 1 <= c_end) issue(c_begin + 1, kb1, vb1, false);
+  if (c_begin + 2 <= c_end) issue(c_begin + 2, kb2, vb2, false);
+  // (guarded steps rather than early exits: the accumulators then merge at one point per step)
+  for (int c = c_begin; c <= c_end; c += 4) {
+    wait_chunk(c, c_end, false);
+    if (c + 3 <= c_end) issue(c + 3, kb3, vb3, false);
     stats(c, kb0);
-    if (c + 1 > c_end) break;
-    wait_vmcnt<0>();
-    wg_barrier();
-    if (c + 2 <= c_end) issue(c + 2, kb0, vb0, false);
-    stats(c + 1, kb1);
+    if (c + 1 <= c_end) {
+      wait_chunk(c + 1, c_end, false);
+      if (c + 4 <= c_end) issue(c + 4, kb0, vb0, false);
+      stats(c + 1, kb1);
+    }
+    if (c + 2 <= c_end) {
+      wait_chunk(c + 2, c_end, false);
+      if (c + 5 <= c_end) issue(c + 5, kb1, vb1, false);
+      stats(c + 2, kb2);
+    }
+    if (c + 3 <= c_end) {
+      wait_chunk(c + 3, c_end, false);
+      if (c + 6 <= c_end) issue(c + 6, kb2, vb2, false);
+      stats(c + 3, kb3);
+    }
   }
 #pragma unroll
   for (int msk = 16; msk <= 32; msk <<= 1) {
@@ -200,20 +240,36 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4Prefi
     }
     const bf16x8 pop = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
 #pragma unroll
-    for (int i = 0; i < S_::VT; ++i)
-      oacc[i] = mfma16x16x32(as_bf16x8(*reinterpret_cast<const u32x4*>(&vt[i][16 * lane])), pop, oacc[i]);
+    for (int i0 = 0; i0 < S_::VT; i0 += 8) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = i0; i < i0 + 8 && i < S_::VT; ++i)
+        oacc[i] = mfma16x16x32(as_bf16x8(*reinterpret_cast<const u32x4*>(&vt[i][16 * lane])), pop, oacc[i]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   };
   issue(c2_begin, kb0, vb0, true);
-  for (int c = c2_begin; c <= c2_end; c += 2) {
-    wait_vmcnt<0>();
-    wg_barrier();
-    if (c + 1 <= c2_end) issue(c + 1, kb1, vb1, true);
+  if (c2_begin + 1 <= c2_end) issue(c2_begin + 1, kb1, vb1, true);
+  if (c2_begin + 2 <= c2_end) issue(c2_begin + 2, kb2, vb2, true);
+  for (int c = c2_begin; c <= c2_end; c += 4) {
+    wait_chunk(c, c2_end, true);
+    if (c + 3 <= c2_end) issue(c + 3, kb3, vb3, true);
     values(c, kb0, vb0);
-    if (c + 1 > c2_end) break;
-    wait_vmcnt<0>();
-    wg_barrier();
-    if (c + 2 <= c2_end) issue(c + 2, kb0, vb0, true);
-    values(c + 1, kb1, vb1);
+    if (c + 1 <= c2_end) {
+      wait_chunk(c + 1, c2_end, true);
+      if (c + 4 <= c2_end) issue(c + 4, kb0, vb0, true);
+      values(c + 1, kb1, vb1);
+    }
+    if (c + 2 <= c2_end) {
+      wait_chunk(c + 2, c2_end, true);
+      if (c + 5 <= c2_end) issue(c + 5, kb1, vb1, true);
+      values(c + 2, kb2, vb2);
+    }
+    if (c + 3 <= c2_end) {
+      wait_chunk(c + 3, c2_end, true);
+      if (c + 6 <= c2_end) issue(c + 6, kb2, vb2, true);
+      values(c + 3, kb3, vb3);
+    }
   }
 
   if (row_ok) {
