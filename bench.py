@@ -335,6 +335,7 @@ def bench_e2b_decode(steps: int, warmup: int, batch: int = 256, prompt: int = 25
     import torch
 
     from gemma4_posttrain_jax_amd import config as C
+    from gemma4_posttrain_jax_amd import kernels
     from gemma4_posttrain_jax_amd import sampler as SMP
 
     dev = torch.device("cuda:0")
@@ -349,22 +350,22 @@ def bench_e2b_decode(steps: int, warmup: int, batch: int = 256, prompt: int = 25
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
     cache = out.kv_cache
-    logits = out.logits[:, -1].float()
-    gen = torch.Generator(device=dev).manual_seed(2)
     lengths = torch.full((batch,), prompt, dtype=torch.int32, device=dev)
     active = torch.ones(batch, dtype=torch.bool, device=dev)
-    engine = SMP.GraphedDecodeStep(params, cfg, cache)  # what generate() replays per token
+    # what generate() does per token at T=1: one graph replay = forward of all layers + LM head +
+    # fused soft-cap / log-softmax / Gumbel-max draw
+    tok, _ = kernels.sample_tokens(out.logits[:, -1], softcap=None, temperature=1.0, seed=2, step=0)
+    engine = SMP.GraphedDecodeStep(params, cfg, cache, temperature=1.0, seed=2)
     torch.cuda.synchronize()
     for i in range(warmup):
-        tok, _ = SMP._sample_token(logits, gen, temperature=1.0, top_k=0, top_p=1.0)
-        logits = engine.step(tok, lengths + i, active)
+        tok, logp = engine.step_sample(tok, lengths + i, active)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(warmup, warmup + steps):  # sample + decode, as generate()'s loop body
-        tok, _ = SMP._sample_token(logits, gen, temperature=1.0, top_k=0, top_p=1.0)
-        logits = engine.step(tok, lengths + i, active)
+    for i in range(warmup, warmup + steps):
+        tok, logp = engine.step_sample(tok, lengths + i, active)
     torch.cuda.synchronize()
     s = (time.perf_counter() - t0) / steps
+    logits = out.logits[:, -1]
     return {"decode_s_per_step": s, "decode_tok_s": batch / s, "prefill_s": prefill_s, "params": params, "cfg": cfg,
             "cache": engine.kv_cache, "logits": logits}
 

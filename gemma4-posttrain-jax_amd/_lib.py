@@ -58,6 +58,14 @@ class G4PrefillArgs(ctypes.Structure):
 
 
 # Every symbol include/g4_rollout.h declares, with its ctypes prototype.
+class G4SampleArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32), ("batch", c_int32), ("vocab", c_int32), ("logits", c_void_p), ("row_stride", c_int64),
+        ("softcap", c_float), ("temperature", c_float), ("seed", ctypes.c_uint64), ("step", c_void_p),
+        ("step_scalar", c_int32), ("token_out", c_void_p), ("logp_out", c_void_p),
+    ]
+
+
 PROTOTYPES = {
     "g4_kv_append": (c_int32, [POINTER(G4AppendArgs), c_void_p]),
     "g4_decode_workspace_size": (c_size_t, [POINTER(G4DecodeArgs)]),
@@ -65,6 +73,7 @@ PROTOTYPES = {
     "g4_prefill_attention": (c_int32, [POINTER(G4PrefillArgs), c_void_p]),
     "g4_kv_source_layers": (c_int32, [c_int32, c_int32, POINTER(c_int32), POINTER(c_int32)]),
     "g4_ring_slot_positions": (c_int32, [c_int32, c_int32, POINTER(c_int32)]),
+    "g4_sample_tokens": (c_int32, [POINTER(G4SampleArgs), c_void_p]),
     "g4_rms_norm": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_float, c_void_p, c_void_p]),
     "g4_residual_norm": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_float, c_void_p, c_void_p, c_void_p]),

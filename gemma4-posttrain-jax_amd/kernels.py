@@ -285,3 +285,35 @@ def gelu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     _lib.check(_lib.lib().g4_gelu_mul(_code(gate_up), rows, cols2 // 2, _ptr(gate_up), _ptr(out), _stream()),
                "g4_gelu_mul")
     return out
+
+
+# --- sampling ------------------------------------------------------------------------------------------
+
+
+def sample_tokens(logits: torch.Tensor, *, softcap: float | None, temperature: float, seed: int,
+                  step: int | torch.Tensor, token_out: torch.Tensor | None = None,
+                  logp_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """g4_sample_tokens on ``[B, V]`` logits (bf16 or f32, rows may be strided): soft-cap (None/0 =
+    already capped), then greedy (temperature <= 0) or Gumbel-max sampling with Philox noise keyed by
+    ``seed`` and ``step`` (an int, or an int32 device counter read by the kernel). Returns
+    ``(token int32 [B], logp f32 [B])`` with logp the full-vocab log-softmax at the token."""
+
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [B, V] with unit inner stride")
+    B, V = logits.shape
+    dev = logits.device
+    token_out = torch.empty(B, dtype=torch.int32, device=dev) if token_out is None else token_out
+    logp_out = torch.empty(B, dtype=torch.float32, device=dev) if logp_out is None else logp_out
+    if isinstance(step, torch.Tensor):
+        if step.dtype != torch.int32 or step.numel() != 1:
+            raise ValueError("step must be a one-element int32 device tensor")
+        step_ptr, step_scalar = _ptr(step), 0
+    else:
+        step_ptr, step_scalar = None, int(step)
+    a = _lib.G4SampleArgs(
+        dtype=_code(logits), batch=B, vocab=V, logits=_ptr(logits), row_stride=logits.stride(0),
+        softcap=float(softcap or 0.0), temperature=float(temperature), seed=int(seed) & (2 ** 64 - 1),
+        step=step_ptr, step_scalar=step_scalar, token_out=_ptr(token_out), logp_out=_ptr(logp_out),
+    )
+    _lib.check(_lib.lib().g4_sample_tokens(ctypes.byref(a), _stream()), "g4_sample_tokens")
+    return token_out, logp_out

@@ -15,9 +15,10 @@ from typing import Any, NamedTuple, Protocol
 
 import torch
 
+from . import kernels
 from .config import Gemma4TextConfig
 from .kvcache import KVCache, init_kv_cache
-from .model import Gemma4Output, Gemma4TextParams, forward_gemma4_lm
+from .model import Gemma4Output, Gemma4TextParams, forward_gemma4_lm, forward_gemma4_text
 
 
 class SamplerConfig(NamedTuple):
@@ -121,11 +122,17 @@ class GraphedDecodeStep:
     whole step (every layer's GEMMs, norms, cache append and decode attention, the LM head) with
     one call and no host work per layer. The cache is updated in place.
 
+    With ``temperature`` given, the graph ends in the fused sampler (``g4_sample_tokens``: the LM
+    head's soft-capping, the full-vocab log-softmax and a greedy / Gumbel-max draw, Philox noise
+    keyed by ``seed`` and a device step counter starting at ``first_rng_step``) and ``step_sample``
+    returns the next token and its log-probability; otherwise ``step`` returns the logits.
+
     Capture runs the step once eagerly first (library handles, packed weights); that warm-up
     writes the cache slot ``cache.length``, which the first replay then overwrites.
     """
 
-    def __init__(self, params: Gemma4TextParams, config: Gemma4TextConfig, cache: KVCache) -> None:
+    def __init__(self, params: Gemma4TextParams, config: Gemma4TextConfig, cache: KVCache, *,
+                 temperature: float | None = None, seed: int = 0, first_rng_step: int = 1) -> None:
         dev = cache.key_mask.device
         B = cache.key_mask.shape[0]
         self.params, self.config, self.cache = params, config, cache
@@ -134,6 +141,10 @@ class GraphedDecodeStep:
         self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
         self.active = torch.ones(B, dtype=torch.bool, device=dev)
         self.slot = torch.full((B,), self.length, dtype=torch.int32, device=dev)
+        self.temperature, self.seed = temperature, seed
+        self.rng_step = torch.full((1,), first_rng_step, dtype=torch.int32, device=dev)
+        self.token_out = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.logp_out = torch.zeros(B, dtype=torch.float32, device=dev)
         self._forward()
         torch.cuda.synchronize(dev)
         self.graph = torch.cuda.CUDAGraph()
@@ -142,28 +153,68 @@ class GraphedDecodeStep:
         with torch.cuda.stream(side), torch.cuda.graph(self.graph, stream=side):
             self.logits = self._forward()
             self.slot.add_(1)
+            if temperature is not None:
+                self.rng_step.add_(1)
         torch.cuda.current_stream(dev).wait_stream(side)
 
-    def _forward(self) -> torch.Tensor:
-        out = forward_gemma4_lm(self.params, self.tok[:, None], self.pos[:, None], config=self.config,
-                                attention_mask=self.active[:, None], kv_cache=self.cache, cache_mode="append",
-                                logits_to_keep=1, write_pos=self.slot)
-        return out.logits[:, -1].float()
+    def _forward(self) -> torch.Tensor | None:
+        if self.temperature is None:
+            out = forward_gemma4_lm(self.params, self.tok[:, None], self.pos[:, None], config=self.config,
+                                    attention_mask=self.active[:, None], kv_cache=self.cache, cache_mode="append",
+                                    logits_to_keep=1, write_pos=self.slot)
+            return out.logits[:, -1].float()
+        hidden, _ = forward_gemma4_text(self.params, self.tok[:, None], self.pos[:, None], config=self.config,
+                                        attention_mask=self.active[:, None], kv_cache=self.cache,
+                                        cache_mode="append", write_pos=self.slot)
+        raw = hidden[:, -1] @ self.params.embed_tokens.t()  # [B, V] before the soft-cap
+        kernels.sample_tokens(raw, softcap=self.config.final_logit_softcapping, temperature=self.temperature,
+                              seed=self.seed, step=self.rng_step, token_out=self.token_out, logp_out=self.logp_out)
+        return None
 
-    def step(self, token_ids: torch.Tensor, position_ids: torch.Tensor, active: torch.Tensor) -> torch.Tensor:
-        """Append ``token_ids`` at the next slot; returns next-token logits ``[B, V]`` f32 (a static
-        buffer, valid until the next call)."""
-
+    def _replay(self, token_ids: torch.Tensor, position_ids: torch.Tensor, active: torch.Tensor) -> None:
         self.tok.copy_(token_ids)
         self.pos.copy_(position_ids)
         self.active.copy_(active)
         self.graph.replay()
         self.length += 1
+
+    def step(self, token_ids: torch.Tensor, position_ids: torch.Tensor, active: torch.Tensor) -> torch.Tensor:
+        """Append ``token_ids`` at the next slot; returns next-token logits ``[B, V]`` f32 (a static
+        buffer, valid until the next call)."""
+
+        if self.temperature is not None:
+            raise RuntimeError("this step was captured with fused sampling: use step_sample")
+        self._replay(token_ids, position_ids, active)
         return self.logits
+
+    def step_sample(self, token_ids: torch.Tensor, position_ids: torch.Tensor,
+                    active: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Append ``token_ids`` and draw the next token: ``(token int32 [B], logp f32 [B])`` (static
+        buffers, valid until the next call)."""
+
+        if self.temperature is None:
+            raise RuntimeError("this step was captured without sampling: use step")
+        self._replay(token_ids, position_ids, active)
+        return self.token_out, self.logp_out
 
     @property
     def kv_cache(self) -> KVCache:
         return self.cache._replace(length=self.length)
+
+
+def _fused_sampling(sc: SamplerConfig, vocab: int, device: torch.device) -> bool:
+    """The native sampler covers the RL configuration: no top-k / top-p truncation."""
+
+    return device.type == "cuda" and (sc.top_k <= 0 or sc.top_k >= vocab) and sc.top_p >= 1.0
+
+
+def _seed_from_key(key, seed: int) -> int:
+    """64-bit Philox key of the native sampler: the integer ``key`` (or ``seed`` when None), or a
+    draw from a ``torch.Generator`` key (one host read)."""
+
+    if isinstance(key, torch.Generator):
+        return int(torch.randint(0, 2 ** 62, (1,), generator=key, device=key.device).item())
+    return int(seed if key is None else key)
 
 
 def _generator(key, device, seed: int) -> torch.Generator:
@@ -246,10 +297,20 @@ def generate(
     eos = torch.tensor(list(sc.eos_ids), dtype=torch.int64, device=dev)
     logits = out.logits[:, -1].float()
     cache = out.kv_cache
-    graphed = GraphedDecodeStep(params, config, cache) if dev.type == "cuda" and N > 1 else None
+    fused = _fused_sampling(sc, config.vocab_size, dev)
+    if fused:  # first token from the prefill logits (already soft-capped), then one graph per step
+        seed = _seed_from_key(key, sc.seed)
+        nxt = kernels.sample_tokens(out.logits[:, -1], softcap=None, temperature=sc.temperature, seed=seed, step=0)
+        graphed = GraphedDecodeStep(params, config, cache, temperature=sc.temperature, seed=seed,
+                                    first_rng_step=1) if N > 1 else None
+    else:
+        graphed = GraphedDecodeStep(params, config, cache) if dev.type == "cuda" and N > 1 else None
     step = 0
     while step < N:
-        sampled, logp = _sample_token(logits, gen, temperature=sc.temperature, top_k=sc.top_k, top_p=sc.top_p)
+        if fused:
+            sampled, logp = nxt
+        else:
+            sampled, logp = _sample_token(logits, gen, temperature=sc.temperature, top_k=sc.top_k, top_p=sc.top_p)
         token = torch.where(active, sampled, torch.full_like(sampled, config.pad_token_id)).to(prompt_ids.dtype)
         logp = torch.where(active, logp, torch.zeros_like(logp))
         completion_ids[:, step] = token
@@ -259,7 +320,9 @@ def generate(
         any_active = bool(next_active.any())  # the only host sync per step (while_loop's cond)
         if step + 1 < N and any_active:
             pos = (prompt_lengths + step).to(torch.int32)
-            if graphed is not None:
+            if fused:
+                nxt = graphed.step_sample(token.to(torch.int32), pos, active)
+            elif graphed is not None:
                 logits = graphed.step(token.to(torch.int32), pos, active)
             else:
                 dec = decode_step(params, config, token.to(torch.int32), pos, cache, attention_mask=active,

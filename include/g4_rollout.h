@@ -191,6 +191,31 @@ int g4_kv_source_layers(int32_t num_layers, int32_t num_kv_shared_layers, const 
 int g4_ring_slot_positions(int32_t last_written, int32_t window_capacity, int32_t* out);
 
 /*
+ * Next-token sampling fused with the LM head's soft-capping. Replaces forward_lm_head's capping
+ * (model.py:676-680) + _sample_token (sampler.py:145-183) for top_k = 0, top_p = 1: per row
+ * x = cast(tanh(l / softcap) * softcap) (softcap 0 = l as given), token = argmax(x) when
+ * temperature <= 0, else argmax(x / temperature + g) with Gumbel noise g = -log(-log(u)), u from
+ * Philox4x32-10 keyed by seed with counter (column / 4, row, step, 0); logp = x[token] -
+ * logsumexp(x) (the unmodified full-vocab policy). Ties go to the lowest column.
+ */
+typedef struct G4SampleArgs {
+  int32_t dtype;            /* of logits */
+  int32_t batch;
+  int32_t vocab;
+  const void* logits;       /* [batch, row_stride] */
+  int64_t row_stride;       /* elements, >= vocab */
+  float softcap;            /* 0 = none */
+  float temperature;        /* <= 0 = greedy */
+  uint64_t seed;
+  const int32_t* step;      /* device int32 counter, or NULL to use step_scalar */
+  int32_t step_scalar;
+  int32_t* token_out;       /* device [batch] */
+  float* logp_out;          /* device [batch] */
+} G4SampleArgs;
+
+int g4_sample_tokens(const G4SampleArgs* args, void* stream);
+
+/*
  * Fused elementwise glue of the decoder layer (row-major [rows, cols] arrays, cols <= 4096 for
  * the norms; one pass each, the reference's rounding points kept). dtype = G4_DTYPE_*.
  *

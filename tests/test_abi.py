@@ -44,7 +44,7 @@ def test_ctypes_structs_match_the_compiled_header(tmp_path):
     if cc is None:
         pytest.skip("no C compiler")
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
-    for st in (_lib.G4AppendArgs, _lib.G4DecodeArgs, _lib.G4PrefillArgs):
+    for st in (_lib.G4AppendArgs, _lib.G4DecodeArgs, _lib.G4PrefillArgs, _lib.G4SampleArgs):
         lines.append(f'printf("{st.__name__} size %zu\\n", sizeof({st.__name__}));')
         for f, _ in st._fields_:
             lines.append(f'printf("{st.__name__} {f} %zu\\n", offsetof({st.__name__}, {f}));')
