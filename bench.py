@@ -354,8 +354,9 @@ def bench_e2b_decode(steps: int, warmup: int, batch: int = 256, prompt: int = 25
     active = torch.ones(batch, dtype=torch.bool, device=dev)
     # what generate() does per token at T=1: one graph replay = forward of all layers + LM head +
     # fused soft-cap / log-softmax / Gumbel-max draw
-    tok, _ = kernels.sample_tokens(out.logits[:, -1], softcap=None, temperature=1.0, seed=2, step=0)
-    engine = SMP.GraphedDecodeStep(params, cfg, cache, temperature=1.0, seed=2)
+    key = SMP.key_tensor(2, dev)  # PRNGKey(2), split once per step on the device
+    tok, _ = kernels.sample_tokens(out.logits[:, -1], softcap=None, temperature=1.0, key=key)
+    engine = SMP.GraphedDecodeStep(params, cfg, cache, temperature=1.0, key=key)
     torch.cuda.synchronize()
     for i in range(warmup):
         tok, logp = engine.step_sample(tok, lengths + i, active)

@@ -23,6 +23,9 @@ G4_APPEND_ROPE_K = 4
 G4_APPEND_NORM_Q = 8
 G4_APPEND_ROPE_Q = 16
 G4_DECODE_SPLIT_KEYS = -1
+G4_ERR_INVALID = -1
+G4_ERR_UNSUPPORTED = -2
+G4_ERR_LAUNCH = -3
 G4_ERR_WORKSPACE = -4
 
 
@@ -60,9 +63,10 @@ class G4PrefillArgs(ctypes.Structure):
 # Every symbol include/g4_rollout.h declares, with its ctypes prototype.
 class G4SampleArgs(ctypes.Structure):
     _fields_ = [
-        ("dtype", c_int32), ("batch", c_int32), ("vocab", c_int32), ("logits", c_void_p), ("row_stride", c_int64),
-        ("softcap", c_float), ("temperature", c_float), ("seed", ctypes.c_uint64), ("step", c_void_p),
-        ("step_scalar", c_int32), ("token_out", c_void_p), ("logp_out", c_void_p),
+        ("dtype", c_int32), ("batch", c_int32), ("vocab", c_int32), ("proposal_width", c_int32),
+        ("logits", c_void_p), ("row_stride", c_int64), ("softcap", c_float), ("temperature", c_float),
+        ("split_key", c_int32), ("key", c_void_p), ("proposal", c_void_p), ("proposal_index", c_void_p), ("token_out", c_void_p),
+        ("logp_out", c_void_p),
     ]
 
 

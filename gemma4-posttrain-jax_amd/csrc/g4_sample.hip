@@ -1,16 +1,12 @@
 // Fused next-token sampling over the LM head's output (g4_sample_tokens).
 //
-// Replaces forward_lm_head's soft-capping (model.py:676-680) followed by _sample_token
-// (sampler.py:145-183) for the configurations RL rollouts use (no top-k, no top-p): per row,
-//   x      = cast(tanh(l / cap) * cap)            (the capped logits in the activation dtype)
-//   token  = argmax(x)                            (temperature <= 0)
-//          = argmax(x / T + gumbel)               (otherwise; Gumbel-max = a categorical draw)
-//   logp   = x[token] - logsumexp(x)              (full-vocab log-softmax of the unmodified policy)
-// in one pass over the row: running max and rescaled sum for the log-softmax, running argmax.
-// The Gumbel noise -log(-log(u)) comes from Philox4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel
-// random numbers: as easy as 1, 2, 3", SC 2011) keyed by the 64-bit seed, counter = (column/4,
-// row, step, 0): reproducible for a fixed seed and independent of the launch shape. `step` may
-// live on the device (advanced by the caller between replays of a captured graph).
+// One step of generate's loop body (sampler.py:265-270): split the generation key, then
+// _sample_token (sampler.py:145-183) on the soft-capped logits (model.py:676-680), in one pass
+// over each row: running max / rescaled sum for the full-vocab log-softmax and a running
+// argmax of the perturbed scores. The random stream is JAX's: threefry2x32 (Salmon, Moraes, Dror,
+// Shaw, "Parallel random numbers: as easy as 1, 2, 3", SC 2011; 20 rounds, the Skein rotation
+// constants), key splitting and random bits in JAX's partitionable layout, uniform floats from
+// the top 23 bits, Gumbel noise -log(-log(u)) and categorical = argmax(scores + noise).
 #include "g4_common.h"
 #include "g4_internal.h"
 
@@ -18,51 +14,57 @@ namespace g4 {
 namespace {
 
 constexpr int kSampleThreads = 1024;
+constexpr float kF32Tiny = 1.17549435e-38f;  // smallest normal float: uniform's minval
 
-struct Philox4 {
-  uint32_t v[4];
-};
+__device__ __forceinline__ uint32_t rotl32(uint32_t x, int r) { return (x << r) | (x >> (32 - r)); }
 
-// Philox4x32 with 10 rounds (Salmon et al. 2011, section 5): multipliers 0xD2511F53 /
-// 0xCD9E8D57, Weyl key increments 0x9E3779B9 / 0xBB67AE85.
-__device__ __forceinline__ Philox4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
-                                                 uint32_t k1) {
+// threefry2x32 with 20 rounds: key schedule (k0, k1, k0 ^ k1 ^ 0x1BD11BDA) injected after every
+// four rounds together with the injection count; rotations 13 15 26 6 / 17 29 16 24.
+__device__ __forceinline__ void threefry2x32(uint32_t k0, uint32_t k1, uint32_t& x0, uint32_t& x1) {
+  const uint32_t ks[3] = {k0, k1, k0 ^ k1 ^ 0x1BD11BDAu};
+  constexpr int rot[2][4] = {{13, 15, 26, 6}, {17, 29, 16, 24}};
+  x0 += ks[0];
+  x1 += ks[1];
 #pragma unroll
-  for (int i = 0; i < 10; ++i) {
-    const uint32_t lo0 = 0xD2511F53u * c0, hi0 = __umulhi(0xD2511F53u, c0);
-    const uint32_t lo1 = 0xCD9E8D57u * c2, hi1 = __umulhi(0xCD9E8D57u, c2);
-    const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
-    c0 = n0;
-    c1 = lo1;
-    c2 = n2;
-    c3 = lo0;
-    k0 += 0x9E3779B9u;
-    k1 += 0xBB67AE85u;
+  for (int i = 0; i < 5; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x0 += x1;
+      x1 = rotl32(x1, rot[i & 1][j]) ^ x0;
+    }
+    x0 += ks[(i + 1) % 3];
+    x1 += ks[(i + 2) % 3] + (uint32_t)(i + 1);
   }
-  return Philox4{{c0, c1, c2, c3}};
 }
 
-// uniform in the open interval (0, 1): 24 random bits, centred in their bucket
-__device__ __forceinline__ float uniform01(uint32_t bits) { return ((float)(bits >> 8) + 0.5f) * (1.0f / 16777216.0f); }
+// Gumbel noise of element `flat` (row-major index into the [batch, K] draw) under sample_key:
+// bits = xor of threefry2x32(key, (flat >> 32, flat & 0xffffffff)); u = float in [1, 2) from the
+// top 23 bits minus 1, floored at the smallest normal; g = -log(-log(u)).
+__device__ __forceinline__ float gumbel(uint32_t k0, uint32_t k1, uint64_t flat) {
+  uint32_t x0 = (uint32_t)(flat >> 32), x1 = (uint32_t)flat;
+  threefry2x32(k0, k1, x0, x1);
+  const uint32_t bits = x0 ^ x1;
+  const float f = __uint_as_float((bits >> 9) | 0x3F800000u) - 1.0f;
+  const float u = fmaxf(kF32Tiny, f + kF32Tiny);
+  return -logf(-logf(u));
+}
 
 struct RowState {
-  float m, s;       // running max of x and sum of exp(x - m)
-  float best;       // best score so far
-  int idx;          // its column
-  float best_x;     // x at that column
+  float m, s;  // running max of x and sum of exp(x - m)
+  float best;  // best score so far
+  int idx;     // its column
 };
 
 __device__ __forceinline__ void merge(RowState& a, const RowState& b) {
   if (b.m > a.m) {
-    a.s = a.s * __expf(a.m - b.m) + b.s;
+    a.s = a.s * expf(a.m - b.m) + b.s;
     a.m = b.m;
   } else if (b.m > kF32Min) {
-    a.s += b.s * __expf(b.m - a.m);
+    a.s += b.s * expf(b.m - a.m);
   }
-  if (b.best > a.best || (b.best == a.best && b.idx < a.idx)) {  // ties: the first column (torch/jax argmax)
+  if (b.best > a.best || (b.best == a.best && b.idx < a.idx)) {  // ties: the first column (argmax)
     a.best = b.best;
     a.idx = b.idx;
-    a.best_x = b.best_x;
   }
 }
 
@@ -72,45 +74,63 @@ __device__ __forceinline__ RowState shfl_state(const RowState& x, int mask) {
   y.s = __shfl_xor(x.s, mask, 64);
   y.best = __shfl_xor(x.best, mask, 64);
   y.idx = __shfl_xor(x.idx, mask, 64);
-  y.best_x = __shfl_xor(x.best_x, mask, 64);
   return y;
 }
 
 template <bool BF16>
-__global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) {
+__device__ __forceinline__ float capped(const typename Elem<BF16>::T* row, int col, float cap) {
   using E = Elem<BF16>;
-  using T = typename E::T;
+  float x = E::load(row, col);
+  if (cap > 0.f) x = E::round(tanhf(x / cap) * cap);  // the reference divides by the cap
+  return x;
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) {
+  using T = typename Elem<BF16>::T;
   __shared__ RowState red[kSampleThreads / 64];
   const int row = blockIdx.x;
   const T* lrow = reinterpret_cast<const T*>(a.logits) + (int64_t)row * a.row_stride;
-  const uint32_t step = a.step ? (uint32_t)*a.step : (uint32_t)a.step_scalar;
-  const uint32_t k0 = (uint32_t)a.seed, k1 = (uint32_t)(a.seed >> 32);
   const bool greedy = !(a.temperature > 0.f);
-  const float cap = a.softcap;  // the reference divides by the cap (no reciprocal)
-  RowState st = {kF32Min, 0.f, -INFINITY, 0x7fffffff, 0.f};
-  // each thread takes 4 consecutive columns per visit (one Philox block)
-  for (int c4 = threadIdx.x; c4 * 4 < a.vocab; c4 += blockDim.x) {
-    Philox4 rnd = {{0u, 0u, 0u, 0u}};
-    if (!greedy) rnd = philox4x32_10((uint32_t)c4, (uint32_t)row, step, 0u, k0, k1);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int colx = 4 * c4 + e;
-      if (colx >= a.vocab) break;
-      float x = E::load(lrow, colx);
-      if (cap > 0.f) x = E::round(tanhf(x / cap) * cap);
-      // log-softmax statistics
-      if (x > st.m) {
-        st.s = st.s * __expf(st.m - x) + 1.f;
-        st.m = x;
-      } else {
-        st.s += __expf(x - st.m);
-      }
+  const bool proposal = !greedy && a.proposal != nullptr;
+  uint32_t k0 = 0u, k1 = 0u;
+  if (!greedy) {
+    if (a.split_key) {  // sample_key = split(key)[1] = threefry2x32(key, (0, 1))
+      k0 = 0u;
+      k1 = 1u;
+      threefry2x32(a.key[0], a.key[1], k0, k1);
+    } else {
+      k0 = a.key[0];
+      k1 = a.key[1];
+    }
+  }
+  RowState st = {kF32Min, 0.f, -INFINITY, 0x7fffffff};
+  // columns c = tid + 1024 n: each thread visits its columns in increasing order, so a strict
+  // comparison keeps the first of equal scores
+  for (int c = threadIdx.x; c < a.vocab; c += kSampleThreads) {
+    const float x = capped<BF16>(lrow, c, a.softcap);
+    if (x > st.m) {
+      st.s = st.s * expf(st.m - x) + 1.f;
+      st.m = x;
+    } else {
+      st.s += expf(x - st.m);
+    }
+    if (!proposal) {
       float score = x;
-      if (!greedy) score = x / a.temperature - __logf(-__logf(uniform01(rnd.v[e])));
-      if (score > st.best) {  // columns visited in increasing order per thread: first wins ties
+      if (!greedy) score = x / a.temperature + gumbel(k0, k1, (uint64_t)row * (uint64_t)a.vocab + (uint64_t)c);
+      if (score > st.best) {
         st.best = score;
-        st.idx = colx;
-        st.best_x = x;
+        st.idx = c;
+      }
+    }
+  }
+  if (proposal) {
+    const float* prow = a.proposal + (int64_t)row * a.proposal_width;
+    for (int j = threadIdx.x; j < a.proposal_width; j += kSampleThreads) {
+      const float score = prow[j] + gumbel(k0, k1, (uint64_t)row * (uint64_t)a.proposal_width + (uint64_t)j);
+      if (score > st.best) {
+        st.best = score;
+        st.idx = j;
       }
     }
   }
@@ -121,9 +141,25 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) 
   __syncthreads();
   if (threadIdx.x == 0) {
     RowState t = red[0];
-    for (int i = 1; i < (int)(blockDim.x >> 6); ++i) merge(t, red[i]);
-    a.token_out[row] = t.idx;
-    a.logp_out[row] = t.best_x - (t.m + __logf(t.s));
+    for (int i = 1; i < kSampleThreads / 64; ++i) merge(t, red[i]);
+    // a row of NaN scores keeps no best: clamp so that every read below stays in bounds
+    const int width = proposal ? a.proposal_width : a.vocab;
+    int token = t.idx < 0 ? 0 : (t.idx >= width ? width - 1 : t.idx);
+    if (proposal && a.proposal_index) token = a.proposal_index[(int64_t)row * a.proposal_width + token];
+    token = token < 0 ? 0 : (token >= a.vocab ? a.vocab - 1 : token);
+    const float x = capped<BF16>(lrow, token, a.softcap);
+    a.token_out[row] = token;
+    a.logp_out[row] = (x - t.m) - logf(t.s);
+  }
+}
+
+// key <- split(key)[0] = threefry2x32(key, (0, 0)), after every row has read the old key
+__global__ void advance_key_kernel(uint32_t* key) {
+  if (threadIdx.x == 0) {
+    uint32_t x0 = 0u, x1 = 0u;
+    threefry2x32(key[0], key[1], x0, x1);
+    key[0] = x0;
+    key[1] = x1;
   }
 }
 
@@ -141,10 +177,26 @@ extern "C" int g4_sample_tokens(const G4SampleArgs* args, void* stream) {
                 (long long)a.row_stride);
   if (!a.logits || !a.token_out || !a.logp_out) return fail(G4_ERR_INVALID, "g4_sample_tokens: NULL pointer");
   if (!(a.softcap >= 0.f)) return fail(G4_ERR_INVALID, "g4_sample_tokens: softcap must be >= 0");
+  const bool greedy = !(a.temperature > 0.f);
+  if (!greedy && !a.key) return fail(G4_ERR_INVALID, "g4_sample_tokens: sampling needs the device key");
+  if (a.split_key != 0 && a.split_key != 1) return fail(G4_ERR_INVALID, "g4_sample_tokens: split_key %d", a.split_key);
+  if (a.proposal) {
+    if (a.proposal_width <= 0) return fail(G4_ERR_INVALID, "g4_sample_tokens: proposal_width %d", a.proposal_width);
+    if (!a.proposal_index && a.proposal_width > a.vocab)
+      return fail(G4_ERR_INVALID, "g4_sample_tokens: proposal_width %d > vocab %d without proposal_index",
+                  a.proposal_width, a.vocab);
+  } else if (a.proposal_width != 0 || a.proposal_index) {
+    return fail(G4_ERR_INVALID, "g4_sample_tokens: proposal_width / proposal_index without a proposal");
+  }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (a.dtype == G4_DTYPE_BF16)
     hipLaunchKernelGGL(sample_kernel<true>, dim3(a.batch), dim3(kSampleThreads), 0, st, a);
   else
     hipLaunchKernelGGL(sample_kernel<false>, dim3(a.batch), dim3(kSampleThreads), 0, st, a);
-  return check_launch("g4_sample_tokens");
+  if (int rc = check_launch("g4_sample_tokens")) return rc;
+  if (a.key && a.split_key) {
+    hipLaunchKernelGGL(advance_key_kernel, dim3(1), dim3(64), 0, st, a.key);
+    return check_launch("g4_sample_tokens (key split)");
+  }
+  return G4_OK;
 }

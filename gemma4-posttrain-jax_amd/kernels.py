@@ -290,30 +290,45 @@ def gelu_mul(gate_up: torch.Tensor) -> torch.Tensor:
 # --- sampling ------------------------------------------------------------------------------------------
 
 
-def sample_tokens(logits: torch.Tensor, *, softcap: float | None, temperature: float, seed: int,
-                  step: int | torch.Tensor, token_out: torch.Tensor | None = None,
+def sample_tokens(logits: torch.Tensor, *, softcap: float | None, temperature: float, key: torch.Tensor | None,
+                  split_key: bool = True, proposal: torch.Tensor | None = None, proposal_index: torch.Tensor | None = None,
+                  token_out: torch.Tensor | None = None,
                   logp_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """g4_sample_tokens on ``[B, V]`` logits (bf16 or f32, rows may be strided): soft-cap (None/0 =
-    already capped), then greedy (temperature <= 0) or Gumbel-max sampling with Philox noise keyed by
-    ``seed`` and ``step`` (an int, or an int32 device counter read by the kernel). Returns
-    ``(token int32 [B], logp f32 [B])`` with logp the full-vocab log-softmax at the token."""
+    already capped), then greedy (temperature <= 0) or a categorical draw over ``logits /
+    temperature``, or over ``proposal [B, K]`` f32 (truncated scores; column j is vocab id
+    ``proposal_index[:, j]``). ``key`` is a 2-word int32 device tensor: with ``split_key`` the
+    generation loop's key, split (the draw uses the second half and ``key`` is advanced in place to
+    the first), otherwise the sample key itself, left unchanged. Returns ``(token int32 [B], logp f32 [B])`` with logp the
+    full-vocab log-softmax of the capped logits at the token."""
 
     if logits.dim() != 2 or logits.stride(1) != 1:
         raise ValueError("logits must be [B, V] with unit inner stride")
     B, V = logits.shape
     dev = logits.device
+    if key is not None and (key.dtype != torch.int32 or key.numel() != 2 or not key.is_contiguous()
+                            or key.device != dev):
+        raise ValueError("key must be a contiguous 2-element int32 tensor on the logits' device")
+    K = 0
+    if proposal is not None:
+        if proposal.dtype != torch.float32 or proposal.dim() != 2 or proposal.shape[0] != B:
+            raise ValueError("proposal must be [B, K] float32")
+        proposal = proposal.contiguous()
+        K = proposal.shape[1]
+        if proposal_index is not None:
+            if proposal_index.shape != proposal.shape:
+                raise ValueError("proposal_index must match the proposal's shape")
+            proposal_index = proposal_index.to(torch.int32).contiguous()
+    elif proposal_index is not None:
+        raise ValueError("proposal_index needs a proposal")
     token_out = torch.empty(B, dtype=torch.int32, device=dev) if token_out is None else token_out
     logp_out = torch.empty(B, dtype=torch.float32, device=dev) if logp_out is None else logp_out
-    if isinstance(step, torch.Tensor):
-        if step.dtype != torch.int32 or step.numel() != 1:
-            raise ValueError("step must be a one-element int32 device tensor")
-        step_ptr, step_scalar = _ptr(step), 0
-    else:
-        step_ptr, step_scalar = None, int(step)
     a = _lib.G4SampleArgs(
-        dtype=_code(logits), batch=B, vocab=V, logits=_ptr(logits), row_stride=logits.stride(0),
-        softcap=float(softcap or 0.0), temperature=float(temperature), seed=int(seed) & (2 ** 64 - 1),
-        step=step_ptr, step_scalar=step_scalar, token_out=_ptr(token_out), logp_out=_ptr(logp_out),
+        dtype=_code(logits), batch=B, vocab=V, proposal_width=K, logits=_ptr(logits), row_stride=logits.stride(0),
+        softcap=float(softcap or 0.0), temperature=float(temperature), split_key=int(bool(split_key)), key=_ptr(key) if key is not None else None,
+        proposal=_ptr(proposal) if proposal is not None else None,
+        proposal_index=_ptr(proposal_index) if proposal_index is not None else None,
+        token_out=_ptr(token_out), logp_out=_ptr(logp_out),
     )
     _lib.check(_lib.lib().g4_sample_tokens(ctypes.byref(a), _stream()), "g4_sample_tokens")
     return token_out, logp_out

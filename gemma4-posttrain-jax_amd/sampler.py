@@ -3,9 +3,11 @@ gemma4_posttrain_jax/sampler.py on one MI355X.
 
 Same functions, arguments and semantics as the reference (sampler.py:30-352): left-padded prompts
 with logical RoPE positions, cache capacity ``P + N``, full-vocab f32 log-probabilities of the
-unmodified policy, EOS masking with early exit. Differences: arrays are torch device tensors, and
-``key`` is an integer seed or a ``torch.Generator`` (the categorical draw is Gumbel-max over
-Philox noise rather than JAX's threefry stream). ``mesh`` must be None (one GPU).
+unmodified policy, EOS masking with early exit, and JAX's random stream: ``PRNGKey(seed)``, one
+``split`` per step, ``categorical`` = Gumbel-max over threefry2x32 noise in JAX's partitionable
+layout (drawn on the device by g4_sample_tokens). Differences: arrays are torch device tensors, a
+key is an int seed or the two uint32 words of ``jax.random.key_data``, and ``mesh`` must be None
+(one GPU).
 """
 
 from __future__ import annotations
@@ -123,16 +125,17 @@ class GraphedDecodeStep:
     one call and no host work per layer. The cache is updated in place.
 
     With ``temperature`` given, the graph ends in the fused sampler (``g4_sample_tokens``: the LM
-    head's soft-capping, the full-vocab log-softmax and a greedy / Gumbel-max draw, Philox noise
-    keyed by ``seed`` and a device step counter starting at ``first_rng_step``) and ``step_sample``
-    returns the next token and its log-probability; otherwise ``step`` returns the logits.
+    head's soft-capping, the full-vocab log-softmax, the split of ``key`` (a 2-word int32 device
+    tensor, advanced in place by every replay) and a greedy / categorical draw) and
+    ``step_sample`` returns the next token and its log-probability; otherwise ``step`` returns the
+    logits.
 
     Capture runs the step once eagerly first (library handles, packed weights); that warm-up
     writes the cache slot ``cache.length``, which the first replay then overwrites.
     """
 
     def __init__(self, params: Gemma4TextParams, config: Gemma4TextConfig, cache: KVCache, *,
-                 temperature: float | None = None, seed: int = 0, first_rng_step: int = 1) -> None:
+                 temperature: float | None = None, key: torch.Tensor | None = None) -> None:
         dev = cache.key_mask.device
         B = cache.key_mask.shape[0]
         self.params, self.config, self.cache = params, config, cache
@@ -141,11 +144,15 @@ class GraphedDecodeStep:
         self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
         self.active = torch.ones(B, dtype=torch.bool, device=dev)
         self.slot = torch.full((B,), self.length, dtype=torch.int32, device=dev)
-        self.temperature, self.seed = temperature, seed
-        self.rng_step = torch.full((1,), first_rng_step, dtype=torch.int32, device=dev)
+        if temperature is not None and temperature > 0 and key is None:
+            raise ValueError("sampling in the graph needs the device key")
+        self.temperature, self.key = temperature, key
         self.token_out = torch.zeros(B, dtype=torch.int32, device=dev)
         self.logp_out = torch.zeros(B, dtype=torch.float32, device=dev)
-        self._forward()
+        saved_key = None if key is None else key.clone()
+        self._forward()  # eager warm-up: its key split is undone below
+        if key is not None:
+            key.copy_(saved_key)
         torch.cuda.synchronize(dev)
         self.graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream(dev)
@@ -153,8 +160,6 @@ class GraphedDecodeStep:
         with torch.cuda.stream(side), torch.cuda.graph(self.graph, stream=side):
             self.logits = self._forward()
             self.slot.add_(1)
-            if temperature is not None:
-                self.rng_step.add_(1)
         torch.cuda.current_stream(dev).wait_stream(side)
 
     def _forward(self) -> torch.Tensor | None:
@@ -168,7 +173,7 @@ class GraphedDecodeStep:
                                         cache_mode="append", write_pos=self.slot)
         raw = hidden[:, -1] @ self.params.embed_tokens.t()  # [B, V] before the soft-cap
         kernels.sample_tokens(raw, softcap=self.config.final_logit_softcapping, temperature=self.temperature,
-                              seed=self.seed, step=self.rng_step, token_out=self.token_out, logp_out=self.logp_out)
+                              key=self.key, split_key=True, token_out=self.token_out, logp_out=self.logp_out)
         return None
 
     def _replay(self, token_ids: torch.Tensor, position_ids: torch.Tensor, active: torch.Tensor) -> None:
@@ -202,58 +207,70 @@ class GraphedDecodeStep:
         return self.cache._replace(length=self.length)
 
 
-def _fused_sampling(sc: SamplerConfig, vocab: int, device: torch.device) -> bool:
-    """The native sampler covers the RL configuration: no top-k / top-p truncation."""
+def _fused_sampling(sc: SamplerConfig, vocab: int) -> bool:
+    """No top-k / top-p truncation (the RL configuration): the draw runs over the whole row, so it
+    can end the captured decode graph."""
 
-    return device.type == "cuda" and (sc.top_k <= 0 or sc.top_k >= vocab) and sc.top_p >= 1.0
-
-
-def _seed_from_key(key, seed: int) -> int:
-    """64-bit Philox key of the native sampler: the integer ``key`` (or ``seed`` when None), or a
-    draw from a ``torch.Generator`` key (one host read)."""
-
-    if isinstance(key, torch.Generator):
-        return int(torch.randint(0, 2 ** 62, (1,), generator=key, device=key.device).item())
-    return int(seed if key is None else key)
+    return (sc.top_k <= 0 or sc.top_k >= vocab) and sc.top_p >= 1.0
 
 
-def _generator(key, device, seed: int) -> torch.Generator:
-    if isinstance(key, torch.Generator):
-        return key
-    g = torch.Generator(device=device)
-    g.manual_seed(int(seed if key is None else key))
-    return g
+def _key_words(key, seed: int) -> list[int]:
+    """The two uint32 words of a JAX threefry key: ``PRNGKey(seed)`` for None, ``PRNGKey(key)`` for
+    an int, else ``key`` itself (``jax.random.key_data``: a sequence, array or tensor of 2 words)."""
+
+    if key is None:
+        key = seed
+    if isinstance(key, int):
+        return [(key >> 32) & 0xFFFFFFFF, key & 0xFFFFFFFF]
+    words = [int(w) & 0xFFFFFFFF for w in (key.tolist() if hasattr(key, "tolist") else key)]
+    if len(words) != 2:
+        raise ValueError(f"a key has two uint32 words, got {len(words)}")
+    return words
 
 
-def _sample_token(logits: torch.Tensor, generator: torch.Generator, *, temperature: float, top_k: int,
+def key_tensor(key, device: torch.device, seed: int = 0) -> torch.Tensor:
+    """A fresh 2-word int32 device tensor holding the key (the native sampler's key format)."""
+
+    return torch.tensor(_key_words(key, seed), dtype=torch.int64).to(torch.int32).to(device)
+
+
+def _proposal(logits32: torch.Tensor, temperature: float, top_k: int,
+              top_p: float) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+    """sampler.py:162-178: the truncated proposal the categorical draw runs over, as ``(scores
+    [B, K] f32, vocab ids [B, K])``, or ``(None, None)`` without truncation. Ties keep the lower
+    vocab id first (lax.top_k and the stable descending argsort do)."""
+
+    V = logits32.shape[-1]
+    if not (0 < top_k < V) and top_p >= 1:
+        return None, None
+    scores, indices = torch.sort(logits32 / temperature, dim=-1, descending=True, stable=True)
+    if 0 < top_k < V:
+        scores, indices = scores[:, :top_k], indices[:, :top_k]
+    if top_p < 1:
+        w = torch.exp(scores - scores.max(dim=-1, keepdim=True).values)
+        probs = w / w.sum(dim=-1, keepdim=True)
+        previous = torch.cumsum(probs, dim=-1) - probs
+        keep = (previous < top_p) | (torch.arange(scores.shape[-1], device=scores.device)[None, :] == 0)
+        scores = torch.where(keep, scores, torch.full_like(scores, -math.inf))
+    return scores.contiguous(), indices.to(torch.int32).contiguous()
+
+
+def _draw(logits: torch.Tensor, key: torch.Tensor, *, temperature: float, top_k: int, top_p: float,
+          split_key: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    logits32 = logits.float().contiguous()
+    proposal, index = (None, None) if temperature <= 0 else _proposal(logits32, temperature, top_k, top_p)
+    return kernels.sample_tokens(logits32, softcap=None, temperature=temperature, key=key, split_key=split_key,
+                                 proposal=proposal, proposal_index=index)
+
+
+def _sample_token(logits: torch.Tensor, key, *, temperature: float, top_k: int,
                   top_p: float = 1.0) -> tuple[torch.Tensor, torch.Tensor]:
     """sampler.py:145-183: sample from the configured proposal (temperature, then top-k, then
-    top-p), score under the full unmodified f32 policy."""
+    top-p) with ``jax.random.categorical(key, ...)``, score under the full unmodified f32 policy.
+    ``key`` is the sample key itself (not split here)."""
 
-    logits32 = logits.float()
-    full_logps = torch.log_softmax(logits32, dim=-1)
-    V = logits32.shape[-1]
-    if temperature <= 0:
-        token = torch.argmax(logits32, dim=-1).to(torch.int32)
-    else:
-        scores = logits32 / temperature
-        indices = None
-        if 0 < top_k < V:
-            scores, indices = torch.topk(scores, top_k, dim=-1)
-        elif top_p < 1:
-            scores, indices = torch.sort(scores, dim=-1, descending=True, stable=True)
-        if top_p < 1:
-            w = torch.exp(scores - scores.max(dim=-1, keepdim=True).values)
-            probs = w / w.sum(dim=-1, keepdim=True)
-            previous = torch.cumsum(probs, dim=-1) - probs
-            keep = (previous < top_p) | (torch.arange(scores.shape[-1], device=scores.device)[None, :] == 0)
-            scores = torch.where(keep, scores, torch.full_like(scores, -math.inf))
-        u = torch.rand(scores.shape, generator=generator, device=scores.device, dtype=torch.float32)
-        gumbel = -torch.log(-torch.log(u))
-        selected = torch.argmax(scores + gumbel, dim=-1)
-        token = (selected if indices is None else torch.gather(indices, 1, selected[:, None])[:, 0]).to(torch.int32)
-    logp = torch.gather(full_logps, 1, token[:, None].long())[:, 0]
-    return token, logp
+    k = key if isinstance(key, torch.Tensor) and key.dtype == torch.int32 else key_tensor(key, logits.device)
+    return _draw(logits, k.to(logits.device), temperature=temperature, top_k=top_k, top_p=top_p, split_key=False)
 
 
 def generate(
@@ -288,7 +305,7 @@ def generate(
     out = prefill(params, config, prompt_ids, prompt_mask, max_new_tokens=sc.max_new_tokens, mesh=mesh, lora=lora)
     dev = prompt_ids.device
     B, N = prompt_ids.shape[0], sc.max_new_tokens
-    gen = _generator(key, dev, sc.seed)
+    key_state = key_tensor(key, dev, sc.seed)  # the loop's key, split once per step on the device
     prompt_lengths = prompt_mask.sum(dim=-1, dtype=torch.int32)
     active = torch.ones(B, dtype=torch.bool, device=dev)
     completion_ids = torch.full((B, N), config.pad_token_id, dtype=prompt_ids.dtype, device=dev)
@@ -297,20 +314,20 @@ def generate(
     eos = torch.tensor(list(sc.eos_ids), dtype=torch.int64, device=dev)
     logits = out.logits[:, -1].float()
     cache = out.kv_cache
-    fused = _fused_sampling(sc, config.vocab_size, dev)
+    fused = _fused_sampling(sc, config.vocab_size)
     if fused:  # first token from the prefill logits (already soft-capped), then one graph per step
-        seed = _seed_from_key(key, sc.seed)
-        nxt = kernels.sample_tokens(out.logits[:, -1], softcap=None, temperature=sc.temperature, seed=seed, step=0)
-        graphed = GraphedDecodeStep(params, config, cache, temperature=sc.temperature, seed=seed,
-                                    first_rng_step=1) if N > 1 else None
+        nxt = kernels.sample_tokens(out.logits[:, -1], softcap=None, temperature=sc.temperature, key=key_state)
+        graphed = GraphedDecodeStep(params, config, cache, temperature=sc.temperature,
+                                    key=key_state) if N > 1 else None
     else:
-        graphed = GraphedDecodeStep(params, config, cache) if dev.type == "cuda" and N > 1 else None
+        graphed = GraphedDecodeStep(params, config, cache) if N > 1 else None
     step = 0
     while step < N:
         if fused:
             sampled, logp = nxt
         else:
-            sampled, logp = _sample_token(logits, gen, temperature=sc.temperature, top_k=sc.top_k, top_p=sc.top_p)
+            sampled, logp = _draw(logits, key_state, temperature=sc.temperature, top_k=sc.top_k, top_p=sc.top_p,
+                                  split_key=True)
         token = torch.where(active, sampled, torch.full_like(sampled, config.pad_token_id)).to(prompt_ids.dtype)
         logp = torch.where(active, logp, torch.zeros_like(logp))
         completion_ids[:, step] = token
@@ -322,13 +339,8 @@ def generate(
             pos = (prompt_lengths + step).to(torch.int32)
             if fused:
                 nxt = graphed.step_sample(token.to(torch.int32), pos, active)
-            elif graphed is not None:
-                logits = graphed.step(token.to(torch.int32), pos, active)
             else:
-                dec = decode_step(params, config, token.to(torch.int32), pos, cache, attention_mask=active,
-                                  lora=lora)
-                logits = dec.logits[:, -1].float()
-                cache = dec.kv_cache
+                logits = graphed.step(token.to(torch.int32), pos, active)
         active = next_active
         step += 1
         if not any_active:

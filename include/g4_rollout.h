@@ -191,26 +191,37 @@ int g4_kv_source_layers(int32_t num_layers, int32_t num_kv_shared_layers, const 
 int g4_ring_slot_positions(int32_t last_written, int32_t window_capacity, int32_t* out);
 
 /*
- * Next-token sampling fused with the LM head's soft-capping. Replaces forward_lm_head's capping
- * (model.py:676-680) + _sample_token (sampler.py:145-183) for top_k = 0, top_p = 1: per row
- * x = cast(tanh(l / softcap) * softcap) (softcap 0 = l as given), token = argmax(x) when
- * temperature <= 0, else argmax(x / temperature + g) with Gumbel noise g = -log(-log(u)), u from
- * Philox4x32-10 keyed by seed with counter (column / 4, row, step, 0); logp = x[token] -
- * logsumexp(x) (the unmodified full-vocab policy). Ties go to the lowest column.
+ * Next-token sampling fused with the LM head's soft-capping: one step of generate's loop body
+ * (sampler.py:265-270) = the key split + _sample_token (sampler.py:145-183), with the capping of
+ * forward_lm_head (model.py:676-680) applied on the fly. Per row b:
+ *   x       = cast(tanh(l / softcap) * softcap)   (softcap 0: x = l)
+ *   (next_key, sample_key) = jax.random.split(key)            threefry2x32, partitionable layout
+ *   token   = argmax(x)                                        temperature <= 0
+ *           = argmax(x / temperature + gumbel(sample_key)[b])   no proposal (top_k 0, top_p 1)
+ *           = proposal_index[b, argmax(proposal[b] + gumbel(sample_key)[b])]   with a proposal
+ *   logp    = (x[token] - max(x)) - log(sum(exp(x - max(x))))   (unmodified full-vocab policy)
+ * gumbel = -log(-log(u)), u = jax.random.uniform(sample_key, [batch, K], minval=tiny): the bits of
+ * element (b, j) are the xor of threefry2x32(sample_key, (hi, lo) of b * K + j). Ties go to the
+ * lowest column. `key` is device memory holding 2 uint32 words (jax.random.key_data). With
+ * split_key = 1 it is generate's loop state: the draw uses split(key)[1] and a second launch on
+ * the stream replaces key by split(key)[0], so graph replays advance it like the reference's
+ * while_loop. With split_key = 0 it is _sample_token's key argument: used as is, left unchanged.
  */
 typedef struct G4SampleArgs {
-  int32_t dtype;            /* of logits */
+  int32_t dtype;                  /* of logits */
   int32_t batch;
   int32_t vocab;
-  const void* logits;       /* [batch, row_stride] */
-  int64_t row_stride;       /* elements, >= vocab */
-  float softcap;            /* 0 = none */
-  float temperature;        /* <= 0 = greedy */
-  uint64_t seed;
-  const int32_t* step;      /* device int32 counter, or NULL to use step_scalar */
-  int32_t step_scalar;
-  int32_t* token_out;       /* device [batch] */
-  float* logp_out;          /* device [batch] */
+  int32_t proposal_width;         /* K columns of proposal / proposal_index (0 without a proposal) */
+  const void* logits;             /* [batch, row_stride] */
+  int64_t row_stride;             /* elements, >= vocab */
+  float softcap;                  /* 0 = none */
+  float temperature;              /* <= 0 = greedy */
+  int32_t split_key;              /* 1: split key in place (loop state); 0: key is the sample key */
+  uint32_t* key;                  /* device [2]; may be NULL only when greedy */
+  const float* proposal;          /* device [batch, K] f32 scores (/ temperature, -inf = cut), or NULL */
+  const int32_t* proposal_index;  /* device [batch, K] vocab ids of the proposal columns, or NULL */
+  int32_t* token_out;             /* device [batch] */
+  float* logp_out;                /* device [batch] */
 } G4SampleArgs;
 
 int g4_sample_tokens(const G4SampleArgs* args, void* stream);

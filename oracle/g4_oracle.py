@@ -25,6 +25,8 @@ from typing import NamedTuple
 
 import numpy as np
 
+from . import jax_random as JR
+
 SLIDING = "sliding_attention"
 FULL = "full_attention"
 
@@ -762,11 +764,10 @@ def log_softmax_f32(logits: np.ndarray) -> np.ndarray:
     return (shifted - np.log(np.exp(shifted).sum(axis=-1, keepdims=True, dtype=np.float32))).astype(np.float32)
 
 
-def sample_token(logits: np.ndarray, *, temperature: float, top_k: int = 0, top_p: float = 1.0,
-                 gumbel: np.ndarray | None = None):
-    """sampler.py:145-183 with the categorical draw written as Gumbel-max over the filtered scores
-    (``gumbel`` supplies the noise; jax.random.categorical draws it from threefry). The recorded
-    logp is always the full unmodified f32 policy's."""
+def sample_token(logits: np.ndarray, *, temperature: float, top_k: int = 0, top_p: float = 1.0, key=None):
+    """sampler.py:145-183: greedy argmax, or ``jax.random.categorical(key, scores)`` over the
+    temperature-scaled, top-k / top-p truncated scores (noise drawn with the scores' shape, from
+    oracle/jax_random.py). The recorded logp is always the full unmodified f32 policy's."""
 
     x = logits.astype(np.float32)
     full = log_softmax_f32(x)
@@ -788,21 +789,19 @@ def sample_token(logits: np.ndarray, *, temperature: float, top_k: int = 0, top_
             prev = np.concatenate([np.zeros_like(probs[:, :1]), np.cumsum(probs, axis=-1)[:, :-1]], axis=-1)
             keep = (prev < top_p) | (np.arange(scores.shape[-1])[None, :] == 0)
             scores = np.where(keep, scores, -np.inf)
-        if gumbel is None:
-            raise ValueError("sampling with temperature > 0 needs gumbel noise")
-        # noise is indexed by position in the (possibly sorted / truncated) score array, as
-        # jax.random.categorical draws it with the shape of ``scores``.
-        sel = np.argmax(scores + gumbel[:, : scores.shape[-1]], axis=-1).astype(np.int32)
+        if key is None:
+            raise ValueError("sampling with temperature > 0 needs a key")
+        sel = JR.categorical(key, scores.astype(np.float32))
         token = sel if order is None else np.take_along_axis(order, sel[:, None], axis=-1)[:, 0].astype(np.int32)
     logp = np.take_along_axis(full, token[:, None].astype(np.int64), axis=-1)[:, 0]
     return token, logp
 
 
 def generate(params, cfg, prompt_ids, prompt_mask, *, sampler_config: SamplerConfig, dtype: str = F32,
-             noise=None, step_hook=None) -> RolloutBatch:
+             key=None, step_hook=None) -> RolloutBatch:
     """sampler.py:204-322: prefill, then up to N sample/append steps with early exit once every
-    row emitted EOS. ``noise(step) -> [B, V]`` supplies Gumbel noise for temperature > 0;
-    ``step_hook(step, logits, cache)`` observes the per-step state for parity tests."""
+    row emitted EOS. ``key`` (uint32 [2], default ``PRNGKey(seed)``) is split once per step
+    (sampler.py:265); ``step_hook(step, logits, cache)`` observes the per-step state."""
 
     sc = sampler_config
     if prompt_ids.shape[1] != sc.max_prompt_len:
@@ -821,12 +820,13 @@ def generate(params, cfg, prompt_ids, prompt_mask, *, sampler_config: SamplerCon
     cmask = np.zeros((B, N), bool)
     logps = np.zeros((B, N), np.float32)
     cur = logits[:, -1].astype(np.float32)
+    key = JR.prng_key(sc.seed) if key is None else np.asarray(key, np.uint32)
     step = 0
     while step < N and active.any():
         if step_hook is not None:
             step_hook(step, cur, cache)
-        tok, lp = sample_token(cur, temperature=sc.temperature, top_k=sc.top_k, top_p=sc.top_p,
-                               gumbel=None if sc.temperature <= 0 else noise(step))
+        key, sample_key = JR.split(key)
+        tok, lp = sample_token(cur, temperature=sc.temperature, top_k=sc.top_k, top_p=sc.top_p, key=sample_key)
         tok = np.where(active, tok, cfg.pad_token_id).astype(np.int32)
         lp = np.where(active, lp, 0.0).astype(np.float32)
         ids[:, step], cmask[:, step], logps[:, step] = tok, active, lp

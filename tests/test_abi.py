@@ -161,3 +161,30 @@ def test_python_wrappers_fail_loudly_without_the_library(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "missing.so")
     with pytest.raises(_lib.G4Error, match="missing"):
         _lib.lib()
+
+
+def _sample_args(**kw):
+    base = dict(dtype=_lib.G4_DTYPE_BF16, batch=4, vocab=1000, proposal_width=0, logits=1, row_stride=1000,
+                softcap=30.0, temperature=1.0, split_key=1, key=1, proposal=None, proposal_index=None,
+                token_out=1, logp_out=1)
+    base.update(kw)
+    return _lib.G4SampleArgs(**base)
+
+
+@pytest.mark.parametrize("override,match", [
+    (dict(dtype=3), "dtype"),
+    (dict(row_stride=999), "row_stride"),
+    (dict(batch=0), "batch"),
+    (dict(logits=None), "NULL"),
+    (dict(softcap=-1.0), "softcap"),
+    (dict(key=None), "key"),
+    (dict(split_key=2), "split_key"),
+    (dict(proposal=1, proposal_width=0), "proposal_width"),
+    (dict(proposal=1, proposal_width=1001), "without proposal_index"),
+    (dict(proposal_width=5), "without a proposal"),
+])
+def test_sample_rejects_invalid_arguments(override, match):
+    a = _sample_args(**override)
+    rc = _lib.lib().g4_sample_tokens(ctypes.byref(a), None)
+    assert rc == _lib.G4_ERR_INVALID
+    assert re.search(match, _lib.lib().g4_last_error().decode())

@@ -1,0 +1,137 @@
+"""GPU parity of the native sampler (g4_sample_tokens) with the oracle's JAX random stream
+(oracle/jax_random.py, pinned by the threefry known-answer vectors and JAX's documented split /
+uniform outputs): greedy tokens and full-policy logp, categorical draws token-for-token with and
+without a top-k / top-p proposal, the key split, the top-p threshold KAT, the soft-cap, and whole
+rollouts (generate at T > 0) against the oracle's generate."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import hf_util as H
+from oracle import g4_oracle as O
+from oracle import jax_random as JR
+
+from gemma4_posttrain_jax_amd import config as C
+from gemma4_posttrain_jax_amd import kernels
+from gemma4_posttrain_jax_amd import model as M
+from gemma4_posttrain_jax_amd import sampler as SMP
+
+pytestmark = pytest.mark.gpu
+
+LOGP_ATOL = 2e-6  # the reference's logp tolerance (tests/test_sampler.py:204, 217)
+
+
+def _key(words, device):
+    return SMP.key_tensor(list(map(int, words)), device)
+
+
+def _words(t: torch.Tensor) -> list[int]:
+    return [int(w) & 0xFFFFFFFF for w in t.cpu().tolist()]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_greedy_tokens_and_logps(device, dtype):
+    rng = np.random.default_rng(1)
+    x = torch.from_numpy((rng.standard_normal((7, 5003)) * 3).astype(np.float32)).to(device).to(dtype)
+    tok, logp = kernels.sample_tokens(x, softcap=None, temperature=0.0, key=None)
+    xr = x.float().cpu().numpy()
+    np.testing.assert_array_equal(tok.cpu().numpy(), np.argmax(xr, axis=-1))
+    ref = torch.log_softmax(torch.from_numpy(xr).double(), -1).numpy()[np.arange(7), tok.cpu().numpy()]
+    np.testing.assert_allclose(logp.cpu().numpy(), ref, rtol=0, atol=LOGP_ATOL)
+
+
+def test_greedy_ties_take_the_first_column(device):
+    x = torch.zeros((3, 4099), dtype=torch.bfloat16, device=device)
+    x[0, 17] = x[0, 4000] = 1.0
+    x[1, 4098] = 2.0
+    tok, logp = kernels.sample_tokens(x, softcap=None, temperature=0.0, key=None)
+    assert tok.cpu().tolist() == [17, 4098, 0]
+    np.testing.assert_allclose(logp[2].item(), -np.log(4099.0), atol=LOGP_ATOL)
+
+
+@pytest.mark.parametrize("temperature", [1.0, 0.7])
+def test_draws_follow_the_jax_stream(device, temperature):
+    """split_key: tokens = categorical(split(key)[1], x / T), key <- split(key)[0]."""
+
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((512, 1000)).astype(np.float32)
+    key = _key([7, 123], device)
+    tok, logp = kernels.sample_tokens(torch.from_numpy(x).to(device), softcap=None, temperature=temperature,
+                                      key=key)
+    nxt, sub = JR.split(np.uint32([7, 123]))
+    want_tok, want_logp = O.sample_token(x, temperature=temperature, key=sub)
+    np.testing.assert_array_equal(tok.cpu().numpy(), want_tok)
+    np.testing.assert_allclose(logp.cpu().numpy(), want_logp, rtol=0, atol=LOGP_ATOL)
+    assert _words(key) == nxt.tolist()
+    # without split_key the key is the sample key itself and stays unchanged
+    key2 = _key(sub, device)
+    tok2, _ = kernels.sample_tokens(torch.from_numpy(x).to(device), softcap=None, temperature=temperature,
+                                    key=key2, split_key=False)
+    np.testing.assert_array_equal(tok2.cpu().numpy(), want_tok)
+    assert _words(key2) == sub.tolist()
+
+
+LOGITS = np.float32([[1.1, -0.7, 0.3, 2.0, -2.0], [-1.0, 1.3, 0.6, -2.3, 0.1]])
+
+
+@pytest.mark.parametrize("temperature,top_k,top_p",
+                         [(1.0, 0, 1.0), (0.7, 0, 1.0), (0.8, 3, 1.0), (0.8, 0, 0.85), (0.8, 4, 0.7), (0.8, 0, 1e-50)])
+def test_sample_token_matches_oracle_token_for_token(device, temperature, top_k, top_p):
+    """The reference's distribution test inputs (tests/test_sampler.py:175-205, key PRNGKey(128),
+    8192 copies of two rows): the GPU's tokens equal the oracle's, whose frequencies the CPU suite
+    checks against transformers' warpers."""
+
+    values = np.repeat(LOGITS, 8192, axis=0)
+    tok, logp = SMP._sample_token(torch.from_numpy(values).to(device), 128, temperature=temperature, top_k=top_k,
+                                  top_p=top_p)
+    want_tok, want_logp = O.sample_token(values, temperature=temperature, top_k=top_k, top_p=top_p,
+                                         key=JR.prng_key(128))
+    np.testing.assert_array_equal(tok.cpu().numpy(), want_tok)
+    np.testing.assert_allclose(logp.cpu().numpy(), want_logp, rtol=0, atol=LOGP_ATOL)
+
+
+def test_top_p_keeps_the_threshold_crossing_token(device):
+    """tests/test_sampler.py:208-217."""
+
+    values = torch.from_numpy(np.log(np.float32([0.5, 0.3, 0.2]))).to(device).expand(8192, 3).contiguous()
+    tok, logp = SMP._sample_token(values, 29, temperature=1.0, top_k=0, top_p=0.6)
+    t = tok.cpu().numpy()
+    assert set(t.tolist()) == {0, 1}
+    assert abs(float(np.mean(t == 0)) - 0.625) <= 0.025
+    np.testing.assert_allclose(logp.cpu().numpy(), np.log(np.float32([0.5, 0.3, 0.2]))[t], atol=LOGP_ATOL)
+
+
+def test_softcap_applied_in_the_logits_dtype(device):
+    rng = np.random.default_rng(3)
+    raw = torch.from_numpy((rng.standard_normal((5, 777)) * 40).astype(np.float32)).to(device).to(torch.bfloat16)
+    key = _key([0, 5], device)
+    tok, logp = kernels.sample_tokens(raw, softcap=30.0, temperature=1.0, key=key)
+    capped = (torch.tanh(raw.float() / 30.0) * 30.0).to(torch.bfloat16).float().cpu().numpy()
+    want_tok, want_logp = O.sample_token(capped, temperature=1.0, key=JR.split(np.uint32([0, 5]))[1])
+    np.testing.assert_array_equal(tok.cpu().numpy(), want_tok)
+    np.testing.assert_allclose(logp.cpu().numpy(), want_logp, rtol=0, atol=LOGP_ATOL)
+
+
+@pytest.mark.parametrize("temperature,top_k,top_p", [(1.0, 0, 1.0), (0.8, 7, 1.0), (0.8, 0, 0.9)])
+def test_generate_matches_oracle_rollout(device, temperature, top_k, top_p):
+    """A whole rollout at T > 0 (TINY_A, f32, left-padded row): the same completion tokens as the
+    oracle's generate under the same PRNGKey, logps within the fp32 model bar."""
+
+    kw = H.TINY_A
+    hf = H.build_hf_model(kw, seed=0)
+    ocfg = O.config_from_hf(kw)
+    oparams = H.hf_to_params(hf, ocfg)
+    cfg = C.config_from_hf(kw)
+    params = M.params_from_numpy(oparams, cfg, dtype=torch.float32, device=device)
+    ids = np.array([[21, 22, 23], [0, 32, 33]], np.int32)
+    sc = SMP.SamplerConfig(3, 6, temperature=temperature, top_k=top_k, top_p=top_p, eos_ids=(), seed=17)
+    rb = SMP.generate(params, cfg, torch.from_numpy(ids).to(device), torch.from_numpy(ids != 0).to(device),
+                      sampler_config=sc, key=123)
+    osc = O.SamplerConfig(3, 6, temperature=temperature, top_k=top_k, top_p=top_p, eos_ids=(), seed=17)
+    orb = O.generate(oparams, ocfg, ids, ids != 0, sampler_config=osc, key=JR.prng_key(123))
+    np.testing.assert_array_equal(rb.completion_ids.cpu().numpy(), orb.completion_ids)
+    # the fp32 model bar (2e-5 x max|logit|) at logits bounded by the soft-cap 30
+    np.testing.assert_allclose(rb.rollout_logps.cpu().numpy(), orb.rollout_logps, rtol=0, atol=2e-5 * 30)
