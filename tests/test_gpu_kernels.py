@@ -186,6 +186,22 @@ def test_decode_linear_long_rows(device, D, num_splits):
                  fused=True, seed=23, num_splits=num_splits)
 
 
+@pytest.mark.parametrize("ring,cap", [(True, 512), (False, 768)])
+def test_decode_e2b_batch(device, ring, cap):
+    """The E2B decode shape the rollout runs: B256 x Hkv2 = 512 pairs, ring 512 (sliding layers)
+    and linear 768 (global layers), ragged write positions, a left-padded row, a finished row."""
+
+    rng = np.random.default_rng(11)
+    B, H, R, D = 256, 2, 4, 256
+    C = 768
+    q_pos = rng.integers(300, 767, B)
+    key_mask = np.ones((B, C), bool)
+    key_mask[3, :50] = False
+    key_mask[7, 400:] = False
+    _decode_case(device, O.BF16, B=B, H=H, R=R, D=D, cap=cap, ring=ring, window=512 if ring else 0, q_pos=q_pos,
+                 key_mask=key_mask, fused=True, seed=26)
+
+
 @pytest.mark.parametrize("D", [128, 256])
 def test_decode_split_keys_long_context(device, D):
     """BASELINE config 3 shape at reduced capacity: global-layer linear cache with ragged
