@@ -82,6 +82,8 @@ PROTOTYPES = {
     "g4_residual_norm": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_float, c_void_p, c_void_p, c_void_p]),
     "g4_gelu_mul": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
+    "g4_convert_f32_to_bf16": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "g4_convert_bf16_to_f32": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p]),
     "g4_last_error": (c_char_p, []),
     "g4_version": (c_char_p, []),
 }

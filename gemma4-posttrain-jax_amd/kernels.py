@@ -332,3 +332,34 @@ def sample_tokens(logits: torch.Tensor, *, softcap: float | None, temperature: f
     )
     _lib.check(_lib.lib().g4_sample_tokens(ctypes.byref(a), _stream()), "g4_sample_tokens")
     return token_out, logp_out
+
+
+def convert_f32_to_bf16(x: torch.Tensor, *, nonfinite: torch.Tensor | None = None) -> torch.Tensor:
+    """g4_convert_f32_to_bf16: the reference's bitwise round-to-nearest-even cast of an f32 tensor
+    (any shape) to bf16. ``nonfinite`` (int32 [1] on the device) is set to 1 if an input is inf /
+    NaN or a result overflows; it is not cleared."""
+
+    if x.dtype != torch.float32:
+        raise TypeError("convert_f32_to_bf16 takes a float32 tensor")
+    src = x.contiguous()
+    if src.data_ptr() % 16:
+        src = src.clone()
+    out = torch.empty(src.shape, dtype=torch.bfloat16, device=src.device)
+    if nonfinite is not None and (nonfinite.dtype != torch.int32 or nonfinite.device != src.device):
+        raise ValueError("nonfinite must be an int32 tensor on the input's device")
+    _lib.check(_lib.lib().g4_convert_f32_to_bf16(_ptr(src), _ptr(out), src.numel(),
+                                                 _ptr(nonfinite) if nonfinite is not None else None, _stream()),
+               "g4_convert_f32_to_bf16")
+    return out
+
+
+def convert_bf16_to_f32(x: torch.Tensor) -> torch.Tensor:
+    """g4_convert_bf16_to_f32: exact widening of a bf16 tensor (any shape) to float32."""
+
+    if x.dtype != torch.bfloat16:
+        raise TypeError("convert_bf16_to_f32 takes a bfloat16 tensor")
+    src = x.contiguous()
+    out = torch.empty(src.shape, dtype=torch.float32, device=src.device)
+    _lib.check(_lib.lib().g4_convert_bf16_to_f32(_ptr(src), _ptr(out), src.numel(), _stream()),
+               "g4_convert_bf16_to_f32")
+    return out

@@ -247,6 +247,19 @@ int g4_residual_norm(int dtype, int rows, int cols, const void* branch, const vo
                      void* residual_out, void* next_out, void* stream);
 int g4_gelu_mul(int dtype, int rows, int cols, const void* gate_up, void* out, void* stream);
 
+/*
+ * Rollout weight handoff. g4_convert_f32_to_bf16: out[i] = bf16 bits of in[i], round to nearest
+ * even on the raw bits, (bits + 0x7FFF + ((bits >> 16) & 1)) >> 16 — the conversion of
+ * inference_device.py:10-45 (device_converter), equal to the astype(bfloat16) of
+ * reshard_for_rollout (sharding.py:200-228) on finite values; signed zeros and subnormals are
+ * kept. *nonfinite (device int32, may be NULL) is set to 1 when an input is inf / NaN or a result
+ * overflows to the inf exponent, and is never cleared: zero it before the call.
+ * in and out 16-byte aligned. g4_convert_bf16_to_f32: the exact widening (bits << 16) of
+ * reshard_after_rollout's cast back (sharding.py:231-241).
+ */
+int g4_convert_f32_to_bf16(const float* in, void* out, int64_t n, int32_t* nonfinite, void* stream);
+int g4_convert_bf16_to_f32(const void* in, float* out, int64_t n, void* stream);
+
 const char* g4_last_error(void);
 const char* g4_version(void);
 

@@ -188,3 +188,13 @@ def test_sample_rejects_invalid_arguments(override, match):
     rc = _lib.lib().g4_sample_tokens(ctypes.byref(a), None)
     assert rc == _lib.G4_ERR_INVALID
     assert re.search(match, _lib.lib().g4_last_error().decode())
+
+
+def test_convert_rejects_invalid_arguments():
+    L = _lib.lib()
+    assert L.g4_convert_f32_to_bf16(1, 1, -1, None, None) == _lib.G4_ERR_INVALID
+    assert L.g4_convert_f32_to_bf16(None, 16, 8, None, None) == _lib.G4_ERR_INVALID
+    assert L.g4_convert_f32_to_bf16(4, 16, 8, None, None) == _lib.G4_ERR_INVALID
+    assert re.search("16-byte aligned", L.g4_last_error().decode())
+    assert L.g4_convert_f32_to_bf16(None, None, 0, None, None) == _lib.G4_OK  # nothing to do
+    assert L.g4_convert_bf16_to_f32(None, 16, 8, None) == _lib.G4_ERR_INVALID
