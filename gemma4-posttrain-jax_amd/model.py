@@ -122,8 +122,9 @@ def params_from_numpy(p, config: Gemma4TextConfig, *, dtype=torch.bfloat16, devi
 
 
 class PackedLayer(NamedTuple):
-    w_qkv: torch.Tensor  # [M, (H*R [+ H [+ H]])*D]: q in (h, r) order, then k, then v
-    w_o: torch.Tensor  # [H*R*D, M] rows in (h, r, d) order
+    # every projection in the [N, K] (output-row-major) layout of g4_linear_bf16
+    w_qkv_t: torch.Tensor  # [(H*R [+ H [+ H]])*D, M]: q rows in (h, r) order, then k, then v
+    w_o_t: torch.Tensor  # [M, H*R*D], columns in (h, r, d) order
     w_gate_up_t: torch.Tensor  # [2F, M]: gate rows then up rows (output-major: a faster GEMM at small M)
     w_down_t: torch.Tensor  # [M, F]
     heads: int
@@ -177,10 +178,10 @@ def pack_weights(params: Gemma4TextParams, config: Gemma4TextConfig) -> PackedWe
             parts.append(a.k_proj.reshape(M, H * D))
         if has_v:
             parts.append(a.v_proj.reshape(M, H * D))
-        w_qkv = torch.cat(parts, dim=1).contiguous()
-        w_o = a.o_proj.permute(1, 0, 2, 3).reshape(H * R * D, M).contiguous()
+        w_qkv_t = torch.cat(parts, dim=1).t().contiguous()
+        w_o_t = a.o_proj.permute(1, 0, 2, 3).reshape(H * R * D, M).t().contiguous()
         w_gu_t = torch.cat([lp.mlp.gate_proj, lp.mlp.up_proj], dim=1).t().contiguous()
-        layers.append(PackedLayer(w_qkv, w_o, w_gu_t, lp.mlp.down_proj.t().contiguous(), H, R, D, has_k, has_v,
+        layers.append(PackedLayer(w_qkv_t, w_o_t, w_gu_t, lp.mlp.down_proj.t().contiguous(), H, R, D, has_k, has_v,
                                   lp.layer_scalar.float().reshape(1).contiguous()))
     dev = params.embed_tokens.device
     dt = params.embed_tokens.dtype
@@ -189,6 +190,13 @@ def pack_weights(params: Gemma4TextParams, config: Gemma4TextConfig) -> PackedWe
     _PACKED_BY_ID.clear()  # one live params object at a time (rollout reuses the same weights)
     _PACKED_BY_ID[key] = (params, packed)
     return packed
+
+
+def _proj(x: torch.Tensor, w_t: torch.Tensor) -> torch.Tensor:
+    """``x [T, K] . w_t[N, K]^T`` in x's dtype (hipBLASLt; the [N, K] weight layout is its faster
+    one for the prefill shapes and equal at decode)."""
+
+    return x @ w_t.t()
 
 
 # --- elementwise glue (PyTorch-ROCm ops, reference rounding points) ----------------------------------
@@ -305,7 +313,7 @@ def forward_gemma4_text(
         lt = config.layer_types[i]
         window = config.sliding_window if lt == SLIDING else 0
         H, R, D = pk.heads, pk.group, pk.head_dim
-        qkv = (h.reshape(B * S, -1) @ pk.w_qkv).reshape(B, S, -1)
+        qkv = _proj(h.reshape(B * S, -1), pk.w_qkv_t).reshape(B, S, -1)
         q = qkv[..., : H * R * D].view(B, S, H, R, D)
         q_out = torch.empty((B, S, H, R, D), dtype=x.dtype, device=dev)
         cos, sin = rot[lt]
@@ -344,13 +352,13 @@ def forward_gemma4_text(
         else:
             attn = kernels.decode_attention(src_cache, q_out.view(B, H, R, D), key_mask, q_pos=slot,
                                             window=config.sliding_window).view(B, 1, H, R, D)
-        o = (attn.reshape(B * S, H * R * D) @ pk.w_o).reshape(B, S, -1)
+        o = _proj(attn.reshape(B * S, H * R * D), pk.w_o_t).reshape(B, S, -1)
         # post-attention norm + residual, then the pre-feedforward norm (one pass)
         x, h = kernels.residual_norm(o, lp.post_attention_norm.weight, x, scalar=None,
                                      next_weight=lp.pre_feedforward_norm.weight, eps=eps)
-        gu = h.reshape(B * S, -1) @ pk.w_gate_up_t.t()
+        gu = _proj(h.reshape(B * S, -1), pk.w_gate_up_t)
         act = kernels.gelu_mul(gu)
-        d = (act @ pk.w_down_t.t()).reshape(B, S, -1)
+        d = _proj(act, pk.w_down_t).reshape(B, S, -1)
         next_w = params.layers[i + 1].input_norm.weight if i + 1 < n_layers else params.final_norm.weight
         if lp.per_layer_input is None:
             # post-feedforward norm + residual, layer scalar, then the next layer's input norm
@@ -379,7 +387,7 @@ def forward_lm_head(embed_tokens: torch.Tensor, hidden: torch.Tensor, softcap: f
     """model.py:676-680: tied-embedding logits, ``tanh(x / cap) * cap``."""
 
     B, S, M = hidden.shape
-    logits = (hidden.reshape(B * S, M) @ embed_tokens.t()).reshape(B, S, -1)
+    logits = _proj(hidden.reshape(B * S, M), embed_tokens).reshape(B, S, -1)
     if softcap is not None:
         logits = (torch.tanh(logits.float() / softcap) * softcap).to(logits.dtype)
     return logits

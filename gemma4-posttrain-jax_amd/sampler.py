@@ -20,7 +20,7 @@ import torch
 from . import kernels
 from .config import Gemma4TextConfig
 from .kvcache import KVCache, init_kv_cache
-from .model import Gemma4Output, Gemma4TextParams, forward_gemma4_lm, forward_gemma4_text
+from .model import Gemma4Output, Gemma4TextParams, _proj, forward_gemma4_lm, forward_gemma4_text
 
 
 class SamplerConfig(NamedTuple):
@@ -171,7 +171,7 @@ class GraphedDecodeStep:
         hidden, _ = forward_gemma4_text(self.params, self.tok[:, None], self.pos[:, None], config=self.config,
                                         attention_mask=self.active[:, None], kv_cache=self.cache,
                                         cache_mode="append", write_pos=self.slot)
-        raw = hidden[:, -1] @ self.params.embed_tokens.t()  # [B, V] before the soft-cap
+        raw = _proj(hidden[:, -1], self.params.embed_tokens)  # [B, V] before the soft-cap
         kernels.sample_tokens(raw, softcap=self.config.final_logit_softcapping, temperature=self.temperature,
                               key=self.key, split_key=True, token_out=self.token_out, logp_out=self.logp_out)
         return None
