@@ -25,12 +25,17 @@ __host__ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
 #endif
 }
 
-// float32 -> bf16 bits, round to nearest even; NaN -> canonical quiet NaN.
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+// float32 -> bf16 bits, round to nearest even: gfx950's conversion instruction (v_cvt_pk_bf16_f32),
+// the same bits as the integer formula (u + 0x7fff + ((u >> 16) & 1)) >> 16 for every non-NaN
+// input, subnormals included; NaN stays a quiet NaN.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
+// two floats -> one packed bf16 pair (lo in bits 0..15), one conversion instruction
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }

@@ -204,16 +204,18 @@ constexpr int kLdsBytes = 160 * 1024;  // gfx950 LDS per workgroup
 
 // Largest key-mask row the LDS-staged kernel can hold next to its static tile buffers (bytes;
 // 0 when the limit cannot be raised). Queried and set once per instantiation.
+constexpr int kPfBlocks = 2;  // 16-row column blocks per wave
+
 template <int D>
 int prefill_lds_max_seq() {
   static int max_seq = -1;
   if (max_seq < 0) {
     hipFuncAttributes attr;
     max_seq = 0;
-    if (hipFuncGetAttributes(&attr, (const void*)prefill_bf16_lds_kernel<D>) == hipSuccess) {
+    if (hipFuncGetAttributes(&attr, (const void*)prefill_bf16_lds_kernel<D, kPfBlocks>) == hipSuccess) {
       const int room = (kLdsBytes - (int)attr.sharedSizeBytes) / 16 * 16;
       const int cap = room < kPfMaxSeq ? room : kPfMaxSeq;
-      if (cap > 0 && hipFuncSetAttribute((const void*)prefill_bf16_lds_kernel<D>,
+      if (cap > 0 && hipFuncSetAttribute((const void*)prefill_bf16_lds_kernel<D, kPfBlocks>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize, cap) == hipSuccess)
         max_seq = cap;
     }
@@ -223,10 +225,10 @@ int prefill_lds_max_seq() {
 
 template <int D>
 void launch_prefill_lds(const G4PrefillArgs& a, hipStream_t st) {
-  const int ppb = kPfWaves * (16 / a.group);
+  const int ppb = kPfWaves * kPfBlocks * (16 / a.group);
   const dim3 grid((unsigned)((a.seq + ppb - 1) / ppb), a.kv_heads, a.batch);
   const size_t lds = ((size_t)a.seq + 15) / 16 * 16;
-  hipLaunchKernelGGL(prefill_bf16_lds_kernel<D>, grid, dim3(kPfWaves * 64), lds, st, a);
+  hipLaunchKernelGGL((prefill_bf16_lds_kernel<D, kPfBlocks>), grid, dim3(kPfWaves * 64), lds, st, a);
 }
 
 }  // namespace

@@ -1,8 +1,9 @@
 // bf16 prefill attention with the key / value chunks staged through LDS (head dims 128, 256);
 // included by g4_prefill.hip after prefill_bf16_kernel.
 //
-// A workgroup of 8 waves owns 8 * 16/R consecutive query positions of one (b, kv head); each
-// wave owns 16 query rows (16/R positions x R heads), the MFMA column block. The key range is
+// A workgroup of 8 waves owns 8 * NB * 16/R consecutive query positions of one (b, kv head); each
+// wave owns NB column blocks of 16 query rows (16/R positions x R heads each), so every K and V^T
+// operand tile it reads from LDS feeds NB MFMAs. The key range is
 // walked in 32-key chunks: every chunk's K and V^T are DMA'd into LDS once per workgroup
 // (buffer_load ... lds through a ring of 4 buffers, three chunks in flight ahead of the one being
 // computed, each wave issuing an equal share) as lane-ordered
@@ -32,7 +33,7 @@ __device__ __forceinline__ void wait_vmcnt() {
   __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int D>
+template <int D, int NB>
 __global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4PrefillArgs a) {
   using S_ = PfShape<D>;
   constexpr int KS = D / 32;
@@ -50,7 +51,8 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4Prefi
   uint8_t* km_lds = reinterpret_cast<uint8_t*>(smem);  // key_mask[b, 0:S]
 
   const int R = a.group;
-  const int ppw = 16 / R;              // positions per wave
+  const int ppc = 16 / R;              // positions per 16-row column block
+  const int ppw = NB * ppc;            // positions per wave
   const int ppb = kPfWaves * ppw;      // positions per workgroup
   const int S = a.seq, H = a.kv_heads;
   const int b = blockIdx.z, h = blockIdx.y;
@@ -60,9 +62,14 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4Prefi
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
   const int p0 = blk * ppb;                       // first position of the workgroup
-  const int my_pos = p0 + w * ppw + col / R;      // this lane's query row (column col)
   const int r = col - (col / R) * R;
-  const bool row_ok = my_pos < S;
+  int my_pos[NB];                                 // this lane's query row (column col) of each block
+  bool row_ok[NB];
+#pragma unroll
+  for (int cb = 0; cb < NB; ++cb) {
+    my_pos[cb] = p0 + w * ppw + cb * ppc + col / R;
+    row_ok[cb] = my_pos[cb] < S;
+  }
   const int64_t bh = (int64_t)b * H + h;
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(reinterpret_cast<const uint16_t*>(a.k) + bh * a.k_stride * D,
                                               (uint32_t)a.k_stride * D * 2u);
@@ -70,14 +77,16 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4Prefi
                                               (uint32_t)a.k_stride * D * 2u);
 
   // q operands (registers) and the row's key-mask bytes (LDS)
-  bf16x8 qop[KS];
-  {
-    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + ((((int64_t)b * S + my_pos) * H + h) * R + r) * D;
+  bf16x8 qop[NB][KS];
+#pragma unroll
+  for (int cb = 0; cb < NB; ++cb) {
+    const uint16_t* qrow =
+        reinterpret_cast<const uint16_t*>(a.q) + ((((int64_t)b * S + my_pos[cb]) * H + h) * R + r) * D;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (row_ok) v = load16(qrow + 32 * s + 8 * grp);
-      qop[s] = as_bf16x8(v);
+      if (row_ok[cb]) v = load16(qrow + 32 * s + 8 * grp);
+      qop[cb][s] = as_bf16x8(v);
     }
   }
   const uint8_t* km = a.key_mask + (int64_t)b * a.key_mask_stride;
@@ -107,55 +116,72 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4Prefi
       }
     }
   };
-  // validity bits of the chunk's 32 keys for this lane's row: bit e <-> key c0 + 8*grp + e
-  auto valid_bits = [&](int c) -> uint32_t {
-    const int c0 = c << 5;
-    const int key = c0 + (lane & 31);
+  // key-mask bits of the chunk's 32 keys (bit e <-> key c0 + 8*grp + e), shared by the blocks
+  auto mask_bits = [&](int c) -> uint32_t {
+    const int key = (c << 5) + (lane & 31);
     const uint64_t mb = __ballot(key < S && km_lds[key < S ? key : 0] != 0);
-    uint32_t bits = (uint32_t)(mb >> (8 * grp)) & 0xffu;
-    // causal: key <= my_pos; window: key > my_pos - window
-    const int lo = c0 + 8 * grp;
-    const int hi_ok = my_pos - lo;  // keys lo + e valid for e <= hi_ok
+    return (uint32_t)(mb >> (8 * grp)) & 0xffu;
+  };
+  // ... restricted to the keys block cb's row may see: causal, and the window
+  auto valid_bits = [&](int c, uint32_t bits, int cb) -> uint32_t {
+    const int lo = (c << 5) + 8 * grp;
+    const int hi_ok = my_pos[cb] - lo;  // keys lo + e valid for e <= hi_ok
     bits &= hi_ok >= 7 ? 0xffu : (hi_ok < 0 ? 0u : (0xffu >> (7 - hi_ok)));
     if (a.window > 0) {
-      const int lo_ok = my_pos - a.window + 1 - lo;  // need e >= lo_ok
+      const int lo_ok = my_pos[cb] - a.window + 1 - lo;  // need e >= lo_ok
       bits &= lo_ok <= 0 ? 0xffu : (lo_ok > 7 ? 0u : (0xffu << lo_ok) & 0xffu);
     }
-    return row_ok ? bits : 0u;
+    return row_ok[cb] ? bits : 0u;
   };
+  // scores of both 16-key halves (bb) for every block: each K tile is read once for NB MFMAs
   // (the scheduling barriers bound how many operand tiles are read ahead into registers)
-  auto qk = [&](unsigned char (&kt)[S_::KT][1024], floatx4 (&acc)[2]) {
+  auto qk = [&](unsigned char (&kt)[S_::KT][1024], floatx4 (&acc)[NB][2]) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb) {
-      floatx4 x = {0.f, 0.f, 0.f, 0.f};
+      floatx4 x[NB];
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
-        x = mfma16x16x32(as_bf16x8(*reinterpret_cast<const u32x4*>(&kt[bb * KS + s][16 * lane])), qop[s], x);
-      acc[bb] = x;
+      for (int cb = 0; cb < NB; ++cb) x[cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const bf16x8 kop = as_bf16x8(*reinterpret_cast<const u32x4*>(&kt[bb * KS + s][16 * lane]));
+#pragma unroll
+        for (int cb = 0; cb < NB; ++cb) x[cb] = mfma16x16x32(kop, qop[cb][s], x[cb]);
+      }
+#pragma unroll
+      for (int cb = 0; cb < NB; ++cb) acc[cb][bb] = x[cb];
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
   // ---- pass 1: row max and sum --------------------------------------------------------------------
-  float m = kBf16Min, l = 0.f;
+  float m[NB], l[NB];
+#pragma unroll
+  for (int cb = 0; cb < NB; ++cb) {
+    m[cb] = kBf16Min;
+    l[cb] = 0.f;
+  }
   auto stats = [&](int c, unsigned char (&kt)[S_::KT][1024]) {
-    floatx4 acc[2];
+    floatx4 acc[NB][2];
     qk(kt, acc);
-    const uint32_t bits = valid_bits(c);
+    const uint32_t mbits = mask_bits(c);
 #pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
+    for (int cb = 0; cb < NB; ++cb) {
+      // one rescale per chunk: l <- l * exp(m - m') + sum exp(s - m') with m' = max(m, chunk max)
+      // (masked keys score the fill value, whose exp vanishes against any real maximum)
+      const uint32_t bits = valid_bits(c, mbits, cb);
+      float sc[8], mx = kBf16Min;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int e = 4 * bb + j;
-        const float s = ((bits >> e) & 1u) ? round_bf16(acc[bb][j]) : kBf16Min;
-        if (s > m) {
-          l = l * __expf(m - s) + 1.f;
-          m = s;
-        } else {
-          l += __expf(s - m);
-        }
+      for (int e = 0; e < 8; ++e) {
+        sc[e] = ((bits >> e) & 1u) ? round_bf16(acc[cb][e >> 2][e & 3]) : kBf16Min;
+        mx = fmaxf(mx, sc[e]);
       }
+      const float mn = fmaxf(m[cb], mx);
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum += __expf(sc[e] - mn);
+      l[cb] = l[cb] * __expf(m[cb] - mn) + sum;
+      m[cb] = mn;
     }
   };
   // One pipeline step: wait for this wave's DMA of chunk c (chunks c+1, c+2 may stay in flight),
@@ -201,50 +227,62 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4Prefi
       stats(c + 3, kb3);
     }
   }
+  bool row_masked[NB], mine_masked = false;
+  float rl[NB];
 #pragma unroll
-  for (int msk = 16; msk <= 32; msk <<= 1) {
-    const float m2 = __shfl_xor(m, msk, 64);
-    const float l2 = __shfl_xor(l, msk, 64);
-    const float mm = fmaxf(m, m2);
-    l = l * __expf(m - mm) + l2 * __expf(m2 - mm);
-    m = mm;
+  for (int cb = 0; cb < NB; ++cb) {
+#pragma unroll
+    for (int msk = 16; msk <= 32; msk <<= 1) {
+      const float m2 = __shfl_xor(m[cb], msk, 64);
+      const float l2 = __shfl_xor(l[cb], msk, 64);
+      const float mm = fmaxf(m[cb], m2);
+      l[cb] = l[cb] * __expf(m[cb] - mm) + l2 * __expf(m2 - mm);
+      m[cb] = mm;
+    }
+    // A row with no valid key is the reference's softmax over S equal fills: 1/S on every key.
+    row_masked[cb] = row_ok[cb] && m[cb] == kBf16Min;
+    mine_masked = mine_masked || row_masked[cb];
+    rl[cb] = 1.0f / l[cb];
   }
-  // A row with no valid key is the reference's softmax over S equal fills: 1/S on every key.
-  const bool row_masked = row_ok && m == kBf16Min;
-  const bool any_masked = __syncthreads_or(row_masked);  // (also: every wave is done with pass 1's LDS)
+  const bool any_masked = __syncthreads_or(mine_masked);  // (also: every wave is done with pass 1's LDS)
   const float p_uniform = round_bf16(1.0f / (float)S);
-  const float rl = 1.0f / l;
   const int c2_begin = any_masked ? 0 : c_begin;
   const int c2_end = any_masked ? (S - 1) >> 5 : c_end;
 
   // ---- pass 2: exact probabilities and O^T = V^T P^T -------------------------------------------------
-  floatx4 oacc[S_::VT];
+  floatx4 oacc[NB][S_::VT];
 #pragma unroll
-  for (int i = 0; i < S_::VT; ++i) oacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int cb = 0; cb < NB; ++cb)
+#pragma unroll
+    for (int i = 0; i < S_::VT; ++i) oacc[cb][i] = floatx4{0.f, 0.f, 0.f, 0.f};
   auto values = [&](int c, unsigned char (&kt)[S_::KT][1024], unsigned char (&vt)[S_::VT][1024]) {
-    floatx4 acc[2];
+    floatx4 acc[NB][2];
     qk(kt, acc);
-    const uint32_t bits = valid_bits(c);
+    const uint32_t mbits = mask_bits(c);
     const int kb = (c << 5) + 8 * grp;
-    uint32_t pw[4] = {0u, 0u, 0u, 0u};
+    bf16x8 pop[NB];
 #pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
+    for (int cb = 0; cb < NB; ++cb) {
+      const uint32_t bits = valid_bits(c, mbits, cb);
+      float p[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int e = 4 * bb + j;
-        float p;
-        if (row_masked) p = kb + e < S ? p_uniform : 0.f;
-        else p = ((bits >> e) & 1u) ? __expf(round_bf16(acc[bb][j]) - m) * rl : 0.f;
-        pw[e >> 1] |= f32_to_bf16_bits(p) << (16 * (e & 1));
+      for (int e = 0; e < 8; ++e) {
+        if (row_masked[cb]) p[e] = kb + e < S ? p_uniform : 0.f;
+        else p[e] = ((bits >> e) & 1u) ? __expf(round_bf16(acc[cb][e >> 2][e & 3]) - m[cb]) * rl[cb] : 0.f;
       }
+      pop[cb] = as_bf16x8(u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                                pack_bf16x2(p[6], p[7])});
     }
-    const bf16x8 pop = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
+    constexpr int GRP = 8 / NB;  // V tiles read ahead per scheduling group
 #pragma unroll
-    for (int i0 = 0; i0 < S_::VT; i0 += 8) {
+    for (int i0 = 0; i0 < S_::VT; i0 += GRP) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = i0; i < i0 + 8 && i < S_::VT; ++i)
-        oacc[i] = mfma16x16x32(as_bf16x8(*reinterpret_cast<const u32x4*>(&vt[i][16 * lane])), pop, oacc[i]);
+      for (int i = i0; i < i0 + GRP && i < S_::VT; ++i) {
+        const bf16x8 vop = as_bf16x8(*reinterpret_cast<const u32x4*>(&vt[i][16 * lane]));
+#pragma unroll
+        for (int cb = 0; cb < NB; ++cb) oacc[cb][i] = mfma16x16x32(vop, pop[cb], oacc[cb][i]);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -272,13 +310,16 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4Prefi
     }
   }
 
-  if (row_ok) {
-    uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((((int64_t)b * S + my_pos) * H + h) * R + r) * D;
 #pragma unroll
-    for (int i = 0; i < S_::VT; ++i) {
-      const uint32_t w0 = f32_to_bf16_bits(oacc[i][0]) | (f32_to_bf16_bits(oacc[i][1]) << 16);
-      const uint32_t w1 = f32_to_bf16_bits(oacc[i][2]) | (f32_to_bf16_bits(oacc[i][3]) << 16);
-      *reinterpret_cast<uint2*>(orow + 16 * i + 4 * grp) = make_uint2(w0, w1);
+  for (int cb = 0; cb < NB; ++cb) {
+    if (row_ok[cb]) {
+      uint16_t* orow =
+          reinterpret_cast<uint16_t*>(a.out) + ((((int64_t)b * S + my_pos[cb]) * H + h) * R + r) * D;
+#pragma unroll
+      for (int i = 0; i < S_::VT; ++i) {
+        *reinterpret_cast<uint2*>(orow + 16 * i + 4 * grp) =
+            make_uint2(pack_bf16x2(oacc[cb][i][0], oacc[cb][i][1]), pack_bf16x2(oacc[cb][i][2], oacc[cb][i][3]));
+      }
     }
   }
 }
