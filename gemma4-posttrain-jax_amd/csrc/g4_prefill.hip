@@ -204,7 +204,11 @@ constexpr int kLdsBytes = 160 * 1024;  // gfx950 LDS per workgroup
 
 // Largest key-mask row the LDS-staged kernel can hold next to its static tile buffers (bytes;
 // 0 when the limit cannot be raised). Queried and set once per instantiation.
+// Two waves per SIMD, two 16-row column blocks each (measured per 32-key chunk against one wave per
+// SIMD with three or four blocks, which reuse each LDS tile more but leave a lone wave to overlap
+// its own MFMA, LDS and vector work: 1.85 ms vs 2.04 / 2.66 ms for the config-4 global layer).
 constexpr int kPfBlocks = 2;  // 16-row column blocks per wave
+constexpr int kPfWaves = 8;   // waves per workgroup
 
 template <int D>
 int prefill_lds_max_seq() {
@@ -212,10 +216,10 @@ int prefill_lds_max_seq() {
   if (max_seq < 0) {
     hipFuncAttributes attr;
     max_seq = 0;
-    if (hipFuncGetAttributes(&attr, (const void*)prefill_bf16_lds_kernel<D, kPfBlocks>) == hipSuccess) {
+    if (hipFuncGetAttributes(&attr, (const void*)prefill_bf16_lds_kernel<D, kPfBlocks, kPfWaves>) == hipSuccess) {
       const int room = (kLdsBytes - (int)attr.sharedSizeBytes) / 16 * 16;
       const int cap = room < kPfMaxSeq ? room : kPfMaxSeq;
-      if (cap > 0 && hipFuncSetAttribute((const void*)prefill_bf16_lds_kernel<D, kPfBlocks>,
+      if (cap > 0 && hipFuncSetAttribute((const void*)prefill_bf16_lds_kernel<D, kPfBlocks, kPfWaves>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize, cap) == hipSuccess)
         max_seq = cap;
     }
@@ -228,7 +232,7 @@ void launch_prefill_lds(const G4PrefillArgs& a, hipStream_t st) {
   const int ppb = kPfWaves * kPfBlocks * (16 / a.group);
   const dim3 grid((unsigned)((a.seq + ppb - 1) / ppb), a.kv_heads, a.batch);
   const size_t lds = ((size_t)a.seq + 15) / 16 * 16;
-  hipLaunchKernelGGL((prefill_bf16_lds_kernel<D, kPfBlocks>), grid, dim3(kPfWaves * 64), lds, st, a);
+  hipLaunchKernelGGL((prefill_bf16_lds_kernel<D, kPfBlocks, kPfWaves>), grid, dim3(kPfWaves * 64), lds, st, a);
 }
 
 }  // namespace

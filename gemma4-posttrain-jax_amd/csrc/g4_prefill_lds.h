@@ -1,9 +1,9 @@
 // bf16 prefill attention with the key / value chunks staged through LDS (head dims 128, 256);
 // included by g4_prefill.hip after prefill_bf16_kernel.
 //
-// A workgroup of 8 waves owns 8 * NB * 16/R consecutive query positions of one (b, kv head); each
-// wave owns NB column blocks of 16 query rows (16/R positions x R heads each), so every K and V^T
-// operand tile it reads from LDS feeds NB MFMAs. The key range is
+// A workgroup of NW waves owns NW * NB * 16/R consecutive query positions of one (b, kv head);
+// each wave owns NB column blocks of 16 query rows (16/R positions x R heads each), so every K and
+// V^T operand tile it reads from LDS feeds NB MFMAs. The key range is
 // walked in 32-key chunks: every chunk's K and V^T are DMA'd into LDS once per workgroup
 // (buffer_load ... lds through a ring of 4 buffers, three chunks in flight ahead of the one being
 // computed, each wave issuing an equal share) as lane-ordered
@@ -16,16 +16,15 @@
 // bf16 probabilities exp(s - m) * (1/l) for the value product. Workgroups are launched heaviest
 // (latest positions, longest causal key range) first.
 
-constexpr int kPfWaves = 8;
 constexpr int kPfMaxSeq = 32768;  // key-mask bytes staged in LDS
 
-template <int D>
+template <int D, int NW>
 struct PfShape {
   static constexpr int KT = 2 * (D / 32);  // K operand tiles per chunk: (bb, s)
   static constexpr int VT = D / 16;        // V^T operand tiles per chunk: d-blocks
-  static constexpr int KT_W = KT / kPfWaves;
-  static constexpr int VT_W = VT / kPfWaves;
-  static_assert(KT % kPfWaves == 0 && VT % kPfWaves == 0, "tiles split evenly over the waves");
+  static constexpr int KT_W = KT / NW;     // DMA'd by each wave
+  static constexpr int VT_W = VT / NW;
+  static_assert(KT % NW == 0 && VT % NW == 0, "tiles split evenly over the waves");
 };
 
 template <int N>
@@ -33,9 +32,9 @@ __device__ __forceinline__ void wait_vmcnt() {
   __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int D, int NB>
-__global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4PrefillArgs a) {
-  using S_ = PfShape<D>;
+template <int D, int NB, int NW>
+__global__ __launch_bounds__(NW * 64) void prefill_bf16_lds_kernel(G4PrefillArgs a) {
+  using S_ = PfShape<D, NW>;
   constexpr int KS = D / 32;
   // four buffers as separate arrays, so the compiler's wait before reading one does not include
   // the DMA still in flight into the others
@@ -53,7 +52,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_bf16_lds_kernel(G4Prefi
   const int R = a.group;
   const int ppc = 16 / R;              // positions per 16-row column block
   const int ppw = NB * ppc;            // positions per wave
-  const int ppb = kPfWaves * ppw;      // positions per workgroup
+  const int ppb = NW * ppw;            // positions per workgroup
   const int S = a.seq, H = a.kv_heads;
   const int b = blockIdx.z, h = blockIdx.y;
   const int nblk = (S + ppb - 1) / ppb;
