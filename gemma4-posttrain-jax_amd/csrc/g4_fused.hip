@@ -8,6 +8,8 @@
 // dtype (model.py:505-554), gelu_tanh(gate) * up in f32 rounded once (model.py:393-396).
 // One workgroup of 256 threads per row; the row is read once (kept in registers between the
 // two reductions of g4_residual_norm).
+#include <initializer_list>
+
 #include "g4_common.h"
 #include "g4_internal.h"
 
@@ -130,6 +132,128 @@ __global__ __launch_bounds__(kFuseThreads) void gelu_mul_kernel(int64_t n, int c
   }
 }
 
+// ---- bf16 rows with cols % 8 == 0: one wave per row ---------------------------------------------
+// A lane owns 8-column groups lane, lane + 64, ... (16-byte loads and stores); both reductions are
+// wave shuffles, so there is no LDS and no barrier. Same rounding points as the kernels above.
+constexpr int kWaveGroups = 8;  // 8-column groups per lane: cols <= 64 * 8 * 8 = 4096
+
+__device__ __forceinline__ void unpack8(u32x4 w, float (&f)[8]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    f[2 * q] = __uint_as_float(w[q] << 16);
+    f[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
+  return u32x4{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])};
+}
+
+// x * (mean(x^2) + eps)^-0.5 * w over the lane's groups (wave-wide mean)
+__device__ __forceinline__ void norm_groups(float (&v)[kWaveGroups][8], int ngroups, int cols,
+                                            const uint16_t* weight, float eps) {
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kWaveGroups; ++j)
+    if (j < ngroups)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
+  const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)cols + eps);
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < kWaveGroups; ++j) {
+    if (j < ngroups) {
+      float w[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+      if (weight) unpack8(load16(weight + 8 * (lane + 64 * j)), w);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[j][e] = weight ? v[j][e] * inv * w[e] : v[j][e] * inv;
+    }
+  }
+}
+
+__global__ __launch_bounds__(64) void rms_norm_wave_kernel(int cols, const uint16_t* x, const uint16_t* weight,
+                                                           float eps, uint16_t* out) {
+  const int lane = threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * cols;
+  const int ngroups = (cols / 8 - lane + 63) / 64;  // groups this lane owns
+  float v[kWaveGroups][8];
+#pragma unroll
+  for (int j = 0; j < kWaveGroups; ++j)
+    if (j < ngroups) unpack8(load16(x + base + 8 * (lane + 64 * j)), v[j]);
+  norm_groups(v, ngroups, cols, weight, eps);
+#pragma unroll
+  for (int j = 0; j < kWaveGroups; ++j)
+    if (j < ngroups) *reinterpret_cast<u32x4*>(out + base + 8 * (lane + 64 * j)) = pack8(v[j]);
+}
+
+__global__ __launch_bounds__(64) void residual_norm_wave_kernel(int cols, const uint16_t* branch,
+                                                                const uint16_t* branch_weight, const uint16_t* residual,
+                                                                const float* scalar, const uint16_t* next_weight,
+                                                                float eps, uint16_t* residual_out, uint16_t* next_out) {
+  const int lane = threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * cols;
+  const int ngroups = (cols / 8 - lane + 63) / 64;
+  float v[kWaveGroups][8], r[kWaveGroups][8];
+#pragma unroll
+  for (int j = 0; j < kWaveGroups; ++j) {
+    if (j < ngroups) {
+      unpack8(load16(branch + base + 8 * (lane + 64 * j)), v[j]);
+      unpack8(load16(residual + base + 8 * (lane + 64 * j)), r[j]);
+    }
+  }
+  const float s = scalar ? *scalar : 1.f;
+  norm_groups(v, ngroups, cols, branch_weight, eps);
+#pragma unroll
+  for (int j = 0; j < kWaveGroups; ++j) {
+    if (j < ngroups) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float x = round_bf16(r[j][e] + round_bf16(v[j][e]));
+        if (scalar) x = round_bf16(x * s);
+        v[j][e] = x;
+      }
+      *reinterpret_cast<u32x4*>(residual_out + base + 8 * (lane + 64 * j)) = pack8(v[j]);
+    }
+  }
+  if (!next_out) return;
+  norm_groups(v, ngroups, cols, next_weight, eps);
+#pragma unroll
+  for (int j = 0; j < kWaveGroups; ++j)
+    if (j < ngroups) *reinterpret_cast<u32x4*>(next_out + base + 8 * (lane + 64 * j)) = pack8(v[j]);
+}
+
+// out = round(gelu_tanh(gate) * up), 8 columns per thread per step (bf16, cols % 8 == 0)
+__global__ __launch_bounds__(kFuseThreads) void gelu_mul_vec_kernel(int64_t n8, int cols8, const uint16_t* gate_up,
+                                                                    uint16_t* out) {
+  const float kBeta = 0.7978845608028654f;  // sqrt(2 / pi)
+  const float kKappa = 0.044715f;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / cols8, c8 = i - row * cols8;
+    float g[8], u[8], y[8];
+    unpack8(load16(gate_up + (row * 2 * cols8 + c8) * 8), g);
+    unpack8(load16(gate_up + (row * 2 * cols8 + cols8 + c8) * 8), u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float inner = kBeta * (g[e] + kKappa * g[e] * g[e] * g[e]);
+      y[e] = 0.5f * g[e] * (1.0f + tanhf(inner)) * u[e];
+    }
+    *reinterpret_cast<u32x4*>(out + 8 * i) = pack8(y);
+  }
+}
+
+// rows for the 16-byte kernels: bf16, cols a multiple of 8, 16-byte aligned arrays (NULL allowed)
+bool vec_rows(int dtype, int cols, std::initializer_list<const void*> ptrs) {
+  if (dtype != G4_DTYPE_BF16 || cols % 8) return false;
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) & 15) return false;
+  return true;
+}
+
+// ... and short enough for one wave per row
+bool wave_rows(int dtype, int cols, std::initializer_list<const void*> ptrs) {
+  return cols <= 64 * 8 * kWaveGroups && vec_rows(dtype, cols, ptrs);
+}
+
 int check_rows(const char* fn, int dtype, int rows, int cols) {
   if (dtype != G4_DTYPE_F32 && dtype != G4_DTYPE_BF16) return fail(G4_ERR_INVALID, "%s: dtype %d", fn, dtype);
   if (rows < 0 || cols <= 0) return fail(G4_ERR_INVALID, "%s: rows %d cols %d", fn, rows, cols);
@@ -148,7 +272,10 @@ extern "C" int g4_rms_norm(int dtype, int rows, int cols, const void* x, const v
   if (!x || !out) return fail(G4_ERR_INVALID, "g4_rms_norm: NULL x/out");
   if (rows == 0) return G4_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (dtype == G4_DTYPE_BF16)
+  if (wave_rows(dtype, cols, {x, weight, out}))
+    hipLaunchKernelGGL(rms_norm_wave_kernel, dim3(rows), dim3(64), 0, st, cols, reinterpret_cast<const uint16_t*>(x),
+                       reinterpret_cast<const uint16_t*>(weight), eps, reinterpret_cast<uint16_t*>(out));
+  else if (dtype == G4_DTYPE_BF16)
     hipLaunchKernelGGL(rms_norm_kernel<true>, dim3(rows), dim3(kFuseThreads), 0, st, cols, x, weight, eps, out);
   else
     hipLaunchKernelGGL(rms_norm_kernel<false>, dim3(rows), dim3(kFuseThreads), 0, st, cols, x, weight, eps, out);
@@ -165,7 +292,13 @@ extern "C" int g4_residual_norm(int dtype, int rows, int cols, const void* branc
   if (!branch || !residual || !residual_out) return fail(G4_ERR_INVALID, "g4_residual_norm: NULL branch/residual/out");
   if (rows == 0) return G4_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (dtype == G4_DTYPE_BF16)
+  if (wave_rows(dtype, cols, {branch, branch_weight, residual, next_weight, residual_out, next_out}))
+    hipLaunchKernelGGL(residual_norm_wave_kernel, dim3(rows), dim3(64), 0, st, cols,
+                       reinterpret_cast<const uint16_t*>(branch), reinterpret_cast<const uint16_t*>(branch_weight),
+                       reinterpret_cast<const uint16_t*>(residual), scalar,
+                       reinterpret_cast<const uint16_t*>(next_weight), eps, reinterpret_cast<uint16_t*>(residual_out),
+                       reinterpret_cast<uint16_t*>(next_out));
+  else if (dtype == G4_DTYPE_BF16)
     hipLaunchKernelGGL(residual_norm_kernel<true>, dim3(rows), dim3(kFuseThreads), 0, st, cols, branch,
                        branch_weight, residual, scalar, next_weight, eps, residual_out, next_out);
   else
@@ -180,9 +313,16 @@ extern "C" int g4_gelu_mul(int dtype, int rows, int cols, const void* gate_up, v
   if (!gate_up || !out) return fail(G4_ERR_INVALID, "g4_gelu_mul: NULL gate_up/out");
   const int64_t n = (int64_t)rows * cols;
   if (n == 0) return G4_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (vec_rows(dtype, cols, {gate_up, out})) {
+    const int64_t n8 = n / 8;
+    const int64_t b8 = (n8 + kFuseThreads - 1) / kFuseThreads;
+    hipLaunchKernelGGL(gelu_mul_vec_kernel, dim3((unsigned)(b8 < 65536 ? b8 : 65536)), dim3(kFuseThreads), 0, st, n8,
+                       cols / 8, reinterpret_cast<const uint16_t*>(gate_up), reinterpret_cast<uint16_t*>(out));
+    return check_launch("g4_gelu_mul");
+  }
   const int64_t blocks64 = (n + kFuseThreads - 1) / kFuseThreads;
   const unsigned blocks = (unsigned)(blocks64 < 65536 ? blocks64 : 65536);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (dtype == G4_DTYPE_BF16)
     hipLaunchKernelGGL(gelu_mul_kernel<true>, dim3(blocks), dim3(kFuseThreads), 0, st, n, cols, gate_up, out);
   else

@@ -343,10 +343,10 @@ GLUE_ATOL = {O.BF16: 1e-5, O.F32: 1e-6}
 
 
 @pytest.mark.parametrize("dtype", [O.BF16, O.F32])
-@pytest.mark.parametrize("cols", [2048, 200])
+@pytest.mark.parametrize("cols", [2048, 4096, 200, 100])
 def test_rms_norm_matches_oracle(device, dtype, cols):
-    """g4_rms_norm against the oracle's rms_norm (model.py:278-285); cols not a multiple of the
-    row stride too."""
+    """g4_rms_norm against the oracle's rms_norm (model.py:278-285): bf16 rows of a multiple of 8
+    take the one-wave-per-row kernel (full and partial 512-column rounds), others the general one."""
 
     rng = np.random.default_rng(cols)
     x = _rand(rng, (5, 3, cols), dtype) * 3
@@ -359,12 +359,12 @@ def test_rms_norm_matches_oracle(device, dtype, cols):
 
 
 @pytest.mark.parametrize("dtype", [O.BF16, O.F32])
-def test_residual_norm_matches_oracle_layer_tail(device, dtype):
+@pytest.mark.parametrize("M", [2048, 4096, 1004])
+def test_residual_norm_matches_oracle_layer_tail(device, dtype, M):
     """g4_residual_norm = the oracle's post-norm, residual add, layer scalar and the next norm
     (forward_decoder_layer, model.py:505-554), each rounded where the oracle rounds."""
 
     rng = np.random.default_rng(5)
-    M = 2048
     a = _rand(rng, (4, 1, M), dtype)
     x = _rand(rng, (4, 1, M), dtype)
     wa = O.cast(1 + 0.3 * rng.standard_normal(M).astype(np.float32), dtype)
@@ -388,8 +388,12 @@ def test_gelu_mul_matches_oracle(device, dtype):
     """g4_gelu_mul = the oracle's gelu_tanh(gate) * up rounded once (forward_mlp, model.py:393-396)."""
 
     rng = np.random.default_rng(6)
-    F = 1000
+    F = 1000  # a multiple of 8: the 16-byte bf16 path; F + 4 below: the general one
     gu = _rand(rng, (3, 2, 2 * F), dtype) * 2
     got = to_np(kernels.gelu_mul(to_dev(gu, dtype, device)))
     ref = O.cast(O.gelu_tanh(gu[..., :F]) * gu[..., F:], dtype)
+    np.testing.assert_allclose(got, ref, rtol=GLUE_RTOL[dtype], atol=GLUE_ATOL[dtype])
+    gu = _rand(rng, (3, 2, 2 * (F + 4)), dtype) * 2
+    got = to_np(kernels.gelu_mul(to_dev(gu, dtype, device)))
+    ref = O.cast(O.gelu_tanh(gu[..., :F + 4]) * gu[..., F + 4:], dtype)
     np.testing.assert_allclose(got, ref, rtol=GLUE_RTOL[dtype], atol=GLUE_ATOL[dtype])
