@@ -259,7 +259,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_k
   }
 }
 
-// O = sum of the split partials (split order), bf16. One workgroup of 256 threads per pair.
+// O = sum of the split partials (split order), bf16. Workgroup (pair, y) owns outputs
+// [256 y, 256 y + 256) of the pair's R x D; the partials of 8 splits are loaded before they are
+// added (in split order), so the loads overlap instead of forming one dependent chain per split.
 __global__ __launch_bounds__(256) void decode_splitk_combine_kernel(G4DecodeArgs a, SplitKWorkspace ws) {
   __shared__ float mh[16], lh[16];
   const int R = a.group, D = a.head_dim;
@@ -271,10 +273,18 @@ __global__ __launch_bounds__(256) void decode_splitk_combine_kernel(G4DecodeArgs
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const bool all_masked = splitk_row_stats(ws, pair, R, n_splits_row, mh, lh, w, (int)(blockDim.x >> 6), lane);
   const int n = all_masked ? ws.n_splits : n_splits_row;
-  uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + (int64_t)pair * R * D;
-  for (int idx = tid; idx < R * D; idx += blockDim.x) {
-    float o = 0.f;
-    for (int s = 0; s < n; ++s) o += ws.partials[((int64_t)pair * ws.n_splits + s) * R * D + idx];
-    out[idx] = (uint16_t)f32_to_bf16_bits(o);
+  const int idx = (int)blockIdx.y * 256 + tid;
+  if (idx >= R * D) return;
+  const float* part = ws.partials + (int64_t)pair * ws.n_splits * R * D + idx;
+  float o = 0.f;
+  int s = 0;
+  for (; s + 8 <= n; s += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = part[(int64_t)(s + j) * R * D];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o += v[j];
   }
+  for (; s < n; ++s) o += part[(int64_t)s * R * D];
+  reinterpret_cast<uint16_t*>(a.out)[(int64_t)pair * R * D + idx] = (uint16_t)f32_to_bf16_bits(o);
 }

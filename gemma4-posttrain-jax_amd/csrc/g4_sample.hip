@@ -105,22 +105,39 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) 
     }
   }
   RowState st = {kF32Min, 0.f, -INFINITY, 0x7fffffff};
-  // columns c = tid + 1024 n: each thread visits its columns in increasing order, so a strict
-  // comparison keeps the first of equal scores
-  for (int c = threadIdx.x; c < a.vocab; c += kSampleThreads) {
-    const float x = capped<BF16>(lrow, c, a.softcap);
-    if (x > st.m) {
-      st.s = st.s * expf(st.m - x) + 1.f;
-      st.m = x;
-    } else {
-      st.s += expf(x - st.m);
+  // columns c = tid + 1024 (kUnroll n + u): each thread visits its columns in increasing order, so
+  // a strict comparison keeps the first of equal scores. kUnroll columns per step give independent
+  // noise chains and one max / sum rescale per step.
+  constexpr int kUnroll = 4;
+  for (int c0 = threadIdx.x; c0 < a.vocab; c0 += kUnroll * kSampleThreads) {
+    float x[kUnroll], mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int c = c0 + u * kSampleThreads;
+      x[u] = c < a.vocab ? capped<BF16>(lrow, c, a.softcap) : -INFINITY;
+      mx = fmaxf(mx, x[u]);
     }
+    const float mn = fmaxf(st.m, mx);
+    float sum = 0.f;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) sum += expf(x[u] - mn);
+    st.s = st.s * expf(st.m - mn) + sum;
+    st.m = mn;
     if (!proposal) {
-      float score = x;
-      if (!greedy) score = x / a.temperature + gumbel(k0, k1, (uint64_t)row * (uint64_t)a.vocab + (uint64_t)c);
-      if (score > st.best) {
-        st.best = score;
-        st.idx = c;
+      float score[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int c = c0 + u * kSampleThreads;
+        score[u] = x[u];
+        if (!greedy && c < a.vocab)
+          score[u] = x[u] / a.temperature + gumbel(k0, k1, (uint64_t)row * (uint64_t)a.vocab + (uint64_t)c);
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (score[u] > st.best) {
+          st.best = score[u];
+          st.idx = c0 + u * kSampleThreads;
+        }
       }
     }
   }
