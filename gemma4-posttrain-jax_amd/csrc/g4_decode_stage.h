@@ -32,17 +32,19 @@ __device__ __forceinline__ float wave_sum64(float v) {
   return v;
 }
 
+using VtTiles = unsigned char[NW][NW][1024];  // [wave][chunk][lane*16]
+
+// The body takes every LDS region as a restrict pointer: once inlined, the compiler knows that the
+// score / statistics accesses never touch the tiles the V^T DMA writes, so it does not make them
+// wait for that DMA.
 template <int D, int NSPLIT>
-__global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_stage_kernel(G4DecodeArgs a) {
-  static_assert(D / NSPLIT == 16 * NW, "one 16-row d-block of V^T per wave");
-  __shared__ __attribute__((aligned(1024))) unsigned char vt_lo[NW][NW][1024];  // chunks 0..7: [wave][chunk][lane*16]
-  __shared__ __attribute__((aligned(1024))) unsigned char vt_hi[NW][NW][1024];  // chunks 8..15
-  __shared__ __attribute__((aligned(16))) uint16_t nk_lds[D];
-  extern __shared__ float smem[];
+__device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles* __restrict__ vt_lo_p,
+                                           VtTiles* __restrict__ vt_hi_p, uint16_t* __restrict__ nk_lds,
+                                           uint16_t* __restrict__ sp, float* __restrict__ wmax,
+                                           float* __restrict__ bsum) {
+  VtTiles& vt_lo = *vt_lo_p;
+  VtTiles& vt_hi = *vt_hi_p;
   const int R = a.group;
-  uint16_t* sp = reinterpret_cast<uint16_t*>(smem);                // [R][stride] scores, then probabilities
-  float* wmax = reinterpret_cast<float*>(sp + R * kStageStride);  // [NW][16] wave maxima
-  float* bsum = wmax + NW * 16;                                   // [R][2] sums of 256-slot blocks
 
   const int npairs = a.batch * a.kv_heads;
   int pair, h;
@@ -97,12 +99,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_stage_kernel(G4
   // Every byte is requested before any compute: a wave stalled on a full memory queue cannot
   // compute anyway, and its K (requested first) has landed by the time its last DMA is queued.
   const uint32_t soff = (uint32_t)(16 * db * ss) * 2u;
-  auto dma_v = [&](unsigned char (&tiles)[NW][NW][1024], int c) {
-    if (c < n_chunks) {
-      const uint32_t voff = (uint32_t)(col * ss + (c << 5) + 8 * grp) * 2u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&tiles[w][c & (NW - 1)][0],
-                                               16, voff, soff, 0, 0);
-    }
+  // Every wave issues all 8 DMAs of a half (a chunk past the row's last one re-reads that last
+  // chunk, which stays inside the pair's slots), so the compiler knows how many loads are in
+  // flight behind each K load and waits for exactly the one it needs.
+  const int c_last = n_chunks > 0 ? n_chunks - 1 : 0;
+  auto dma_v = [&](VtTiles& tiles, int c) {
+    const int cs = c < n_chunks ? c : c_last;
+    const uint32_t voff = (uint32_t)(col * ss + (cs << 5) + 8 * grp) * 2u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&tiles[w][c & (NW - 1)][0],
+                                             16, voff, soff, 0, 0);
   };
 #pragma unroll
   for (int c = 0; c < NW; ++c) dma_v(vt_lo, c);
@@ -184,7 +189,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_stage_kernel(G4
   const int cn = (int)(kr.new_slot >> 5), gn = (int)(kr.new_slot & 31) >> 3, en = (int)(kr.new_slot & 7);
   const int n_chunks2 = all_masked ? (a.capacity + 31) >> 5 : n_chunks;
   floatx4 oacc = {0.f, 0.f, 0.f, 0.f}, oacc1 = {0.f, 0.f, 0.f, 0.f};  // even / odd chunks
-  auto value_half = [&](unsigned char (&tiles)[NW][NW][1024], int c_first) {
+  auto value_half = [&](VtTiles& tiles, int c_first) {
     // the appended slot's value into the staged tile (the lanes of the slot's 8-slot group)
     if (has_new && cn >= c_first && cn < c_first + NW && grp == gn)
       *reinterpret_cast<uint16_t*>(&tiles[w][cn - c_first][16 * lane + 2 * en]) = (uint16_t)nvb;
@@ -232,4 +237,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_stage_kernel(G4
     const uint32_t w1 = f32_to_bf16_bits(oacc[2]) | (f32_to_bf16_bits(oacc[3]) << 16);
     *reinterpret_cast<uint2*>(orow + 16 * db + 4 * grp) = make_uint2(w0, w1);
   }
+}
+
+template <int D, int NSPLIT>
+__global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_stage_kernel(G4DecodeArgs a) {
+  static_assert(D / NSPLIT == 16 * NW, "one 16-row d-block of V^T per wave");
+  __shared__ __attribute__((aligned(1024))) VtTiles vt_lo;  // chunks 0..7
+  __shared__ __attribute__((aligned(1024))) VtTiles vt_hi;  // chunks 8..15
+  __shared__ __attribute__((aligned(16))) uint16_t nk_lds[D];
+  extern __shared__ float smem[];
+  uint16_t* sp = reinterpret_cast<uint16_t*>(smem);                      // [R][stride] scores, then probabilities
+  float* wmax = reinterpret_cast<float*>(sp + a.group * kStageStride);  // [NW][16] wave maxima
+  float* bsum = wmax + NW * 16;                                         // [R][2] sums of 256-slot blocks
+  stage_body<D, NSPLIT>(a, &vt_lo, &vt_hi, nk_lds, sp, wmax, bsum);
 }
