@@ -15,7 +15,7 @@ namespace {
 enum VecKind { kQ = 0, kK = 1, kV = 2 };
 
 template <bool BF16, int D>
-__global__ __launch_bounds__(256) void append_kernel(G4AppendArgs a) {
+__global__ __launch_bounds__(1024) void append_kernel(G4AppendArgs a) {
   using E = Elem<BF16>;
   using T = typename E::T;
   // D >= 64: lane l owns d in [l*D/64, (l+1)*D/64) and its RoPE partner is lane l^32;
@@ -73,12 +73,24 @@ __global__ __launch_bounds__(256) void append_kernel(G4AppendArgs a) {
       src = reinterpret_cast<const T*>(a.v) + in_base + (int64_t)head * D;
     }
 
-    float x[PER];
-#pragma unroll
-    for (int e = 0; e < PER; ++e) x[e] = lane_on ? E::load(src, lane * PER + e) : 0.f;
-
     const bool norm = (kind == kQ && (a.flags & G4_APPEND_NORM_Q)) || (kind == kK && (a.flags & G4_APPEND_NORM_K)) ||
                       (kind == kV && (a.flags & G4_APPEND_NORM_V));
+    const bool rope = (kind == kQ && (a.flags & G4_APPEND_ROPE_Q)) || (kind == kK && (a.flags & G4_APPEND_ROPE_K));
+    const T* w = norm ? (kind == kQ ? reinterpret_cast<const T*>(a.q_norm_weight)
+                                    : (kind == kK ? reinterpret_cast<const T*>(a.k_norm_weight) : nullptr))
+                      : nullptr;
+    // Every input of the vector (its elements, norm weights, cos / sin) is requested before any
+    // arithmetic: one memory round trip per vector.
+    float x[PER], wv[PER], cv[PER], sv[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const int d = lane * PER + e;
+      x[e] = lane_on ? E::load(src, d) : 0.f;
+      wv[e] = (w && lane_on) ? E::load(w, d) : 1.f;
+      cv[e] = (rope && lane_on) ? a.rope_cos[rope_base + d] : 0.f;
+      sv[e] = (rope && lane_on) ? a.rope_sin[rope_base + d] : 0.f;
+    }
+
     if (norm) {
       // forward_rms_norm (model.py:278-285): f32 statistics, x * (mean(x^2) + eps)^-0.5 * w.
       float ss = 0.f;
@@ -86,17 +98,14 @@ __global__ __launch_bounds__(256) void append_kernel(G4AppendArgs a) {
       for (int e = 0; e < PER; ++e) ss += x[e] * x[e];
       ss = wave_sum(ss);
       const float inv = 1.0f / __fsqrt_rn(ss / (float)D + a.eps);
-      const T* w = kind == kQ ? reinterpret_cast<const T*>(a.q_norm_weight)
-                              : (kind == kK ? reinterpret_cast<const T*>(a.k_norm_weight) : nullptr);
 #pragma unroll
       for (int e = 0; e < PER; ++e) {
         float y = x[e] * inv;
-        if (w && lane_on) y = y * E::load(w, lane * PER + e);
+        if (w) y = y * wv[e];
         x[e] = E::round(y);
       }
     }
 
-    const bool rope = (kind == kQ && (a.flags & G4_APPEND_ROPE_Q)) || (kind == kK && (a.flags & G4_APPEND_ROPE_K));
     if (rope) {
       // x*cos + rotate_half(x)*sin with cos/sin first rounded to the activation dtype
       // (model.py:309-317); products and sum are rounded separately (no FMA contraction).
@@ -106,8 +115,8 @@ __global__ __launch_bounds__(256) void append_kernel(G4AppendArgs a) {
         const int d = lane * PER + e;
         const float partner = __shfl_xor(x[e], PARTNER, 64);
         const float rot = d < D / 2 ? -partner : partner;
-        const float c = lane_on ? E::round(a.rope_cos[rope_base + d]) : 0.f;
-        const float sn = lane_on ? E::round(a.rope_sin[rope_base + d]) : 0.f;
+        const float c = E::round(cv[e]);
+        const float sn = E::round(sv[e]);
         const float t0 = x[e] * c;  // plain operators: the pragma above keeps them unfused
         const float t1 = rot * sn;
         x[e] = E::round(t0 + t1);
@@ -149,7 +158,9 @@ __global__ __launch_bounds__(256) void append_kernel(G4AppendArgs a) {
 template <bool BF16>
 int launch_append(const G4AppendArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)((int64_t)a.batch * a.seq));
-  const dim3 block(256);
+  // one wave per head vector (q heads, k heads, v heads) up to 16 waves; more vectors loop
+  const int nvec = (a.q ? a.kv_heads * a.group : 0) + (a.k ? 2 * a.kv_heads : 0);
+  const dim3 block((unsigned)(64 * (nvec < 1 ? 1 : (nvec > 16 ? 16 : nvec))));
   switch (a.head_dim) {
     case 8: hipLaunchKernelGGL((append_kernel<BF16, 8>), grid, block, 0, st, a); break;
     case 16: hipLaunchKernelGGL((append_kernel<BF16, 16>), grid, block, 0, st, a); break;

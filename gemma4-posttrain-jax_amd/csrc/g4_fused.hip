@@ -149,9 +149,17 @@ __device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
   return u32x4{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])};
 }
 
-// x * (mean(x^2) + eps)^-0.5 * w over the lane's groups (wave-wide mean)
+// The lane's groups of a weight row, loaded up front (with the data, one memory round trip).
+__device__ __forceinline__ void load_weight_groups(u32x4 (&w)[kWaveGroups], int ngroups, const uint16_t* weight) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < kWaveGroups; ++j)
+    if (weight && j < ngroups) w[j] = load16(weight + 8 * (lane + 64 * j));
+}
+
+// x * (mean(x^2) + eps)^-0.5 * w over the lane's groups (wave-wide mean); w from load_weight_groups
 __device__ __forceinline__ void norm_groups(float (&v)[kWaveGroups][8], int ngroups, int cols,
-                                            const uint16_t* weight, float eps) {
+                                            const u32x4 (&wg)[kWaveGroups], bool has_weight, float eps) {
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < kWaveGroups; ++j)
@@ -159,14 +167,13 @@ __device__ __forceinline__ void norm_groups(float (&v)[kWaveGroups][8], int ngro
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
   const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)cols + eps);
-  const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int j = 0; j < kWaveGroups; ++j) {
     if (j < ngroups) {
       float w[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
-      if (weight) unpack8(load16(weight + 8 * (lane + 64 * j)), w);
+      if (has_weight) unpack8(wg[j], w);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[j][e] = weight ? v[j][e] * inv * w[e] : v[j][e] * inv;
+      for (int e = 0; e < 8; ++e) v[j][e] = has_weight ? v[j][e] * inv * w[e] : v[j][e] * inv;
     }
   }
 }
@@ -177,10 +184,12 @@ __global__ __launch_bounds__(64) void rms_norm_wave_kernel(int cols, const uint1
   const int64_t base = (int64_t)blockIdx.x * cols;
   const int ngroups = (cols / 8 - lane + 63) / 64;  // groups this lane owns
   float v[kWaveGroups][8];
+  u32x4 wg[kWaveGroups];
+  load_weight_groups(wg, ngroups, weight);
 #pragma unroll
   for (int j = 0; j < kWaveGroups; ++j)
     if (j < ngroups) unpack8(load16(x + base + 8 * (lane + 64 * j)), v[j]);
-  norm_groups(v, ngroups, cols, weight, eps);
+  norm_groups(v, ngroups, cols, wg, weight != nullptr, eps);
 #pragma unroll
   for (int j = 0; j < kWaveGroups; ++j)
     if (j < ngroups) *reinterpret_cast<u32x4*>(out + base + 8 * (lane + 64 * j)) = pack8(v[j]);
@@ -194,6 +203,9 @@ __global__ __launch_bounds__(64) void residual_norm_wave_kernel(int cols, const 
   const int64_t base = (int64_t)blockIdx.x * cols;
   const int ngroups = (cols / 8 - lane + 63) / 64;
   float v[kWaveGroups][8], r[kWaveGroups][8];
+  u32x4 wb[kWaveGroups], wn[kWaveGroups];  // both weight rows with the data: one round trip
+  load_weight_groups(wb, ngroups, branch_weight);
+  load_weight_groups(wn, ngroups, next_out ? next_weight : nullptr);
 #pragma unroll
   for (int j = 0; j < kWaveGroups; ++j) {
     if (j < ngroups) {
@@ -202,7 +214,7 @@ __global__ __launch_bounds__(64) void residual_norm_wave_kernel(int cols, const 
     }
   }
   const float s = scalar ? *scalar : 1.f;
-  norm_groups(v, ngroups, cols, branch_weight, eps);
+  norm_groups(v, ngroups, cols, wb, branch_weight != nullptr, eps);
 #pragma unroll
   for (int j = 0; j < kWaveGroups; ++j) {
     if (j < ngroups) {
@@ -216,7 +228,7 @@ __global__ __launch_bounds__(64) void residual_norm_wave_kernel(int cols, const 
     }
   }
   if (!next_out) return;
-  norm_groups(v, ngroups, cols, next_weight, eps);
+  norm_groups(v, ngroups, cols, wn, next_weight != nullptr, eps);
 #pragma unroll
   for (int j = 0; j < kWaveGroups; ++j)
     if (j < ngroups) *reinterpret_cast<u32x4*>(next_out + base + 8 * (lane + 64 * j)) = pack8(v[j]);
