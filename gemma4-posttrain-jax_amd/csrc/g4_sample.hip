@@ -85,7 +85,7 @@ __device__ __forceinline__ float capped(const typename Elem<BF16>::T* row, int c
   return x;
 }
 
-template <bool BF16>
+template <bool BF16, bool VEC>
 __global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) {
   using T = typename Elem<BF16>::T;
   __shared__ RowState red[kSampleThreads / 64];
@@ -105,40 +105,76 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) 
     }
   }
   RowState st = {kF32Min, 0.f, -INFINITY, 0x7fffffff};
-  // columns c = tid + 1024 (kUnroll n + u): each thread visits its columns in increasing order, so
-  // a strict comparison keeps the first of equal scores. kUnroll columns per step give independent
-  // noise chains and one max / sum rescale per step.
-  constexpr int kUnroll = 4;
-  for (int c0 = threadIdx.x; c0 < a.vocab; c0 += kUnroll * kSampleThreads) {
-    float x[kUnroll], mx = -INFINITY;
+  // One step over N columns col0 + u * stride (u = 0 .. N-1, increasing): the max / sum rescale once
+  // per step, then the perturbed scores (N independent noise chains). Each thread visits its columns
+  // in increasing order, so a strict comparison keeps the first of equal scores.
+  auto step = [&](auto& x, int col0, int stride) {
+    constexpr int N = sizeof(x) / sizeof(x[0]);
+    float mx = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int c = c0 + u * kSampleThreads;
-      x[u] = c < a.vocab ? capped<BF16>(lrow, c, a.softcap) : -INFINITY;
-      mx = fmaxf(mx, x[u]);
-    }
+    for (int u = 0; u < N; ++u) mx = fmaxf(mx, x[u]);
     const float mn = fmaxf(st.m, mx);
     float sum = 0.f;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) sum += expf(x[u] - mn);
+    for (int u = 0; u < N; ++u) sum += expf(x[u] - mn);
     st.s = st.s * expf(st.m - mn) + sum;
     st.m = mn;
-    if (!proposal) {
-      float score[kUnroll];
+    if (proposal) return;
+    float score[N];
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+      const int c = col0 + u * stride;
+      score[u] = x[u];
+      if (!greedy && c < a.vocab) {
+        const float t = a.temperature == 1.0f ? x[u] : x[u] / a.temperature;
+        score[u] = t + gumbel(k0, k1, (uint64_t)row * (uint64_t)a.vocab + (uint64_t)c);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+      if (score[u] > st.best) {
+        st.best = score[u];
+        st.idx = col0 + u * stride;
+      }
+    }
+  };
+  if (VEC) {
+    // 8 consecutive columns per thread and step (one 16-byte bf16 load, two for f32), the next
+    // step's columns requested before this step's arithmetic.
+    using E = Elem<BF16>;
+    constexpr int kRaw = BF16 ? 1 : 2;
+    const int nchunks = a.vocab / 8;
+    u32x4 cur[kRaw], nxt[kRaw];
+    auto load_raw = [&](int j, u32x4 (&r)[kRaw]) {
+#pragma unroll
+      for (int q = 0; q < kRaw; ++q) r[q] = *reinterpret_cast<const u32x4*>(lrow + 8 * j + 4 * q * (BF16 ? 2 : 1));
+    };
+    int j = threadIdx.x;
+    if (j < nchunks) load_raw(j, nxt);
+    for (; j < nchunks; j += kSampleThreads) {
+#pragma unroll
+      for (int q = 0; q < kRaw; ++q) cur[q] = nxt[q];
+      if (j + kSampleThreads < nchunks) load_raw(j + kSampleThreads, nxt);
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t word = cur[BF16 ? 0 : e / 4][BF16 ? e / 2 : e % 4];
+        x[e] = BF16 ? (e & 1 ? __uint_as_float(word & 0xffff0000u) : __uint_as_float(word << 16)) : __uint_as_float(word);
+        if (a.softcap > 0.f) x[e] = E::round(tanhf(x[e] / a.softcap) * a.softcap);  // the reference divides by the cap
+      }
+      step(x, 8 * j, 1);
+    }
+  } else {
+    // columns c = tid + 1024 (4 n + u)
+    constexpr int kUnroll = 4;
+    for (int c0 = threadIdx.x; c0 < a.vocab; c0 += kUnroll * kSampleThreads) {
+      float x[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int c = c0 + u * kSampleThreads;
-        score[u] = x[u];
-        if (!greedy && c < a.vocab)
-          score[u] = x[u] / a.temperature + gumbel(k0, k1, (uint64_t)row * (uint64_t)a.vocab + (uint64_t)c);
+        x[u] = c < a.vocab ? capped<BF16>(lrow, c, a.softcap) : -INFINITY;
       }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        if (score[u] > st.best) {
-          st.best = score[u];
-          st.idx = c0 + u * kSampleThreads;
-        }
-      }
+      step(x, c0, kSampleThreads);
     }
   }
   if (proposal) {
@@ -206,10 +242,19 @@ extern "C" int g4_sample_tokens(const G4SampleArgs* args, void* stream) {
     return fail(G4_ERR_INVALID, "g4_sample_tokens: proposal_width / proposal_index without a proposal");
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (a.dtype == G4_DTYPE_BF16)
-    hipLaunchKernelGGL(sample_kernel<true>, dim3(a.batch), dim3(kSampleThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL(sample_kernel<false>, dim3(a.batch), dim3(kSampleThreads), 0, st, a);
+  const size_t esize = a.dtype == G4_DTYPE_BF16 ? 2 : 4;
+  const bool vec = a.vocab % 8 == 0 && (a.row_stride * esize) % 16 == 0 && reinterpret_cast<uintptr_t>(a.logits) % 16 == 0;
+  if (a.dtype == G4_DTYPE_BF16) {
+    if (vec)
+      hipLaunchKernelGGL((sample_kernel<true, true>), dim3(a.batch), dim3(kSampleThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((sample_kernel<true, false>), dim3(a.batch), dim3(kSampleThreads), 0, st, a);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((sample_kernel<false, true>), dim3(a.batch), dim3(kSampleThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((sample_kernel<false, false>), dim3(a.batch), dim3(kSampleThreads), 0, st, a);
+  }
   if (int rc = check_launch("g4_sample_tokens")) return rc;
   if (a.key && a.split_key) {
     hipLaunchKernelGGL(advance_key_kernel, dim3(1), dim3(64), 0, st, a.key);
