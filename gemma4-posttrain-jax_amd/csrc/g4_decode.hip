@@ -234,7 +234,8 @@ int launch_split_keys(const G4DecodeArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)(npairs * ws.n_splits)), block(kDecodeWaves * 64);
   const size_t lds = stage_lds_bytes(a.group);
   hipLaunchKernelGGL(decode_bf16_splitk_scores_kernel<D>, grid, block, lds, st, a, ws);
-  hipLaunchKernelGGL(decode_bf16_splitk_values_kernel<D>, grid, block, lds, st, a, ws);
+  hipLaunchKernelGGL(decode_bf16_splitk_values_kernel<D>, dim3((unsigned)(npairs * ws.n_splits * (D / 16 / kDecodeWaves))),
+                     block, lds, st, a, ws);
   hipLaunchKernelGGL(decode_splitk_combine_kernel, dim3((unsigned)npairs, (unsigned)((a.group * a.head_dim + 255) / 256)),
                      dim3(256), 0, st, a, ws);
   return G4_OK;

@@ -168,12 +168,17 @@ __device__ __forceinline__ bool splitk_row_stats(const SplitKWorkspace& ws, int 
 template <int D>
 __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_kernel(G4DecodeArgs a,
                                                                                        SplitKWorkspace ws) {
-  constexpr int DPW = D / 16 / NW;  // d-blocks per wave (all of D in one workgroup)
+  // DSPLIT workgroups per (pair, split), one 16-row d-block per wave each: V^T takes 64 registers
+  // per lane, so two workgroups fit on a CU and one's loads overlap the other's tail.
+  constexpr int DSPLIT = D / 16 / NW;
+  constexpr int DPW = 1;
+  static_assert(DSPLIT >= 1 && DSPLIT * NW * 16 == D, "whole d-blocks per wave");
   __shared__ float mh[16], lh[16];
   extern __shared__ float smem[];
   const int R = a.group;
   uint16_t* sp = reinterpret_cast<uint16_t*>(smem);  // [R][stride] probabilities of the split
-  const int pair = blockIdx.x / ws.n_splits, split = blockIdx.x % ws.n_splits;
+  const int dh = (int)(blockIdx.x % DSPLIT), item = (int)(blockIdx.x / DSPLIT);
+  const int pair = item / ws.n_splits, split = item % ws.n_splits;
   const int b = pair / a.kv_heads;
   const KeyRange kr = key_range(a, b);
   const int n_chunks = (kr.n_keys + 31) >> 5;
@@ -197,7 +202,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_k
     if (i < n_here) {
       const uint32_t voff = (uint32_t)(col * ss + ((cbase + i) << 5) + 8 * grp) * 2u;
 #pragma unroll
-      for (int ii = 0; ii < DPW; ++ii) vv[i][ii] = buffer_load16(rv, voff, (uint32_t)(16 * (w * DPW + ii) * ss) * 2u);
+      for (int ii = 0; ii < DPW; ++ii) vv[i][ii] = buffer_load16(rv, voff, (uint32_t)(16 * ((dh * NW + w) * DPW + ii) * ss) * 2u);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -247,7 +252,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_k
     const bf16x8 pop = prob_operand(sp, kStageStride, (i << 5) + 8 * grp, R, col);
 #pragma unroll
     for (int ii = 0; ii < DPW; ++ii)
-      oacc[ii] = mfma16x16x32(as_bf16x8(buffer_load16(rv, voff, (uint32_t)(16 * (w * DPW + ii) * ss) * 2u)), pop,
+      oacc[ii] = mfma16x16x32(as_bf16x8(buffer_load16(rv, voff, (uint32_t)(16 * ((dh * NW + w) * DPW + ii) * ss) * 2u)), pop,
                               oacc[ii]);
   }
   // lane (grp, col < R) holds O^T[d = 16*(w*DPW + ii) + 4*grp + j][head col]
@@ -255,7 +260,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_k
     float* o = ws.partials + (((int64_t)pair * ws.n_splits + split) * R + col) * D;
 #pragma unroll
     for (int ii = 0; ii < DPW; ++ii)
-      *reinterpret_cast<floatx4*>(o + 16 * (w * DPW + ii) + 4 * grp) = oacc[ii];
+      *reinterpret_cast<floatx4*>(o + 16 * ((dh * NW + w) * DPW + ii) + 4 * grp) = oacc[ii];
   }
 }
 
