@@ -24,7 +24,7 @@ constexpr int kDecodeWaves = 8;
 
 struct KeyRange {
   int64_t q;         // absolute query position
-  int n_keys;        // slots scanned: all Wc ring slots, or 0..min(q, C-1) for a linear cache
+  int n_keys;        // slots scanned: ring slots 0..min(q, Wc-1), or 0..min(q, C-1) for a linear cache
   int64_t new_slot;  // slot of the fused append (-1: none)
 };
 
@@ -33,7 +33,9 @@ __device__ __forceinline__ KeyRange key_range(const G4DecodeArgs& a, int b) {
   kr.q = a.q_pos ? (int64_t)a.q_pos[b] : (int64_t)a.q_pos_scalar;
   const bool ring = a.kind == G4_CACHE_RING;
   if (ring) {
-    kr.n_keys = a.capacity;
+    // Before the ring wraps (q < Wc - 1) a slot r > q holds p = r - Wc < 0: never written, never
+    // valid (model.py:355-364), so the scan stops at slot q as for a linear cache.
+    kr.n_keys = kr.q < (int64_t)a.capacity - 1 ? (kr.q < 0 ? 0 : (int)(kr.q + 1)) : a.capacity;
   } else {
     int64_t last = kr.q < (int64_t)a.capacity - 1 ? kr.q : (int64_t)a.capacity - 1;
     kr.n_keys = last < 0 ? 0 : (int)(last + 1);

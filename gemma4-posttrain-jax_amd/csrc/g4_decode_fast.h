@@ -196,8 +196,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_fast_kernel(G4D
   const bool ok1 = slot_valid_flat(a, b, kr, c1 + (lane & 31), mb1);
   __builtin_amdgcn_sched_barrier(0);
   u32x4 k0[2][D / 32], k1[2][D / 32];
-  load_k_chunk<D>(k0, rk, c0, col, grp);
-  load_k_chunk<D>(k1, rk, c1, col, grp);
+  // a chunk past the row's last one (never scored) re-reads that last chunk: an L2 hit, not HBM
+  const int kc_last = n_chunks > 0 ? n_chunks - 1 : 0;
+  load_k_chunk<D>(k0, rk, w < n_chunks ? c0 : kc_last << 5, col, grp);
+  load_k_chunk<D>(k1, rk, w + NW < n_chunks ? c1 : kc_last << 5, col, grp);
   __builtin_amdgcn_sched_barrier(0);
   if (tid < R * D / 8) reinterpret_cast<u32x4*>(L.qs)[tid] = qv;
   if (has_new && tid < D / 8) {
@@ -229,11 +231,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_fast_kernel(G4D
     __builtin_amdgcn_sched_barrier(0);
     fast_load_v<S::DPW>(vb, rv, ss, 1, n_chunks, dblock0, col, grp);
     __builtin_amdgcn_sched_barrier(0);
-  } else {  // a long row has more than 2*NW chunks: every wave has both first-round chunks
-    patch_k_sel<D>(k0, L.nk, kr.new_slot, c0, col, grp);
-    mx = score_to_lds<D>(k0, qop, vb0, L.sp, t_alloc, c0, R, col, grp, mx);
-    patch_k_sel<D>(k1, L.nk, kr.new_slot, c1, col, grp);
-    mx = score_to_lds<D>(k1, qop, vb1, L.sp, t_alloc, c1, R, col, grp, mx);
+  } else {  // a long row (capacity beyond 2*NW chunks; its filled part may still be shorter)
+    if (w < n_chunks) {
+      patch_k_sel<D>(k0, L.nk, kr.new_slot, c0, col, grp);
+      mx = score_to_lds<D>(k0, qop, vb0, L.sp, t_alloc, c0, R, col, grp, mx);
+    }
+    if (w + NW < n_chunks) {
+      patch_k_sel<D>(k1, L.nk, kr.new_slot, c1, col, grp);
+      mx = score_to_lds<D>(k1, qop, vb1, L.sp, t_alloc, c1, R, col, grp, mx);
+    }
     for (int c = w + 2 * NW; c < n_chunks; c += 2 * NW) {
       const int e0 = c << 5, e1 = (c + NW) << 5;
       load_k_chunk<D>(k0, rk, e0, col, grp);

@@ -94,8 +94,10 @@ __device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles* __res
   const bool ok1 = slot_valid_flat(a, b, kr, c1 + (lane & 31), mb1);
   __builtin_amdgcn_sched_barrier(0);
   u32x4 k0[2][D / 32], k1[2][D / 32];
-  load_k_chunk<D>(k0, rk, c0, col, grp);
-  load_k_chunk<D>(k1, rk, c1, col, grp);
+  // a chunk past the row's last one (never scored) re-reads that last chunk: an L2 hit, not HBM
+  const int kc_last = n_chunks > 0 ? n_chunks - 1 : 0;
+  load_k_chunk<D>(k0, rk, w < n_chunks ? c0 : kc_last << 5, col, grp);
+  load_k_chunk<D>(k1, rk, w + NW < n_chunks ? c1 : kc_last << 5, col, grp);
   // Every byte is requested before any compute: a wave stalled on a full memory queue cannot
   // compute anyway, and its K (requested first) has landed by the time its last DMA is queued.
   const uint32_t soff = (uint32_t)(16 * db * ss) * 2u;
