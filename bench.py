@@ -7,7 +7,9 @@ step appends one token per row and attends (one launch of the fused append + dec
 graph so the timed region holds only GPU work.
 
 Also reported: ``decode_tok_s_b256`` — full decode steps (30-layer E2B-like model, B=256, T=1
-sampling, BASELINE ``configs[4]``) per second x 256, and the oracle's CPU time for the same step.
+sampling, BASELINE ``configs[4]``) per second x 256, averaged over every step of a 512-token
+rollout; ``rollout_tok_s_b256`` — 256 x 512 tokens over prefill + all decode steps (the reference
+harness's slot tokens/s); and the oracle's CPU time for the same step.
 
 Also: ``long_context_decode`` (``configs[2]``, split-K decode over a 32768-slot linear cache,
 HBM-bound) and ``prefill_attention`` (``configs[3]``, causal / sliding attention on MFMA).
@@ -330,7 +332,15 @@ def random_params(cfg, dev, seed=0):
 
 
 def bench_e2b_decode(steps: int, warmup: int, batch: int = 256, prompt: int = 256, new_tokens: int = 512) -> dict:
-    """Full decode steps (sample at T=1 + one-token forward of all 30 layers + LM head) at B=256."""
+    """A whole rollout at B=256: prefill of the 256-token prompts, then the
+    ``new_tokens - 1`` graphed decode steps that generate() runs (sample at T=1 + one-token forward
+    of all 30 layers + LM head; the last sampled token is not decoded, sampler.py:287-300).
+
+    ``steps`` = 0 times every decode step after ``warmup`` (the caches fill from 256 to 767
+    positions over the rollout, so the average covers short and full rows alike); ``steps`` > 0
+    times only that many steps right after the prefill. The prefill is run twice and the second
+    call is timed (the first pays one-time library and allocator set-up, as the reference's
+    harness excludes compilation and warms up before timing, benchmark_rollout.py:296-311)."""
 
     import torch
 
@@ -344,6 +354,7 @@ def bench_e2b_decode(steps: int, warmup: int, batch: int = 256, prompt: int = 25
     g = torch.Generator(device=dev).manual_seed(1)
     ids = torch.randint(0, cfg.vocab_size, (batch, prompt), device=dev, generator=g, dtype=torch.int32)
     mask = torch.ones_like(ids, dtype=torch.bool)
+    SMP.prefill(params, cfg, ids, mask, max_new_tokens=new_tokens)  # set-up run, discarded
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     out = SMP.prefill(params, cfg, ids, mask, max_new_tokens=new_tokens)
@@ -357,17 +368,21 @@ def bench_e2b_decode(steps: int, warmup: int, batch: int = 256, prompt: int = 25
     key = SMP.key_tensor(2, dev)  # PRNGKey(2), split once per step on the device
     tok, _ = kernels.sample_tokens(out.logits[:, -1], softcap=None, temperature=1.0, key=key)
     engine = SMP.GraphedDecodeStep(params, cfg, cache, temperature=1.0, key=key)
+    n_decode = new_tokens - 1
+    timed = n_decode - warmup if steps <= 0 else min(steps, n_decode - warmup)
     torch.cuda.synchronize()
     for i in range(warmup):
         tok, logp = engine.step_sample(tok, lengths + i, active)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(warmup, warmup + steps):
+    for i in range(warmup, warmup + timed):
         tok, logp = engine.step_sample(tok, lengths + i, active)
     torch.cuda.synchronize()
-    s = (time.perf_counter() - t0) / steps
+    s = (time.perf_counter() - t0) / timed
+    rollout_s = prefill_s + n_decode * s
     logits = out.logits[:, -1]
-    return {"decode_s_per_step": s, "decode_tok_s": batch / s, "prefill_s": prefill_s, "params": params, "cfg": cfg,
+    return {"decode_s_per_step": s, "decode_tok_s": batch / s, "prefill_s": prefill_s, "steps_timed": timed,
+            "rollout_s": rollout_s, "rollout_tok_s": batch * new_tokens / rollout_s, "params": params, "cfg": cfg,
             "cache": engine.kv_cache, "logits": logits}
 
 
@@ -420,7 +435,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--e2b-steps", type=int, default=8)
+    ap.add_argument("--e2b-steps", type=int, default=0,
+                    help="E2B decode steps to time (0: every step of the 512-token rollout)")
     ap.add_argument("--no-e2b", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the configs[2]/[3] lines")
@@ -482,7 +498,10 @@ def main() -> int:
         e2b = bench_e2b_decode(args.e2b_steps, 2)
         line["decode_tok_s_b256"] = round(e2b["decode_tok_s"], 1)
         line["decode_ms_per_step_b256"] = round(e2b["decode_s_per_step"] * 1e3, 3)
+        line["decode_steps_timed_b256"] = e2b["steps_timed"]
         line["prefill_s_b256_p256"] = round(e2b["prefill_s"], 3)
+        # the reference harness's slot tokens/s: batch x new tokens / (prefill + every decode step)
+        line["rollout_tok_s_b256"] = round(e2b["rollout_tok_s"], 1)
         if not args.no_cpu:
             cpu5 = cpu_baseline_e2b_decode(e2b)
             line["cpu_decode_s_per_step_b256"] = round(cpu5["s_per_step"], 3)
