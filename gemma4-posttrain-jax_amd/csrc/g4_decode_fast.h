@@ -116,6 +116,21 @@ __device__ __forceinline__ void fast_load_v(u32x4 (&vg)[8][DPW], __amdgpu_buffer
   }
 }
 
+// fast_load_v with every load issued (a chunk past the row re-reads the last one: an L2 hit), so the
+// number of loads behind it is fixed and later waits need not include them
+template <int DPW>
+__device__ __forceinline__ void fast_load_v_fixed(u32x4 (&vg)[8][DPW], __amdgpu_buffer_rsrc_t rv, int64_t ss, int g,
+                                                  int n_chunks, int dblock0, int col, int grp) {
+  const int c_last = n_chunks > 0 ? n_chunks - 1 : 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = g * 8 + i < n_chunks ? g * 8 + i : c_last;
+    const uint32_t voff = (uint32_t)(col * ss + (c << 5) + 8 * grp) * 2u;
+#pragma unroll
+    for (int ii = 0; ii < DPW; ++ii) vg[i][ii] = buffer_load16(rv, voff, (uint32_t)(16 * (dblock0 + ii) * ss) * 2u);
+  }
+}
+
 template <int DPW>
 __device__ __forceinline__ void fast_consume_v(const u32x4 (&vg)[8][DPW], floatx4 (&oacc)[DPW], const FastLds& L,
                                                int t_alloc, int g, int n_chunks, int R, int dblock0, int col, int grp,
@@ -256,6 +271,12 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_fast_kernel(G4D
         mx = score_to_lds<D>(k1, qop, bits1, L.sp, t_alloc, e1, R, col, grp, mx);
       }
     }
+    // V of the first 16 chunks requested now, with the K registers free: it lands while the
+    // softmax runs
+    __builtin_amdgcn_sched_barrier(0);
+    fast_load_v_fixed<S::DPW>(va, rv, ss, 0, n_chunks, dblock0, col, grp);
+    fast_load_v_fixed<S::DPW>(vb, rv, ss, 1, n_chunks, dblock0, col, grp);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // ---- 4. softmax statistics and probabilities --------------------------------------------------
@@ -312,7 +333,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_fast_kernel(G4D
   __syncthreads();
 
   // ---- 5. value pass over this wave's d-blocks -------------------------------------------------
-  if (LONG || n_chunks2 != n_chunks) {
+  if (n_chunks2 != n_chunks) {  // a fully masked row reads V over the whole capacity
     fast_load_v<S::DPW>(va, rv, ss, 0, n_chunks2, dblock0, col, grp);
     fast_load_v<S::DPW>(vb, rv, ss, 1, n_chunks2, dblock0, col, grp);
   }
