@@ -52,6 +52,18 @@ def test_greedy_ties_take_the_first_column(device):
     np.testing.assert_allclose(logp[2].item(), -np.log(4099.0), atol=LOGP_ATOL)
 
 
+def test_greedy_ties_take_the_first_column_vectorized(device):
+    """Rows of 8-column multiples take the 16-byte path (8 consecutive columns per thread and
+    step): ties across threads, inside one thread's 8 columns, and an all-equal row."""
+
+    x = torch.zeros((3, 4096), dtype=torch.bfloat16, device=device)
+    x[0, 17] = x[0, 4000] = 1.0
+    x[1, 9] = x[1, 8] = x[1, 2056] = 2.0
+    tok, logp = kernels.sample_tokens(x, softcap=None, temperature=0.0, key=None)
+    assert tok.cpu().tolist() == [17, 8, 0]
+    np.testing.assert_allclose(logp[2].item(), -np.log(4096.0), atol=LOGP_ATOL)
+
+
 @pytest.mark.parametrize("temperature", [1.0, 0.7])
 def test_draws_follow_the_jax_stream(device, temperature):
     """split_key: tokens = categorical(split(key)[1], x / T), key <- split(key)[0]."""
