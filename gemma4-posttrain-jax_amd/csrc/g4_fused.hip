@@ -195,43 +195,79 @@ __global__ __launch_bounds__(64) void rms_norm_wave_kernel(int cols, const uint1
     if (j < ngroups) *reinterpret_cast<u32x4*>(out + base + 8 * (lane + 64 * j)) = pack8(v[j]);
 }
 
-__global__ __launch_bounds__(64) void residual_norm_wave_kernel(int cols, const uint16_t* branch,
-                                                                const uint16_t* branch_weight, const uint16_t* residual,
-                                                                const float* scalar, const uint16_t* next_weight,
-                                                                float eps, uint16_t* residual_out, uint16_t* next_out) {
-  const int lane = threadIdx.x;
+// ---- bf16 rows with cols % 8 == 0: 4 waves per row ----------------------------------------------
+// Thread t owns the 8-column groups t, t + 256, ... (16-byte loads and stores). A reduction is a
+// wave shuffle tree and one LDS exchange of the 4 wave sums; each of the two reductions has its
+// own LDS slots, so one barrier each. Same rounding points as the kernels above.
+constexpr int kRowThreads = 256;
+constexpr int kRowGroups = 2;  // 8-column groups per thread: cols <= 256 * 8 * 2 = 4096
+
+__device__ __forceinline__ float row_sum(float v, float* red4) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
+  wg_barrier();
+  return (red4[0] + red4[1]) + (red4[2] + red4[3]);
+}
+
+template <int G>
+__global__ __launch_bounds__(kRowThreads) void residual_norm_row_kernel(int cols, const uint16_t* branch,
+                                                                        const uint16_t* branch_weight,
+                                                                        const uint16_t* residual, const float* scalar,
+                                                                        const uint16_t* next_weight, float eps,
+                                                                        uint16_t* residual_out, uint16_t* next_out) {
+  __shared__ float red[2][4];
+  const int t = threadIdx.x;
   const int64_t base = (int64_t)blockIdx.x * cols;
-  const int ngroups = (cols / 8 - lane + 63) / 64;
-  float v[kWaveGroups][8], r[kWaveGroups][8];
-  u32x4 wb[kWaveGroups], wn[kWaveGroups];  // both weight rows with the data: one round trip
-  load_weight_groups(wb, ngroups, branch_weight);
-  load_weight_groups(wn, ngroups, next_out ? next_weight : nullptr);
+  const int ng = cols / 8;
+  float v[G][8], r[G][8], wb[G][8], wn[G][8];
 #pragma unroll
-  for (int j = 0; j < kWaveGroups; ++j) {
-    if (j < ngroups) {
-      unpack8(load16(branch + base + 8 * (lane + 64 * j)), v[j]);
-      unpack8(load16(residual + base + 8 * (lane + 64 * j)), r[j]);
+  for (int j = 0; j < G; ++j) {  // every load of the row up front: one memory round trip
+    const int g = t + kRowThreads * j;
+    u32x4 a = {0u, 0u, 0u, 0u}, b = a, c = a, d = a;
+    if (g < ng) {
+      a = load16(branch + base + 8 * g);
+      b = load16(residual + base + 8 * g);
+      if (branch_weight) c = load16(branch_weight + 8 * g);
+      if (next_out && next_weight) d = load16(next_weight + 8 * g);
     }
+    unpack8(a, v[j]);
+    unpack8(b, r[j]);
+    unpack8(c, wb[j]);
+    unpack8(d, wn[j]);
   }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < G; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
+  const float inv = 1.0f / sqrtf(row_sum(ss, red[0]) / (float)cols + eps);
   const float s = scalar ? *scalar : 1.f;
-  norm_groups(v, ngroups, cols, wb, branch_weight != nullptr, eps);
 #pragma unroll
-  for (int j = 0; j < kWaveGroups; ++j) {
-    if (j < ngroups) {
+  for (int j = 0; j < G; ++j) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float x = round_bf16(r[j][e] + round_bf16(v[j][e]));
-        if (scalar) x = round_bf16(x * s);
-        v[j][e] = x;
-      }
-      *reinterpret_cast<u32x4*>(residual_out + base + 8 * (lane + 64 * j)) = pack8(v[j]);
+    for (int e = 0; e < 8; ++e) {
+      const float y = branch_weight ? v[j][e] * inv * wb[j][e] : v[j][e] * inv;
+      float x = round_bf16(r[j][e] + round_bf16(y));
+      if (scalar) x = round_bf16(x * s);
+      v[j][e] = x;
     }
+    const int g = t + kRowThreads * j;
+    if (g < ng) *reinterpret_cast<u32x4*>(residual_out + base + 8 * g) = pack8(v[j]);
   }
   if (!next_out) return;
-  norm_groups(v, ngroups, cols, wn, next_weight != nullptr, eps);
+  ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kWaveGroups; ++j)
-    if (j < ngroups) *reinterpret_cast<u32x4*>(next_out + base + 8 * (lane + 64 * j)) = pack8(v[j]);
+  for (int j = 0; j < G; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
+  const float inv2 = 1.0f / sqrtf(row_sum(ss, red[1]) / (float)cols + eps);
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[j][e] = next_weight ? v[j][e] * inv2 * wn[j][e] : v[j][e] * inv2;
+    const int g = t + kRowThreads * j;
+    if (g < ng) *reinterpret_cast<u32x4*>(next_out + base + 8 * g) = pack8(v[j]);
+  }
 }
 
 // out = round(gelu_tanh(gate) * up), 8 columns per thread per step (bf16, cols % 8 == 0)
@@ -304,13 +340,14 @@ extern "C" int g4_residual_norm(int dtype, int rows, int cols, const void* branc
   if (!branch || !residual || !residual_out) return fail(G4_ERR_INVALID, "g4_residual_norm: NULL branch/residual/out");
   if (rows == 0) return G4_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (wave_rows(dtype, cols, {branch, branch_weight, residual, next_weight, residual_out, next_out}))
-    hipLaunchKernelGGL(residual_norm_wave_kernel, dim3(rows), dim3(64), 0, st, cols,
-                       reinterpret_cast<const uint16_t*>(branch), reinterpret_cast<const uint16_t*>(branch_weight),
-                       reinterpret_cast<const uint16_t*>(residual), scalar,
-                       reinterpret_cast<const uint16_t*>(next_weight), eps, reinterpret_cast<uint16_t*>(residual_out),
-                       reinterpret_cast<uint16_t*>(next_out));
-  else if (dtype == G4_DTYPE_BF16)
+  if (vec_rows(dtype, cols, {branch, branch_weight, residual, next_weight, residual_out, next_out}) &&
+      cols <= kRowThreads * 8 * kRowGroups) {
+    const auto kern = cols <= kRowThreads * 8 ? residual_norm_row_kernel<1> : residual_norm_row_kernel<2>;
+    hipLaunchKernelGGL(kern, dim3(rows), dim3(kRowThreads), 0, st, cols, reinterpret_cast<const uint16_t*>(branch),
+                       reinterpret_cast<const uint16_t*>(branch_weight), reinterpret_cast<const uint16_t*>(residual),
+                       scalar, reinterpret_cast<const uint16_t*>(next_weight), eps,
+                       reinterpret_cast<uint16_t*>(residual_out), reinterpret_cast<uint16_t*>(next_out));
+  } else if (dtype == G4_DTYPE_BF16)
     hipLaunchKernelGGL(residual_norm_kernel<true>, dim3(rows), dim3(kFuseThreads), 0, st, cols, branch,
                        branch_weight, residual, scalar, next_weight, eps, residual_out, next_out);
   else
