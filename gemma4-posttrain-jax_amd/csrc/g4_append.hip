@@ -6,6 +6,8 @@
 // owning elements [l*D/64, (l+1)*D/64) so a RoPE partner (d +- D/2) is lane l^32 in the same
 // register. K rows go to the head-major key cache, V to the transposed value cache
 // (cache_vt[b, h, d, slot]) that the MFMA attention kernels read as contiguous key runs.
+#include <initializer_list>
+
 #include "g4_common.h"
 #include "g4_internal.h"
 
@@ -14,7 +16,58 @@ namespace {
 
 enum VecKind { kQ = 0, kK = 1, kV = 2 };
 
-template <bool BF16, int D>
+// PER consecutive elements in one access (PER = 2, 4 or 8; the address aligned to the access)
+template <int PER>
+__device__ __forceinline__ void ld_bf16(const uint16_t* p, float (&x)[PER]) {
+  uint32_t w[PER / 2];
+  if constexpr (PER == 2) {
+    w[0] = *reinterpret_cast<const uint32_t*>(p);
+  } else if constexpr (PER == 4) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    w[0] = v.x, w[1] = v.y;
+  } else {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = v[i];
+  }
+#pragma unroll
+  for (int i = 0; i < PER / 2; ++i) {
+    x[2 * i] = __uint_as_float(w[i] << 16);
+    x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+template <int PER>
+__device__ __forceinline__ void st_bf16(uint16_t* p, const float (&x)[PER]) {
+  uint32_t w[PER / 2];
+#pragma unroll
+  for (int i = 0; i < PER / 2; ++i) w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+  if constexpr (PER == 2) {
+    *reinterpret_cast<uint32_t*>(p) = w[0];
+  } else if constexpr (PER == 4) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+  } else {
+    *reinterpret_cast<u32x4*>(p) = u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
+template <int PER>
+__device__ __forceinline__ void ld_f32(const float* p, float (&x)[PER]) {
+#pragma unroll
+  for (int i = 0; i < PER; i += 2) {
+    if constexpr (PER == 2) {
+      const float2 v = *reinterpret_cast<const float2*>(p);
+      x[0] = v.x, x[1] = v.y;
+    } else if (i % 4 == 0) {
+      const float4 v = *reinterpret_cast<const float4*>(p + i);
+      x[i] = v.x, x[i + 1] = v.y, x[i + 2] = v.z, x[i + 3] = v.w;
+    }
+  }
+}
+
+// VEC: bf16 with D >= 128 and every row aligned to its lane's PER elements (checked on the host):
+// each lane's elements move in one access per array instead of one per element.
+template <bool BF16, int D, bool VEC = false>
 __global__ __launch_bounds__(1024) void append_kernel(G4AppendArgs a) {
   using E = Elem<BF16>;
   using T = typename E::T;
@@ -82,13 +135,24 @@ __global__ __launch_bounds__(1024) void append_kernel(G4AppendArgs a) {
     // Every input of the vector (its elements, norm weights, cos / sin) is requested before any
     // arithmetic: one memory round trip per vector.
     float x[PER], wv[PER], cv[PER], sv[PER];
+    if constexpr (VEC) {
+      ld_bf16<PER>(reinterpret_cast<const uint16_t*>(src) + lane * PER, x);
 #pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      const int d = lane * PER + e;
-      x[e] = lane_on ? E::load(src, d) : 0.f;
-      wv[e] = (w && lane_on) ? E::load(w, d) : 1.f;
-      cv[e] = (rope && lane_on) ? a.rope_cos[rope_base + d] : 0.f;
-      sv[e] = (rope && lane_on) ? a.rope_sin[rope_base + d] : 0.f;
+      for (int e = 0; e < PER; ++e) wv[e] = 1.f, cv[e] = sv[e] = 0.f;
+      if (w) ld_bf16<PER>(reinterpret_cast<const uint16_t*>(w) + lane * PER, wv);
+      if (rope) {
+        ld_f32<PER>(a.rope_cos + rope_base + lane * PER, cv);
+        ld_f32<PER>(a.rope_sin + rope_base + lane * PER, sv);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const int d = lane * PER + e;
+        x[e] = lane_on ? E::load(src, d) : 0.f;
+        wv[e] = (w && lane_on) ? E::load(w, d) : 1.f;
+        cv[e] = (rope && lane_on) ? a.rope_cos[rope_base + d] : 0.f;
+        sv[e] = (rope && lane_on) ? a.rope_sin[rope_base + d] : 0.f;
+      }
     }
 
     if (norm) {
@@ -125,21 +189,19 @@ __global__ __launch_bounds__(1024) void append_kernel(G4AppendArgs a) {
 
     const int64_t bh = (int64_t)b * H + head;
     if (!lane_on) continue;
+    auto store_row = [&](T* dst) {
+      if constexpr (VEC) {
+        st_bf16<PER>(reinterpret_cast<uint16_t*>(dst) + lane * PER, x);
+      } else {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) E::store(dst, lane * PER + e, x[e]);
+      }
+    };
     if (kind == kQ) {
-      T* dst = reinterpret_cast<T*>(a.q_out) + ((((int64_t)token) * H + head) * R + r) * D;
-#pragma unroll
-      for (int e = 0; e < PER; ++e) E::store(dst, lane * PER + e, x[e]);
+      store_row(reinterpret_cast<T*>(a.q_out) + ((((int64_t)token) * H + head) * R + r) * D);
     } else if (kind == kK) {
-      if (to_cache) {
-        T* dst = reinterpret_cast<T*>(a.cache_k) + (bh * a.slot_stride + slot) * D;
-#pragma unroll
-        for (int e = 0; e < PER; ++e) E::store(dst, lane * PER + e, x[e]);
-      }
-      if (a.k_out) {
-        T* dst = reinterpret_cast<T*>(a.k_out) + (bh * a.chunk_stride + s) * D;
-#pragma unroll
-        for (int e = 0; e < PER; ++e) E::store(dst, lane * PER + e, x[e]);
-      }
+      if (to_cache) store_row(reinterpret_cast<T*>(a.cache_k) + (bh * a.slot_stride + slot) * D);
+      if (a.k_out) store_row(reinterpret_cast<T*>(a.k_out) + (bh * a.chunk_stride + s) * D);
     } else {
       if (to_cache) {
         T* dst = reinterpret_cast<T*>(a.cache_vt) + bh * D * a.slot_stride + slot;
@@ -155,12 +217,33 @@ __global__ __launch_bounds__(1024) void append_kernel(G4AppendArgs a) {
   }
 }
 
+// The vectorized path needs every row start aligned to one lane's D/64 bf16 elements (and the
+// f32 RoPE rows to 16 bytes).
+bool vec_rows_ok(const G4AppendArgs& a) {
+  const uintptr_t al = (uintptr_t)(a.head_dim / 64) * 2;
+  for (const void* p : std::initializer_list<const void*>{a.q, a.k, a.v, a.q_out, a.cache_k, a.k_out,
+                                                        a.q_norm_weight, a.k_norm_weight})
+    if (reinterpret_cast<uintptr_t>(p) % al) return false;
+  for (const void* p : std::initializer_list<const void*>{a.rope_cos, a.rope_sin})
+    if (reinterpret_cast<uintptr_t>(p) % 16) return false;
+  return (a.in_row_stride * 2) % (int64_t)al == 0;
+}
+
 template <bool BF16>
 int launch_append(const G4AppendArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)((int64_t)a.batch * a.seq));
   // one wave per head vector (q heads, k heads, v heads) up to 16 waves; more vectors loop
   const int nvec = (a.q ? a.kv_heads * a.group : 0) + (a.k ? 2 * a.kv_heads : 0);
   const dim3 block((unsigned)(64 * (nvec < 1 ? 1 : (nvec > 16 ? 16 : nvec))));
+  if (BF16 && a.head_dim >= 128 && vec_rows_ok(a)) {
+    switch (a.head_dim) {
+      case 128: hipLaunchKernelGGL((append_kernel<true, 128, true>), grid, block, 0, st, a); break;
+      case 256: hipLaunchKernelGGL((append_kernel<true, 256, true>), grid, block, 0, st, a); break;
+      case 512: hipLaunchKernelGGL((append_kernel<true, 512, true>), grid, block, 0, st, a); break;
+      default: return fail(G4_ERR_UNSUPPORTED, "g4_kv_append: head_dim %d", a.head_dim);
+    }
+    return check_launch("g4_kv_append");
+  }
   switch (a.head_dim) {
     case 8: hipLaunchKernelGGL((append_kernel<BF16, 8>), grid, block, 0, st, a); break;
     case 16: hipLaunchKernelGGL((append_kernel<BF16, 16>), grid, block, 0, st, a); break;
