@@ -23,6 +23,7 @@ G4_APPEND_ROPE_K = 4
 G4_APPEND_NORM_Q = 8
 G4_APPEND_ROPE_Q = 16
 G4_DECODE_SPLIT_KEYS = -1
+G4_DECODE_TWO_PASS = -2
 G4_ERR_INVALID = -1
 G4_ERR_UNSUPPORTED = -2
 G4_ERR_LAUNCH = -3

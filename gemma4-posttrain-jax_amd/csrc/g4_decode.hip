@@ -87,6 +87,7 @@ __device__ __forceinline__ void fused_append(const G4DecodeArgs& a, int pair, co
 #include "g4_decode_fast.h"
 #include "g4_decode_stage.h"
 #include "g4_decode_splitk.h"
+#include "g4_decode_twopass.h"
 
 // ----------------------------------------------------------------------------------------------
 // f32, VALU
@@ -243,12 +244,53 @@ int launch_split_keys(const G4DecodeArgs& a, hipStream_t st) {
   return G4_OK;
 }
 
+// Pairs from which the automatic choice takes the two-launch path for rows of at most 1024
+// slots: with fewer, one workgroup per CU holds a whole row and the one-launch kernels are faster
+// (measured: 128 pairs 19.3 vs 22.2 us, 512 pairs 71.8 vs 62.9 us on a 512-slot ring).
+constexpr int64_t kTwoPassMinPairs = 256;
+
+bool two_pass_applies(const G4DecodeArgs& a) {
+  return a.dtype == G4_DTYPE_BF16 && (a.head_dim == 128 || a.head_dim == 256) && a.capacity <= kTpMaxSlots;
+}
+
+bool use_two_pass(const G4DecodeArgs& a) {
+  if (!two_pass_applies(a)) return false;
+  if (a.num_splits == G4_DECODE_TWO_PASS) return true;
+  return a.num_splits == 0 && (int64_t)a.batch * a.kv_heads >= kTwoPassMinPairs;
+}
+
+template <int D, int NCH>
+void launch_tp_values(const G4DecodeArgs& a, const uint16_t* ws, int row_slots, hipStream_t st) {
+  hipLaunchKernelGGL((decode_bf16_tp_values_kernel<D, NCH>), dim3((unsigned)((int64_t)a.batch * a.kv_heads * (D / 16 / kTpWavesV))),
+                     dim3(kTpWavesV * 64), (size_t)a.group * tp_lds_stride(NCH) * 2, st, a, ws, row_slots);
+}
+
+template <int D>
+int launch_two_pass(const G4DecodeArgs& a, hipStream_t st) {
+  const int64_t npairs = (int64_t)a.batch * a.kv_heads;
+  const int cap_chunks = (a.capacity + 31) / 32;
+  const int parts = (cap_chunks + kTpWavesS - 1) / kTpWavesS;
+  const int row_slots = twopass_row_slots(a.capacity);
+  uint16_t* ws = reinterpret_cast<uint16_t*>(a.workspace);
+  hipLaunchKernelGGL(decode_bf16_tp_scores_kernel<D>, dim3((unsigned)(npairs * parts)), dim3(kTpWavesS * 64), 0, st, a,
+                     ws, parts, row_slots);
+  if (cap_chunks <= 16)
+    launch_tp_values<D, 16>(a, ws, row_slots, st);
+  else if (cap_chunks <= 24)
+    launch_tp_values<D, 24>(a, ws, row_slots, st);
+  else
+    launch_tp_values<D, 32>(a, ws, row_slots, st);
+  return G4_OK;
+}
+
 }  // namespace
 }  // namespace g4
 
 extern "C" size_t g4_decode_workspace_size(const G4DecodeArgs* args) {
   using namespace g4;
-  if (!args || !use_split_keys(*args)) return 0;
+  if (!args) return 0;
+  if (use_two_pass(*args)) return twopass_workspace_bytes(args->batch * args->kv_heads, args->group, args->capacity);
+  if (!use_split_keys(*args)) return 0;
   return splitk_workspace_bytes(args->batch * args->kv_heads, args->group, args->head_dim, args->capacity);
 }
 
@@ -278,8 +320,20 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int t_alloc = (a.capacity + 31) / 32 * 32;
   const dim3 grid((unsigned)((int64_t)a.batch * a.kv_heads));
-  if (a.num_splits < G4_DECODE_SPLIT_KEYS || a.num_splits > 2)
+  if (a.num_splits < G4_DECODE_TWO_PASS || a.num_splits > 2)
     return fail(G4_ERR_INVALID, "g4_decode_attention: num_splits %d", a.num_splits);
+  if (a.num_splits == G4_DECODE_TWO_PASS && !two_pass_applies(a))
+    return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: two-pass needs bf16, head_dim 128/256, capacity <= %d",
+                kTpMaxSlots);
+  if (use_two_pass(a)) {
+    const size_t need = twopass_workspace_bytes(a.batch * a.kv_heads, a.group, a.capacity);
+    if (!a.workspace || a.workspace_bytes < need)
+      return fail(G4_ERR_WORKSPACE, "g4_decode_attention: two-pass needs %zu B of workspace (have %zu)", need,
+                  a.workspace ? a.workspace_bytes : (size_t)0);
+    const int rc = a.head_dim == 256 ? launch_two_pass<256>(a, st) : launch_two_pass<128>(a, st);
+    if (rc != G4_OK) return rc;
+    return check_launch("g4_decode_attention");
+  }
   if (use_split_keys(a)) {
     const size_t need = splitk_workspace_bytes(a.batch * a.kv_heads, a.group, a.head_dim, a.capacity);
     if (!a.workspace || a.workspace_bytes < need)

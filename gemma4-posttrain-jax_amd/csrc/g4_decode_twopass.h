@@ -1,0 +1,218 @@
+// bf16 decode attention in two stream-ordered launches, for rows of at most 1024 slots over many
+// (b, kv head) pairs (the E2B rollout batch: the 512-slot sliding-window ring and the global
+// layers' linear cache); included by g4_decode.hip after g4_decode_splitk.h.
+//
+// The one-launch kernels keep a pair's whole row on one CU: K streams in, the row is scored, the
+// softmax runs behind barriers and the value pass follows, so every CU ends each pair with a
+// compute tail during which it has no loads in flight. Here each launch is a plain stream of
+// small independent workgroups, so one workgroup's tail overlaps the next one's loads:
+//   scores  one wave per 32-slot chunk: K into registers, MFMA against the register-held q
+//           operand, bf16-rounded masked scores into the workspace. The wave whose chunk holds the
+//           appended slot substitutes the new K row and, after its loads, writes the slot back to
+//           the cache (K row and V^T column).
+//   values  one wave per 16-row d-block of V^T: the wave requests its first score row and its
+//           whole V^T block (16 rows x the row's chunks, registers) right behind it, forms the
+//           exact probabilities bf16(exp(s - m) / l) of its head while V is in flight (one LDS
+//           exchange, one barrier that waits for LDS traffic only), then runs the value MFMAs.
+//           Nothing is combined across workgroups.
+// The probabilities are the single-launch kernels' (row max and row sum of the same bf16 scores),
+// so the result differs from theirs only in the f32 order of the row sum.
+//
+// Workspace: scores bf16 [pairs][R][row_slots], row_slots = 512 (capacity <= 512) or 1024.
+
+constexpr int kTpWavesS = 4;  // waves per scores workgroup
+constexpr int kTpWavesV = 4;  // waves per values workgroup
+constexpr int kTpMaxSlots = 1024;
+
+__host__ __device__ inline int twopass_row_slots(int capacity) { return capacity <= 512 ? 512 : kTpMaxSlots; }
+
+__host__ __device__ inline size_t twopass_workspace_bytes(int npairs, int R, int capacity) {
+  return (size_t)npairs * R * twopass_row_slots(capacity) * 2;
+}
+
+// grid: pairs x parts, parts = ceil(ceil(capacity / 32) / kTpWavesS); wave w of part p takes chunk
+// kTpWavesS * p + w.
+template <int D>
+__global__ __launch_bounds__(kTpWavesS * 64) void decode_bf16_tp_scores_kernel(G4DecodeArgs a, uint16_t* ws,
+                                                                              int parts, int row_slots) {
+  const int R = a.group;
+  const int pair = (int)(blockIdx.x / parts), part = (int)(blockIdx.x % parts);
+  const int b = pair / a.kv_heads;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const KeyRange kr = key_range(a, b);
+  const int n_chunks = (kr.n_keys + 31) >> 5;
+  const int chunk = part * kTpWavesS + w;
+  const bool writer = kr.new_slot >= 0 && (int)(kr.new_slot >> 5) == chunk;  // stores the appended slot
+  const uint16_t* nk = reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D;
+
+  if (chunk < n_chunks) {
+    const __amdgpu_buffer_rsrc_t rk =
+        make_rsrc(reinterpret_cast<const uint16_t*>(a.cache_k) + (int64_t)pair * a.slot_stride * D,
+                  (uint32_t)a.slot_stride * D * 2u);
+    u32x4 kv[2][D / 32];
+    load_k_chunk<D>(kv, rk, chunk << 5, col, grp);
+    bf16x8 qop[D / 32];
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) qop[s] = q_operand_global(a, pair, R, D, col, grp, s);
+    uint8_t mb;
+    const bool ok = slot_valid_flat(a, b, kr, (chunk << 5) + (lane & 31), mb);
+    const uint64_t vbits = __ballot(ok && mb != 0);
+    if (writer) patch_k_sel<D>(kv, nk, kr.new_slot, chunk << 5, col, grp);
+    score_to_lds<D>(kv, qop, vbits, ws + (int64_t)pair * R * row_slots, row_slots, chunk << 5, R, col, grp,
+                    kBf16Min);
+  }
+  // the fused append's cache write: the K row after this wave's K loads have been consumed (no
+  // other wave of the launch reads that chunk); the V^T column is read only by the values launch
+  if (writer) {
+    uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
+    if (lane < D / 8) *reinterpret_cast<u32x4*>(ck + 8 * lane) = load16(nk + 8 * lane);
+    uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride + kr.new_slot;
+    const uint16_t* nv = reinterpret_cast<const uint16_t*>(a.new_v) + (int64_t)pair * D;
+    for (int d = lane; d < D; d += 64) cv[(int64_t)d * a.slot_stride] = nv[d];
+  }
+}
+
+// Exact probabilities of head hh from its score row (lane owns slots 512 i + 8 lane .. +7, below
+// `slots`) into LDS row hh; returns whether the row has no valid slot (then, with `store`, the
+// row is the uniform bf16(1/capacity) over the capacity).
+template <int NB>
+__device__ __forceinline__ bool tp_probabilities(const u32x4 (&sv)[NB], int hh, bool store, uint16_t* sp,
+                                                 int stride, int slots, int n_scanned, int capacity, int lane) {
+  float e[NB][8];
+  float m = kBf16Min;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int s0 = 512 * i + 8 * lane;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      e[i][2 * j] = s0 + 2 * j < n_scanned ? bf16_lo(sv[i][j]) : kBf16Min;
+      e[i][2 * j + 1] = s0 + 2 * j + 1 < n_scanned ? bf16_hi(sv[i][j]) : kBf16Min;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = fmaxf(m, e[i][j]);
+  }
+  m = wave_max(m);
+  const bool masked = m == kBf16Min;  // no valid slot in the row (the same for every head)
+  if (!store) return masked;
+  float l = 0.f;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      e[i][j] = 512 * i + 8 * lane + j < n_scanned ? expf(e[i][j] - m) : 0.f;
+      l += e[i][j];
+    }
+  }
+  l = wave_sum(l);
+  const float pu = round_bf16(1.0f / (float)capacity);
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int s0 = 512 * i + 8 * lane;
+    if (s0 < slots) {
+      uint32_t pw[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float p0, p1;
+        if (masked) {
+          p0 = s0 + 2 * j < capacity ? pu : 0.f;
+          p1 = s0 + 2 * j + 1 < capacity ? pu : 0.f;
+        } else {
+          p0 = e[i][2 * j] / l;
+          p1 = e[i][2 * j + 1] / l;
+        }
+        pw[j] = f32_to_bf16_bits(p0) | (f32_to_bf16_bits(p1) << 16);
+      }
+      *reinterpret_cast<u32x4*>(sp + hh * stride + s0) = u32x4{pw[0], pw[1], pw[2], pw[3]};
+    }
+  }
+  return masked;
+}
+
+// LDS row stride (bf16 entries) of the values kernel's probabilities: 64 bytes of padding spread
+// the R rows over the banks.
+__host__ __device__ constexpr int tp_lds_stride(int nch) { return nch * 32 + 32; }
+
+// grid: pairs x D / (16 kTpWavesV). NCH >= ceil(capacity / 32): V^T chunks held in registers.
+template <int D, int NCH>
+__global__ __launch_bounds__(kTpWavesV * 64) void decode_bf16_tp_values_kernel(G4DecodeArgs a, const uint16_t* ws,
+                                                                              int row_slots) {
+  constexpr int kParts = D / 16 / kTpWavesV;  // workgroups per pair
+  static_assert(kParts >= 1 && kParts * kTpWavesV * 16 == D, "one 16-row d-block of V^T per wave");
+  constexpr int NB = (NCH + 15) / 16;  // 512-slot blocks of a score row
+  constexpr int kStride = tp_lds_stride(NCH);
+  extern __shared__ float smem[];
+  uint16_t* sp = reinterpret_cast<uint16_t*>(smem);  // [R][kStride] probabilities
+  const int R = a.group;
+  const int pair = (int)(blockIdx.x / kParts), part = (int)(blockIdx.x % kParts);
+  const int b = pair / a.kv_heads;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const int db = part * kTpWavesV + w;  // value dims [16*db, 16*db + 16)
+  const KeyRange kr = key_range(a, b);
+  const int n_chunks = (kr.n_keys + 31) >> 5;
+  const int n_scanned = n_chunks << 5;
+  const int64_t ss = a.slot_stride;
+  const __amdgpu_buffer_rsrc_t rv =
+      make_rsrc(reinterpret_cast<const uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride,
+                (uint32_t)a.slot_stride * D * 2u);
+  const uint16_t* srow = ws + (int64_t)pair * R * row_slots;
+
+  // requests: the score row of head w (head 0 for a wave without a head of its own: it needs only
+  // the row's validity), then NCH V^T loads. All NCH are issued (a chunk past the row's scanned
+  // ones re-reads the last scanned chunk, an L2 hit), so the wait for the score row counts
+  // exactly the loads behind it.
+  const int h0 = w < R ? w : 0;
+  u32x4 sv[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    sv[i] = u32x4{0u, 0u, 0u, 0u};
+    if (512 * i + 8 * lane < row_slots) sv[i] = load16(srow + h0 * row_slots + 512 * i + 8 * lane);
+  }
+  const uint32_t soff = (uint32_t)(16 * db * ss) * 2u;
+  const int c_last = n_chunks > 0 ? n_chunks - 1 : 0;
+  u32x4 vv[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+    vv[c] = buffer_load16(rv, (uint32_t)(col * ss + ((c < n_chunks ? c : c_last) << 5) + 8 * grp) * 2u, soff);
+
+  // exact probabilities: head w first; heads w + 4, w + 8, ... (R > 4) from rows loaded afterwards
+  const bool all_masked = tp_probabilities<NB>(sv, w, w < R, sp, kStride, NCH * 32, n_scanned, a.capacity, lane);
+  for (int hh = w + kTpWavesV; hh < R; hh += kTpWavesV) {
+    u32x4 sh[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      sh[i] = u32x4{0u, 0u, 0u, 0u};
+      if (512 * i + 8 * lane < row_slots) sh[i] = load16(srow + hh * row_slots + 512 * i + 8 * lane);
+    }
+    tp_probabilities<NB>(sh, hh, true, sp, kStride, NCH * 32, n_scanned, a.capacity, lane);
+  }
+  wg_barrier();  // probabilities are in LDS (the V^T loads stay in flight)
+
+  floatx4 oacc = {0.f, 0.f, 0.f, 0.f}, oacc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < NCH; c += 2) {
+    if (c < n_chunks)
+      oacc = mfma16x16x32(as_bf16x8(vv[c]), prob_operand(sp, kStride, (c << 5) + 8 * grp, R, col), oacc);
+    if (c + 1 < n_chunks)
+      oacc1 = mfma16x16x32(as_bf16x8(vv[c + 1]), prob_operand(sp, kStride, ((c + 1) << 5) + 8 * grp, R, col), oacc1);
+  }
+  oacc += oacc1;
+  // a fully masked row averages every slot below the capacity, including ones never scanned
+  if (all_masked) {
+    const int cap_chunks = (a.capacity + 31) >> 5;
+    for (int c = n_chunks; c < cap_chunks; ++c) {
+      const u32x4 v = buffer_load16(rv, (uint32_t)(col * ss + (c << 5) + 8 * grp) * 2u, soff);
+      oacc = mfma16x16x32(as_bf16x8(v), prob_operand(sp, kStride, (c << 5) + 8 * grp, R, col), oacc);
+    }
+  }
+  // lane (grp, col < R) holds O^T[d = 16*db + 4*grp + j][head col]
+  if (col < R) {
+    uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)pair * R + col) * D;
+    const uint32_t w0 = f32_to_bf16_bits(oacc[0]) | (f32_to_bf16_bits(oacc[1]) << 16);
+    const uint32_t w1 = f32_to_bf16_bits(oacc[2]) | (f32_to_bf16_bits(oacc[3]) << 16);
+    *reinterpret_cast<uint2*>(orow + 16 * db + 4 * grp) = make_uint2(w0, w1);
+  }
+}

@@ -137,7 +137,8 @@ typedef struct G4DecodeArgs {
   size_t workspace_bytes;
   int32_t num_splits;   /* 0 = choose automatically; 1 or 2 = workgroups per (b, kv head), one
                            pass, each owning a slice of the head dim (2: head dim 256);
-                           G4_DECODE_SPLIT_KEYS = split the key range (bf16, head dims 128/256) */
+                           G4_DECODE_SPLIT_KEYS = split the key range (bf16, head dims 128/256);
+                           G4_DECODE_TWO_PASS = scores and values in two launches (rows <= 1024) */
 } G4DecodeArgs;
 
 /* num_splits value: split-K over 512-slot key ranges in three launches (scores, values,
@@ -145,6 +146,13 @@ typedef struct G4DecodeArgs {
  * choice takes it for bf16 rows longer than 512 slots when B * Hkv < 256 or when a one-pass
  * row does not fit in LDS. */
 #define G4_DECODE_SPLIT_KEYS (-1)
+
+/* num_splits value: two stream-ordered launches for rows of at most 1024 slots (bf16, head dims
+ * 128/256): the first scores K chunk by chunk into the workspace, the second forms the exact
+ * probabilities and runs the value product, one wave per 16-row block of V^T. Uses the
+ * workspace (bf16 scores [B * Hkv][R][512 or 1024]). The automatic choice takes it for such rows
+ * when B * Hkv >= 256. */
+#define G4_DECODE_TWO_PASS (-2)
 
 /* Bytes of workspace the call described by args needs (0 when the chosen path uses none). The
  * workspace is plain scratch: no state is kept in it between calls. */

@@ -110,6 +110,11 @@ def _decode_args(**kw):
     (dict(num_splits=3), "num_splits"),
     (dict(num_splits=_lib.G4_DECODE_SPLIT_KEYS), "split-K needs"),
     (dict(num_splits=2, head_dim=128), "num_splits 2 with head_dim 128"),
+    (dict(num_splits=-3), "num_splits"),
+    (dict(num_splits=_lib.G4_DECODE_TWO_PASS, capacity=1040, slot_stride=1088, kind=_lib.G4_CACHE_LINEAR),
+     "two-pass needs bf16"),
+    (dict(num_splits=_lib.G4_DECODE_TWO_PASS, head_dim=64), "two-pass needs bf16"),
+    (dict(num_splits=_lib.G4_DECODE_TWO_PASS, dtype=_lib.G4_DTYPE_F32), "two-pass needs bf16"),
 ])
 def test_decode_rejects_invalid_arguments(override, match):
     a = _decode_args(**override)
@@ -135,6 +140,26 @@ def test_decode_split_keys_workspace():
     # ring rows of 512 slots and one-pass choices need none
     assert L.g4_decode_workspace_size(ctypes.byref(_decode_args())) == 0
     assert L.g4_decode_workspace_size(ctypes.byref(_decode_args(**long_rows, num_splits=1))) == 0
+
+
+def test_decode_two_pass_workspace():
+    """The two-launch path keeps bf16 scores [B * Hkv][R][512] in the workspace and refuses to run
+    without enough of it."""
+
+    L = _lib.lib()
+    a = _decode_args(num_splits=_lib.G4_DECODE_TWO_PASS, batch=64)
+    need = L.g4_decode_workspace_size(ctypes.byref(a))
+    assert need == 64 * 2 * 4 * 512 * 2
+    # rows of 513..1024 slots keep 1024-slot score rows; the automatic choice takes the path for
+    # >= 256 (b, kv head) pairs and leaves fewer to the one-launch kernels (no workspace)
+    linear = dict(kind=_lib.G4_CACHE_LINEAR, capacity=768, slot_stride=768, key_mask_stride=768)
+    assert L.g4_decode_workspace_size(ctypes.byref(_decode_args(**linear, batch=128))) == 128 * 2 * 4 * 1024 * 2
+    assert L.g4_decode_workspace_size(ctypes.byref(_decode_args(batch=127))) == 0
+    assert L.g4_decode_workspace_size(ctypes.byref(_decode_args(batch=127, num_splits=1))) == 0
+    assert L.g4_decode_attention(ctypes.byref(a), None) == _lib.G4_ERR_WORKSPACE
+    assert re.search("two-pass needs .* workspace", L.g4_last_error().decode())
+    a = _decode_args(num_splits=_lib.G4_DECODE_TWO_PASS, batch=64, workspace=1, workspace_bytes=need - 1)
+    assert L.g4_decode_attention(ctypes.byref(a), None) == _lib.G4_ERR_WORKSPACE
 
 
 def test_append_and_prefill_reject_invalid_arguments():

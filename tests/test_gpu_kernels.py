@@ -156,10 +156,12 @@ def _decode_case(device, dtype, *, B, H, R, D, cap, ring, window, q_pos, key_mas
     return err
 
 
-@pytest.mark.parametrize("fused,num_splits", [(False, 0), (True, 0), (True, 1), (True, 2)])
+@pytest.mark.parametrize("fused,num_splits", [(False, 0), (True, 0), (True, 1), (True, 2),
+                                               (False, _lib.G4_DECODE_TWO_PASS), (True, _lib.G4_DECODE_TWO_PASS)])
 def test_decode_ring_config2_shape(device, fused, num_splits):
     """BASELINE config 2: B64, Hq8/Hkv2, D256, W512 ring that has wrapped several times;
-    per-row write positions U[1536, 2048). num_splits 1/2: one or two workgroups per (b, kv head)."""
+    per-row write positions U[1536, 2048). num_splits 1/2: one or two workgroups per (b, kv head);
+    G4_DECODE_TWO_PASS: scores and values in two launches."""
 
     rng = np.random.default_rng(2)
     B, H, R, D, W = 64, 2, 4, 256, 512
@@ -186,10 +188,11 @@ def test_decode_linear_long_rows(device, D, num_splits):
                  fused=True, seed=23, num_splits=num_splits)
 
 
-@pytest.mark.parametrize("ring,cap", [(True, 512), (False, 768)])
-def test_decode_e2b_batch(device, ring, cap):
+@pytest.mark.parametrize("ring,cap,num_splits", [(True, 512, 0), (False, 768, 0), (True, 512, 2), (False, 768, 2)])
+def test_decode_e2b_batch(device, ring, cap, num_splits):
     """The E2B decode shape the rollout runs: B256 x Hkv2 = 512 pairs, ring 512 (sliding layers)
-    and linear 768 (global layers), ragged write positions, a left-padded row, a finished row."""
+    and linear 768 (global layers), ragged write positions, a left-padded row, a finished row.
+    num_splits 0: the library's choice (two launches at this many pairs); 2: one launch."""
 
     rng = np.random.default_rng(11)
     B, H, R, D = 256, 2, 4, 256
@@ -199,7 +202,43 @@ def test_decode_e2b_batch(device, ring, cap):
     key_mask[3, :50] = False
     key_mask[7, 400:] = False
     _decode_case(device, O.BF16, B=B, H=H, R=R, D=D, cap=cap, ring=ring, window=512 if ring else 0, q_pos=q_pos,
-                 key_mask=key_mask, fused=True, seed=26)
+                 key_mask=key_mask, fused=True, seed=26, num_splits=num_splits)
+
+
+@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("ring,cap", [(True, 48), (False, 48), (False, 768), (False, 1000), (True, 1024)])
+def test_decode_two_pass_edge_rows(device, D, ring, cap):
+    """G4_DECODE_TWO_PASS on rows shorter than the capacity (16, 24 and 32 chunks of V^T in
+    registers): ring not yet full, left padding, a finished row, a fully masked row (uniform
+    average over the capacity, including never-scanned slots), a row whose only valid key is the
+    appended one."""
+
+    B, H, R = 5, 2, 4
+    sc = cap // 48
+    q_pos = np.array([5, 20, 40, 33, 9]) * sc
+    key_mask = np.ones((B, cap), bool)
+    key_mask[1, :3 * sc] = False
+    key_mask[2, 30 * sc:] = False
+    key_mask[3, :] = False
+    key_mask[4, :9 * sc] = False
+    _decode_case(device, O.BF16, B=B, H=H, R=R, D=D, cap=cap, ring=ring, window=cap if ring else 0, q_pos=q_pos,
+                 key_mask=key_mask, fused=True, seed=27, num_splits=_lib.G4_DECODE_TWO_PASS)
+
+
+@pytest.mark.parametrize("R,W", [(1, 512), (2, 512), (8, 512), (16, 512), (4, 768), (16, 1024)])
+def test_decode_two_pass_group_sizes(device, R, W):
+    """G4_DECODE_TWO_PASS with 1..16 query heads per KV head: values waves with no head of their
+    own (R < 4) and waves with several (R > 4); a wrapped ring of 512..1024 slots, one row fully
+    masked."""
+
+    rng = np.random.default_rng(12)
+    B, H, D = 6, 2, 256
+    q_pos = rng.integers(600, 1400, B)
+    key_mask = np.ones((B, 1400), bool)
+    key_mask[2, :] = False
+    key_mask[4, 700:] = False
+    _decode_case(device, O.BF16, B=B, H=H, R=R, D=D, cap=W, ring=True, window=W, q_pos=q_pos, key_mask=key_mask,
+                 fused=True, seed=28, num_splits=_lib.G4_DECODE_TWO_PASS)
 
 
 @pytest.mark.parametrize("D", [128, 256])
