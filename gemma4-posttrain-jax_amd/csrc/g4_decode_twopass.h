@@ -161,9 +161,9 @@ __global__ __launch_bounds__(kTpWavesV * 64) void decode_bf16_tp_values_kernel(G
   const uint16_t* srow = ws + (int64_t)pair * R * row_slots;
 
   // requests: the score row of head w (head 0 for a wave without a head of its own: it needs only
-  // the row's validity), then NCH V^T loads. All NCH are issued (a chunk past the row's scanned
-  // ones re-reads the last scanned chunk, an L2 hit), so the wait for the score row counts
-  // exactly the loads behind it.
+  // the row's validity), then NCH V^T loads. All NCH are issued, so the wait for the score row
+  // counts exactly the loads behind it; a chunk past the row's scanned ones is read at an offset
+  // beyond the buffer resource's size, which returns zeros without a memory request.
   const int h0 = w < R ? w : 0;
   u32x4 sv[NB];
 #pragma unroll
@@ -172,11 +172,11 @@ __global__ __launch_bounds__(kTpWavesV * 64) void decode_bf16_tp_values_kernel(G
     if (512 * i + 8 * lane < row_slots) sv[i] = load16(srow + h0 * row_slots + 512 * i + 8 * lane);
   }
   const uint32_t soff = (uint32_t)(16 * db * ss) * 2u;
-  const int c_last = n_chunks > 0 ? n_chunks - 1 : 0;
+  const uint32_t pair_bytes = (uint32_t)a.slot_stride * D * 2u;  // the resource's size: offsets from here read 0
   u32x4 vv[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
-    vv[c] = buffer_load16(rv, (uint32_t)(col * ss + ((c < n_chunks ? c : c_last) << 5) + 8 * grp) * 2u, soff);
+    vv[c] = buffer_load16(rv, c < n_chunks ? (uint32_t)(col * ss + (c << 5) + 8 * grp) * 2u : pair_bytes, soff);
 
   // exact probabilities: head w first; heads w + 4, w + 8, ... (R > 4) from rows loaded afterwards
   const bool all_masked = tp_probabilities<NB>(sv, w, w < R, sp, kStride, NCH * 32, n_scanned, a.capacity, lane);
