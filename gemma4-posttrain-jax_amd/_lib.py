@@ -71,6 +71,13 @@ class G4SampleArgs(ctypes.Structure):
     ]
 
 
+class G4LinearArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", c_void_p), ("w", c_void_p), ("y", c_void_p), ("m", c_int32), ("n", c_int32), ("k", c_int32),
+        ("ldy", c_int32), ("ksplit", c_int32), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
 PROTOTYPES = {
     "g4_kv_append": (c_int32, [POINTER(G4AppendArgs), c_void_p]),
     "g4_decode_workspace_size": (c_size_t, [POINTER(G4DecodeArgs)]),
@@ -83,6 +90,10 @@ PROTOTYPES = {
     "g4_residual_norm": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_float, c_void_p, c_void_p, c_void_p]),
     "g4_gelu_mul": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
+    "g4_residual_norm_splitk": (c_int32, [c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
+                                          c_void_p, c_float, c_void_p, c_void_p, c_void_p]),
+    "g4_linear_workspace_size": (c_size_t, [POINTER(G4LinearArgs)]),
+    "g4_linear_bf16": (c_int32, [POINTER(G4LinearArgs), c_void_p]),
     "g4_convert_f32_to_bf16": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "g4_convert_bf16_to_f32": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p]),
     "g4_last_error": (c_char_p, []),
@@ -133,6 +144,6 @@ def ring_slot_positions(last_written: int, window_capacity: int) -> list[int]:
 
 
 __all__ = [
-    "G4AppendArgs", "G4DecodeArgs", "G4PrefillArgs", "G4Error", "PROTOTYPES", "LIB_PATH", "lib", "check",
+    "G4AppendArgs", "G4DecodeArgs", "G4PrefillArgs", "G4LinearArgs", "G4Error", "PROTOTYPES", "LIB_PATH", "lib", "check",
     "kv_source_layers", "ring_slot_positions", "c_uint8",
 ]

@@ -201,6 +201,7 @@ __global__ __launch_bounds__(64) void rms_norm_wave_kernel(int cols, const uint1
 // own LDS slots, so one barrier each. Same rounding points as the kernels above.
 constexpr int kRowThreads = 256;
 constexpr int kRowGroups = 2;  // 8-column groups per thread: cols <= 256 * 8 * 2 = 4096
+constexpr int kMaxNormSplits = 8;  // f32 partial rows a split-K branch may arrive in
 
 __device__ __forceinline__ float row_sum(float v, float* red4) {
   v = wave_sum(v);
@@ -209,8 +210,12 @@ __device__ __forceinline__ float row_sum(float v, float* red4) {
   return (red4[0] + red4[1]) + (red4[2] + red4[3]);
 }
 
-template <int G>
+// KS = 0: the branch is a bf16 row. KS > 0: the branch is bf16(sum of ksplit <= KS f32 partial
+// rows [ksplit][rows][cols], added in split order) -- the split-K projection's output, formed here
+// instead of in a separate pass.
+template <int G, int KS>
 __global__ __launch_bounds__(kRowThreads) void residual_norm_row_kernel(int cols, const uint16_t* branch,
+                                                                        const float* partials, int ksplit,
                                                                         const uint16_t* branch_weight,
                                                                         const uint16_t* residual, const float* scalar,
                                                                         const uint16_t* next_weight, float eps,
@@ -224,13 +229,42 @@ __global__ __launch_bounds__(kRowThreads) void residual_norm_row_kernel(int cols
   for (int j = 0; j < G; ++j) {  // every load of the row up front: one memory round trip
     const int g = t + kRowThreads * j;
     u32x4 a = {0u, 0u, 0u, 0u}, b = a, c = a, d = a;
+    floatx4 pl[KS > 0 ? KS : 1][2];
     if (g < ng) {
-      a = load16(branch + base + 8 * g);
+      if (KS == 0) {
+        a = load16(branch + base + 8 * g);
+      } else {
+        const int64_t plane = (int64_t)gridDim.x * cols;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          if (s < ksplit) {
+            const floatx4* p = reinterpret_cast<const floatx4*>(partials + s * plane + base + 8 * g);
+            pl[s][0] = p[0];
+            pl[s][1] = p[1];
+          }
+        }
+      }
       b = load16(residual + base + 8 * g);
       if (branch_weight) c = load16(branch_weight + 8 * g);
       if (next_out && next_weight) d = load16(next_weight + 8 * g);
     }
-    unpack8(a, v[j]);
+    if (KS == 0 || g >= ng) {
+      unpack8(a, v[j]);
+    } else {
+      floatx4 lo = pl[0][0], hi = pl[0][1];
+#pragma unroll
+      for (int s = 1; s < KS; ++s) {
+        if (s < ksplit) {
+          lo += pl[s][0];
+          hi += pl[s][1];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[j][e] = round_bf16(lo[e]);
+        v[j][4 + e] = round_bf16(hi[e]);
+      }
+    }
     unpack8(b, r[j]);
     unpack8(c, wb[j]);
     unpack8(d, wn[j]);
@@ -342,9 +376,10 @@ extern "C" int g4_residual_norm(int dtype, int rows, int cols, const void* branc
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (vec_rows(dtype, cols, {branch, branch_weight, residual, next_weight, residual_out, next_out}) &&
       cols <= kRowThreads * 8 * kRowGroups) {
-    const auto kern = cols <= kRowThreads * 8 ? residual_norm_row_kernel<1> : residual_norm_row_kernel<2>;
+    const auto kern = cols <= kRowThreads * 8 ? residual_norm_row_kernel<1, 0> : residual_norm_row_kernel<2, 0>;
     hipLaunchKernelGGL(kern, dim3(rows), dim3(kRowThreads), 0, st, cols, reinterpret_cast<const uint16_t*>(branch),
-                       reinterpret_cast<const uint16_t*>(branch_weight), reinterpret_cast<const uint16_t*>(residual),
+                       (const float*)nullptr, 0, reinterpret_cast<const uint16_t*>(branch_weight),
+                       reinterpret_cast<const uint16_t*>(residual),
                        scalar, reinterpret_cast<const uint16_t*>(next_weight), eps,
                        reinterpret_cast<uint16_t*>(residual_out), reinterpret_cast<uint16_t*>(next_out));
   } else if (dtype == G4_DTYPE_BF16)
@@ -354,6 +389,32 @@ extern "C" int g4_residual_norm(int dtype, int rows, int cols, const void* branc
     hipLaunchKernelGGL(residual_norm_kernel<false>, dim3(rows), dim3(kFuseThreads), 0, st, cols, branch,
                        branch_weight, residual, scalar, next_weight, eps, residual_out, next_out);
   return check_launch("g4_residual_norm");
+}
+
+extern "C" int g4_residual_norm_splitk(int rows, int cols, const float* partials, int ksplit,
+                                       const void* branch_weight, const void* residual, const float* scalar,
+                                       const void* next_weight, float eps, void* residual_out, void* next_out,
+                                       void* stream) {
+  using namespace g4;
+  if (int rc = check_rows("g4_residual_norm_splitk", G4_DTYPE_BF16, rows, cols)) return rc;
+  if (ksplit < 1 || ksplit > kMaxNormSplits)
+    return fail(G4_ERR_UNSUPPORTED, "g4_residual_norm_splitk: ksplit %d (1..%d)", ksplit, kMaxNormSplits);
+  if (!partials || !residual || !residual_out)
+    return fail(G4_ERR_INVALID, "g4_residual_norm_splitk: NULL partials/residual/out");
+  if (!vec_rows(G4_DTYPE_BF16, cols, {branch_weight, residual, next_weight, residual_out, next_out}) ||
+      (reinterpret_cast<uintptr_t>(partials) & 15) || cols > kRowThreads * 8 * kRowGroups)
+    return fail(G4_ERR_UNSUPPORTED,
+                "g4_residual_norm_splitk: cols %d (a multiple of 8, <= %d) and 16-byte aligned rows needed", cols,
+                kRowThreads * 8 * kRowGroups);
+  if (rows == 0) return G4_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const auto kern = cols <= kRowThreads * 8 ? residual_norm_row_kernel<1, kMaxNormSplits>
+                                            : residual_norm_row_kernel<2, kMaxNormSplits>;
+  hipLaunchKernelGGL(kern, dim3(rows), dim3(kRowThreads), 0, st, cols, (const uint16_t*)nullptr, partials, ksplit,
+                     reinterpret_cast<const uint16_t*>(branch_weight), reinterpret_cast<const uint16_t*>(residual),
+                     scalar, reinterpret_cast<const uint16_t*>(next_weight), eps,
+                     reinterpret_cast<uint16_t*>(residual_out), reinterpret_cast<uint16_t*>(next_out));
+  return check_launch("g4_residual_norm_splitk");
 }
 
 extern "C" int g4_gelu_mul(int dtype, int rows, int cols, const void* gate_up, void* out, void* stream) {

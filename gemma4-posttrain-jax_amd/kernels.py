@@ -334,6 +334,71 @@ def sample_tokens(logits: torch.Tensor, *, softcap: float | None, temperature: f
     return token_out, logp_out
 
 
+def _linear_call(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None, ksplit: int) -> torch.Tensor | None:
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or x.dim() != 2 or w.dim() != 2:
+        raise ValueError("linear needs 2-D bf16 x and w")
+    if not x.is_contiguous() or not w.is_contiguous() or x.shape[1] != w.shape[1]:
+        raise ValueError(f"x {tuple(x.shape)} and w {tuple(w.shape)} must be contiguous with equal k")
+    m, k = x.shape
+    n = w.shape[0]
+    if out is not None and (out.dtype != x.dtype or out.dim() != 2 or tuple(out.shape) != (m, n) or out.stride(1) != 1):
+        raise ValueError("out must be a bf16 [m, n] tensor with unit inner stride")
+    a = _lib.G4LinearArgs(x=_ptr(x), w=_ptr(w), y=_ptr(out), m=m, n=n, k=k, ldy=out.stride(0) if out is not None else 0,
+                          ksplit=ksplit, workspace=None, workspace_bytes=0)
+    need = _lib.lib().g4_linear_workspace_size(ctypes.byref(a))
+    ws = None
+    if need:
+        ws = torch.empty(need // 4, dtype=torch.float32, device=x.device)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), need
+    _lib.check(_lib.lib().g4_linear_bf16(ctypes.byref(a), _stream()), "g4_linear_bf16")
+    return ws
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, *, out: torch.Tensor | None = None, ksplit: int = 1) -> torch.Tensor:
+    """g4_linear_bf16: ``x [m, k] @ w[n, k]^T`` in bf16 with f32 accumulation (m <= 256, the decode
+    batch); ``ksplit`` > 1 splits k across workgroups (partials in a workspace from torch's caching
+    allocator, added in split order)."""
+
+    if out is None:
+        out = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=x.device)
+    _linear_call(x, w, out, ksplit)
+    return out
+
+
+def linear_partials(x: torch.Tensor, w: torch.Tensor, *, ksplit: int) -> torch.Tensor:
+    """g4_linear_bf16 without y: the f32 partial sums ``[ksplit, m, n]`` of ``x @ w^T`` over ksplit
+    k ranges (for ``residual_norm_splitk``)."""
+
+    if ksplit < 2:
+        raise ValueError("linear_partials needs ksplit >= 2")
+    ws = _linear_call(x, w, None, ksplit)
+    return ws.view(ksplit, x.shape[0], w.shape[0])
+
+
+def residual_norm_splitk(partials: torch.Tensor, branch_weight: torch.Tensor | None, residual: torch.Tensor, *,
+                         scalar: torch.Tensor | None, next_weight: torch.Tensor | None,
+                         eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """g4_residual_norm_splitk: ``residual_norm`` whose branch is ``bf16(partials.sum(0))`` (added in
+    split order); ``partials`` f32 ``[ksplit, rows, cols]``, residual bf16 ``[..., cols]``."""
+
+    if partials.dtype != torch.float32 or partials.dim() != 3 or not partials.is_contiguous():
+        raise ValueError("partials must be a contiguous f32 [ksplit, rows, cols] tensor")
+    ks, rows, cols = partials.shape
+    if residual.dtype != torch.bfloat16 or residual.numel() != rows * cols or not residual.is_contiguous():
+        raise ValueError("residual must be a contiguous bf16 tensor of rows x cols elements")
+    for w in (branch_weight, next_weight):
+        if w is not None and (w.dtype != residual.dtype or w.numel() != cols or not w.is_contiguous()):
+            raise ValueError("norm weights must be contiguous [cols] tensors in the activation dtype")
+    if scalar is not None and (scalar.dtype != torch.float32 or scalar.numel() != 1):
+        raise ValueError("scalar must be a one-element f32 tensor")
+    x = torch.empty_like(residual)
+    h = torch.empty_like(residual)
+    _lib.check(_lib.lib().g4_residual_norm_splitk(rows, cols, _ptr(partials), ks, _ptr(branch_weight), _ptr(residual),
+                                                  _ptr(scalar), _ptr(next_weight), eps, _ptr(x), _ptr(h), _stream()),
+               "g4_residual_norm_splitk")
+    return x, h
+
+
 def convert_f32_to_bf16(x: torch.Tensor, *, nonfinite: torch.Tensor | None = None) -> torch.Tensor:
     """g4_convert_f32_to_bf16: the reference's bitwise round-to-nearest-even cast of an f32 tensor
     (any shape) to bf16. ``nonfinite`` (int32 [1] on the device) is set to 1 if an input is inf /

@@ -192,6 +192,20 @@ def pack_weights(params: Gemma4TextParams, config: Gemma4TextConfig) -> PackedWe
     return packed
 
 
+# K splits of the decode-batch down projection (measured best at M=256, N=2048, K=8192: 8 splits,
+# 256 workgroups; hipBLASLt's tile re-reads each weight block once per 32-row tile)
+DOWN_KSPLIT = 8
+
+
+def _split_down(act: torch.Tensor, w_t: torch.Tensor) -> bool:
+    """Whether the down projection runs as g4_linear_bf16 split-K partials fed to the residual norm:
+    a bf16 decode batch of at most 256 rows and shapes the kernels take."""
+
+    n, k = w_t.shape
+    return (act.dtype == torch.bfloat16 and act.shape[0] <= 256 and n % 64 == 0 and n % 8 == 0 and n <= 4096
+            and k % (64 * DOWN_KSPLIT) == 0 and act.is_contiguous() and w_t.is_contiguous())
+
+
 def _proj(x: torch.Tensor, w_t: torch.Tensor) -> torch.Tensor:
     """``x [T, K] . w_t[N, K]^T`` in x's dtype (hipBLASLt; the [N, K] weight layout is its faster
     one for the prefill shapes and equal at decode)."""
@@ -358,8 +372,17 @@ def forward_gemma4_text(
                                      next_weight=lp.pre_feedforward_norm.weight, eps=eps)
         gu = _proj(h.reshape(B * S, -1), pk.w_gate_up_t)
         act = kernels.gelu_mul(gu)
-        d = _proj(act, pk.w_down_t).reshape(B, S, -1)
         next_w = params.layers[i + 1].input_norm.weight if i + 1 < n_layers else params.final_norm.weight
+        if lp.per_layer_input is None and _split_down(act, pk.w_down_t):
+            # decode batch: the down projection's split-K partial sums go straight into the
+            # post-feedforward norm + residual (+ layer scalar) + next norm
+            part = kernels.linear_partials(act, pk.w_down_t, ksplit=DOWN_KSPLIT)
+            x, h = kernels.residual_norm_splitk(part, lp.post_feedforward_norm.weight, x, scalar=pk.scalar_f32,
+                                                next_weight=next_w, eps=eps)
+            if layer_outputs is not None:
+                layer_outputs.append(x)
+            continue
+        d = _proj(act, pk.w_down_t).reshape(B, S, -1)
         if lp.per_layer_input is None:
             # post-feedforward norm + residual, layer scalar, then the next layer's input norm
             # (the final norm after the last layer)

@@ -256,6 +256,43 @@ int g4_residual_norm(int dtype, int rows, int cols, const void* branch, const vo
 int g4_gelu_mul(int dtype, int rows, int cols, const void* gate_up, void* out, void* stream);
 
 /*
+ * g4_residual_norm_splitk: g4_residual_norm (bf16) whose branch arrives as ksplit <= 8 f32 partial
+ * rows [ksplit][rows][cols] (16-byte aligned): branch = bf16(partials[0] + ... + partials[ksplit-1])
+ * added in that order -- the y g4_linear_bf16 would have written. The MLP's down projection at
+ * decode (model.py:393-396, 546-553) feeds it without a separate pass over the partials.
+ */
+int g4_residual_norm_splitk(int rows, int cols, const float* partials, int ksplit, const void* branch_weight,
+                            const void* residual, const float* scalar, const void* next_weight, float eps,
+                            void* residual_out, void* next_out, void* stream);
+
+/*
+ * Decode-step projection: y[m, n] = bf16(sum_k x[m, k] * w[n, k]), f32 accumulation, for the
+ * rollout's decode batch (m <= 256 rows). Replaces the q/k/v, o, gate/up and down projections of
+ * forward_attention / forward_mlp (model.py:463-482, 500, 393-396) at S = 1, where the reference's
+ * einsums (XLA dots, f32 accumulation, bf16 result) multiply one token per row. x [m, k] row-major
+ * (16-byte aligned), w [n, k] row-major (the packed, output-major weight), y [m, ldy] (8-byte
+ * aligned). n a multiple of 64, k a multiple of 64 * ksplit. ksplit > 1 splits k over that many
+ * workgroups per column block; their f32 partial sums are added in split order (workspace
+ * [ksplit][m][n] f32, g4_linear_workspace_size bytes). With ksplit > 1 and y == NULL the partial
+ * sums are left in the workspace (for g4_residual_norm_splitk).
+ */
+typedef struct G4LinearArgs {
+  const void* x;
+  const void* w;
+  void* y;
+  int32_t m;
+  int32_t n;
+  int32_t k;
+  int32_t ldy;
+  int32_t ksplit;
+  void* workspace;
+  size_t workspace_bytes;
+} G4LinearArgs;
+
+size_t g4_linear_workspace_size(const G4LinearArgs* args);
+int g4_linear_bf16(const G4LinearArgs* args, void* stream);
+
+/*
  * Rollout weight handoff. g4_convert_f32_to_bf16: out[i] = bf16 bits of in[i], round to nearest
  * even on the raw bits, (bits + 0x7FFF + ((bits >> 16) & 1)) >> 16 — the conversion of
  * inference_device.py:10-45 (device_converter), equal to the astype(bfloat16) of

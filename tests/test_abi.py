@@ -162,6 +162,54 @@ def test_decode_two_pass_workspace():
     assert L.g4_decode_attention(ctypes.byref(a), None) == _lib.G4_ERR_WORKSPACE
 
 
+def _linear_args(**kw):
+    base = dict(x=16, w=16, y=16, m=256, n=2048, k=8192, ldy=2048, ksplit=1, workspace=None, workspace_bytes=0)
+    base.update(kw)
+    return _lib.G4LinearArgs(**base)
+
+
+@pytest.mark.parametrize("override,match", [
+    (dict(x=None), "NULL"),
+    (dict(m=257), "m 257"),
+    (dict(m=0), "m 0"),
+    (dict(n=100, ldy=100), "n 100"),
+    (dict(k=8192 + 32), "k 8224"),
+    (dict(ksplit=3), "k 8192 .* ksplit 3"),
+    (dict(ksplit=0), "ksplit 0"),
+    (dict(ldy=1024), "ldy"),
+    (dict(y=18), "alignment"),
+    (dict(ksplit=8), "workspace"),
+])
+def test_linear_rejects_invalid_arguments(override, match):
+    a = _linear_args(**override)
+    rc = _lib.lib().g4_linear_bf16(ctypes.byref(a), None)
+    assert rc in (_lib.G4_ERR_INVALID, _lib.G4_ERR_UNSUPPORTED, _lib.G4_ERR_WORKSPACE)
+    assert re.search(match, _lib.lib().g4_last_error().decode())
+
+
+@pytest.mark.parametrize("override,match", [
+    (dict(ksplit=9), "ksplit 9"),
+    (dict(ksplit=0), "ksplit 0"),
+    (dict(partials=None), "NULL"),
+    (dict(partials=8), "aligned"),
+    (dict(cols=4104), "cols 4104"),
+    (dict(cols=12), "cols 12"),
+])
+def test_residual_norm_splitk_rejects_invalid_arguments(override, match):
+    a = dict(rows=4, cols=2048, partials=16, ksplit=8, branch_weight=16, residual=16, scalar=None, next_weight=16,
+             eps=1e-6, residual_out=16, next_out=16, stream=None)
+    a.update(override)
+    rc = _lib.lib().g4_residual_norm_splitk(*a.values())
+    assert rc in (_lib.G4_ERR_INVALID, _lib.G4_ERR_UNSUPPORTED)
+    assert re.search(match, _lib.lib().g4_last_error().decode())
+
+
+def test_linear_workspace_size():
+    L = _lib.lib()
+    assert L.g4_linear_workspace_size(ctypes.byref(_linear_args())) == 0
+    assert L.g4_linear_workspace_size(ctypes.byref(_linear_args(ksplit=8))) == 8 * 256 * 2048 * 4
+
+
 def test_append_and_prefill_reject_invalid_arguments():
     L = _lib.lib()
     a = _lib.G4AppendArgs(dtype=_lib.G4_DTYPE_BF16, kind=_lib.G4_CACHE_LINEAR, batch=1, seq=10, kv_heads=1, group=0,

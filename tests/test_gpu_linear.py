@@ -1,0 +1,67 @@
+"""g4_linear_bf16 (the decode-step projection GEMM) against an fp32 reference of the same product.
+
+The bar: |y - x.w^T| <= 2^-8 |x.w^T| + 1e-5 elementwise, i.e. the bf16 rounding of an f32-accumulated
+dot product (half an ulp is 2^-9 relative) plus summation-order slack."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gemma4_posttrain_jax_amd import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(m, n, k, ksplit, seed, ldy=None):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn((n, k), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    out = None
+    if ldy is not None:
+        out = torch.full((m, ldy), float("nan"), device="cuda", dtype=torch.bfloat16)[:, :n]
+    y = kernels.linear(x, w, out=out, ksplit=ksplit)
+    ref = x.double().cpu() @ w.double().cpu().T
+    err = (y.double().cpu() - ref).abs()
+    bar = ref.abs() * 2.0 ** -8 + 1e-5
+    assert torch.all(err <= bar), f"max excess {(err - bar).max().item():.3g} (max err {err.max().item():.3g})"
+    if ldy is not None:  # columns past n untouched
+        assert torch.isnan(out.as_strided((m, ldy), (ldy, 1))[:, n:].float()).all()
+
+
+@pytest.mark.parametrize("n,k,ksplit", [(16384, 2048, 1), (2048, 8192, 8), (3072, 2048, 4), (2048, 2048, 1),
+                                        (2048, 8192, 1)])
+def test_linear_e2b_projection_shapes(device, n, k, ksplit):
+    """The E2B decode projections at B=256: gate/up, down (split 8), q/k/v, o; down unsplit."""
+
+    _check(256, n, k, ksplit, seed=n + k + ksplit)
+
+
+@pytest.mark.parametrize("m", [1, 17, 64, 200])
+def test_linear_partial_row_blocks(device, m):
+    """Fewer rows than the 256-row tile (rows past m read as zero, never stored); split-K; a
+    strided output with columns past n left untouched."""
+
+    _check(m, 192, 640, 5 if m != 64 else 1, seed=m, ldy=256)
+
+
+@pytest.mark.parametrize("rows,cols,k,ksplit,with_scalar", [(256, 2048, 8192, 8, True), (37, 4096, 1536, 3, False),
+                                                            (5, 64, 512, 2, True)])
+def test_residual_norm_splitk_equals_unfused(device, rows, cols, k, ksplit, with_scalar):
+    """The down projection's partial sums fed straight into the residual norm give the same bits
+    as g4_linear_bf16's own split-K sum followed by g4_residual_norm (same split order, same
+    rounding points)."""
+
+    g = torch.Generator(device="cuda").manual_seed(rows + cols)
+    act = torch.randn((rows, k), device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn((cols, k), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    res = torch.randn((rows, cols), device="cuda", generator=g).to(torch.bfloat16)
+    bw = (1 + 0.1 * torch.randn(cols, device="cuda", generator=g)).to(torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn(cols, device="cuda", generator=g)).to(torch.bfloat16)
+    scalar = torch.tensor([0.75], device="cuda") if with_scalar else None
+    part = kernels.linear_partials(act, w, ksplit=ksplit)
+    x1, h1 = kernels.residual_norm_splitk(part, bw, res, scalar=scalar, next_weight=nw, eps=1e-6)
+    y = kernels.linear(act, w, ksplit=ksplit)
+    x2, h2 = kernels.residual_norm(y, bw, res, scalar=scalar, next_weight=nw, eps=1e-6)
+    assert torch.equal(x1.view(torch.int16), x2.view(torch.int16))
+    assert torch.equal(h1.view(torch.int16), h2.view(torch.int16))
