@@ -78,6 +78,16 @@ class G4LinearArgs(ctypes.Structure):
     ]
 
 
+class G4PrologueArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_int32), ("hidden", c_int32), ("vocab", c_int32), ("key_mask_stride", c_int32),
+        ("tokens", c_void_p), ("positions", c_void_p), ("active", c_void_p), ("slot", c_void_p),
+        ("key_mask", c_void_p), ("embed", c_void_p), ("embed_scale", c_float), ("n_tables", c_int32),
+        ("rot_dim", c_int32 * 2), ("inv_freq", c_void_p * 2), ("cos_out", c_void_p * 2), ("sin_out", c_void_p * 2),
+        ("x_out", c_void_p),
+    ]
+
+
 PROTOTYPES = {
     "g4_kv_append": (c_int32, [POINTER(G4AppendArgs), c_void_p]),
     "g4_decode_workspace_size": (c_size_t, [POINTER(G4DecodeArgs)]),
@@ -92,6 +102,7 @@ PROTOTYPES = {
     "g4_gelu_mul": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "g4_residual_norm_splitk": (c_int32, [c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
                                           c_void_p, c_float, c_void_p, c_void_p, c_void_p]),
+    "g4_decode_prologue": (c_int32, [POINTER(G4PrologueArgs), c_void_p]),
     "g4_linear_workspace_size": (c_size_t, [POINTER(G4LinearArgs)]),
     "g4_linear_bf16": (c_int32, [POINTER(G4LinearArgs), c_void_p]),
     "g4_convert_f32_to_bf16": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
@@ -144,6 +155,6 @@ def ring_slot_positions(last_written: int, window_capacity: int) -> list[int]:
 
 
 __all__ = [
-    "G4AppendArgs", "G4DecodeArgs", "G4PrefillArgs", "G4LinearArgs", "G4Error", "PROTOTYPES", "LIB_PATH", "lib", "check",
+    "G4AppendArgs", "G4DecodeArgs", "G4PrefillArgs", "G4LinearArgs", "G4PrologueArgs", "G4Error", "PROTOTYPES", "LIB_PATH", "lib", "check",
     "kv_source_layers", "ring_slot_positions", "c_uint8",
 ]

@@ -89,6 +89,19 @@ __device__ __forceinline__ u32x4 load16(const uint16_t* p) { return *reinterpret
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// 8 bf16 values (one 16-byte word) <-> 8 floats (exact widening; narrowing rounds to nearest even).
+__device__ __forceinline__ void unpack8(u32x4 w, float (&f)[8]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    f[2 * q] = __uint_as_float(w[q] << 16);
+    f[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
+  return u32x4{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])};
+}
+
 // Raw buffer access (gfx9 resource word 3 = 0x00020000): base and size live in SGPRs, each lane
 // supplies a 32-bit byte offset, and a uniform offset rides in soffset. Reads at or beyond
 // `bytes` return zero instead of touching memory.

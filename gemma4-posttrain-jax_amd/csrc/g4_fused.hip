@@ -137,18 +137,6 @@ __global__ __launch_bounds__(kFuseThreads) void gelu_mul_kernel(int64_t n, int c
 // wave shuffles, so there is no LDS and no barrier. Same rounding points as the kernels above.
 constexpr int kWaveGroups = 8;  // 8-column groups per lane: cols <= 64 * 8 * 8 = 4096
 
-__device__ __forceinline__ void unpack8(u32x4 w, float (&f)[8]) {
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    f[2 * q] = __uint_as_float(w[q] << 16);
-    f[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
-  }
-}
-
-__device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
-  return u32x4{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])};
-}
-
 // The lane's groups of a weight row, loaded up front (with the data, one memory round trip).
 __device__ __forceinline__ void load_weight_groups(u32x4 (&w)[kWaveGroups], int ngroups, const uint16_t* weight) {
   const int lane = threadIdx.x & 63;

@@ -334,6 +334,39 @@ def sample_tokens(logits: torch.Tensor, *, softcap: float | None, temperature: f
     return token_out, logp_out
 
 
+def decode_prologue(embed: torch.Tensor, tokens: torch.Tensor, positions: torch.Tensor, active: torch.Tensor,
+                    slot: torch.Tensor, key_mask: torch.Tensor, *, embed_scale: float,
+                    inv_freq: list[torch.Tensor]) -> tuple[torch.Tensor, list[tuple[torch.Tensor, torch.Tensor]]]:
+    """g4_decode_prologue: ``x = bf16(embed[tokens] * embed_scale)`` ``[B, M]``, ``key_mask[b, slot[b]] =
+    active[b]`` in place, and per ``inv_freq`` table the f32 rotary ``(cos, sin)`` ``[B, D]`` of
+    ``positions``. tokens / positions / slot: int32 ``[B]``, active: bool ``[B]``."""
+
+    B = tokens.shape[0]
+    if embed.dtype != torch.bfloat16 or embed.dim() != 2 or not embed.is_contiguous():
+        raise ValueError("embed must be a contiguous bf16 [vocab, hidden] tensor")
+    for name, t, dt in (("tokens", tokens, torch.int32), ("positions", positions, torch.int32),
+                        ("slot", slot, torch.int32), ("active", active, torch.bool)):
+        if t.dtype != dt or tuple(t.shape) != (B,):
+            raise ValueError(f"{name} must be a [{B}] {dt} tensor")
+    tokens, positions, slot, active = (t.contiguous() for t in (tokens, positions, slot, active))
+    if key_mask.dtype != torch.bool or key_mask.dim() != 2 or key_mask.shape[0] != B or key_mask.stride(1) != 1:
+        raise ValueError("key_mask must be a [B, C] bool tensor with unit inner stride")
+    if len(inv_freq) > 2 or any(f.dtype != torch.float32 or f.dim() != 1 or not f.is_contiguous() for f in inv_freq):
+        raise ValueError("inv_freq: at most two contiguous f32 [D/2] tensors")
+    x = torch.empty((B, embed.shape[1]), dtype=embed.dtype, device=embed.device)
+    tables = [(torch.empty((B, 2 * f.numel()), dtype=torch.float32, device=embed.device),
+               torch.empty((B, 2 * f.numel()), dtype=torch.float32, device=embed.device)) for f in inv_freq]
+    a = _lib.G4PrologueArgs(batch=B, hidden=embed.shape[1], vocab=embed.shape[0], key_mask_stride=key_mask.stride(0),
+                            tokens=_ptr(tokens), positions=_ptr(positions), active=_ptr(active), slot=_ptr(slot),
+                            key_mask=_ptr(key_mask), embed=_ptr(embed), embed_scale=embed_scale,
+                            n_tables=len(inv_freq), x_out=_ptr(x))
+    for i, (f, (c, sn)) in enumerate(zip(inv_freq, tables)):
+        a.rot_dim[i] = 2 * f.numel()
+        a.inv_freq[i], a.cos_out[i], a.sin_out[i] = _ptr(f), _ptr(c), _ptr(sn)
+    _lib.check(_lib.lib().g4_decode_prologue(ctypes.byref(a), _stream()), "g4_decode_prologue")
+    return x, tables
+
+
 def _linear_call(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None, ksplit: int) -> torch.Tensor | None:
     if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or x.dim() != 2 or w.dim() != 2:
         raise ValueError("linear needs 2-D bf16 x and w")

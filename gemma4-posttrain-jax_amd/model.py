@@ -139,6 +139,7 @@ class PackedWeights(NamedTuple):
     layers: tuple
     embed_scale: torch.Tensor  # bf16/f32 scalar sqrt(M) rounded to the param dtype (model.py:600)
     inv_freq: dict  # layer type -> f32 [D/2] device tensor (model.py:294-302)
+    embed_scale_f: float  # the same rounded scale as a host float (no device read inside a graph)
 
 
 _PACKED: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
@@ -186,7 +187,8 @@ def pack_weights(params: Gemma4TextParams, config: Gemma4TextConfig) -> PackedWe
     dev = params.embed_tokens.device
     dt = params.embed_tokens.dtype
     inv = {k: torch.from_numpy(v).to(dev) for k, v in _rope_inv_freq(config).items()}
-    packed = PackedWeights(tuple(layers), torch.tensor(math.sqrt(config.hidden_size), dtype=dt, device=dev), inv)
+    scale = torch.tensor(math.sqrt(config.hidden_size), dtype=dt)
+    packed = PackedWeights(tuple(layers), scale.to(dev), inv, float(scale.float()))
     _PACKED_BY_ID.clear()  # one live params object at a time (rollout reuses the same weights)
     _PACKED_BY_ID[key] = (params, packed)
     return packed
@@ -293,9 +295,22 @@ def forward_gemma4_text(
         attention_mask = torch.ones((B, S), dtype=torch.bool, device=dev)
     attention_mask = attention_mask.to(torch.bool)
 
-    x = params.embed_tokens[input_ids.long()]
-    x = (x.float() * pw.embed_scale.float()).to(x.dtype)
-    pli = _per_layer_inputs(params, config, input_ids.long(), x) if config.hidden_size_per_layer_input else None
+    # graphed decode step: the embedding, key-mask update and rotary tables in one native launch
+    fused_prologue = (write_pos is not None and cache_mode == "append" and kv_cache is not None and S == 1
+                      and params.embed_tokens.dtype == torch.bfloat16 and not config.hidden_size_per_layer_input
+                      and params.embed_tokens.shape[1] % 8 == 0)
+    if fused_prologue:
+        tabs = (SLIDING, FULL)
+        x, tables = kernels.decode_prologue(
+            params.embed_tokens, input_ids[:, 0], position_ids[:, 0], attention_mask[:, 0], write_pos,
+            kv_cache.key_mask, embed_scale=pw.embed_scale_f, inv_freq=[pw.inv_freq[t] for t in tabs])
+        x = x.view(B, 1, -1)
+        rot = {t: (c.view(B, 1, -1), sn.view(B, 1, -1)) for t, (c, sn) in zip(tabs, tables)}
+        pli = None
+    else:
+        x = params.embed_tokens[input_ids.long()]
+        x = (x.float() * pw.embed_scale.float()).to(x.dtype)
+        pli = _per_layer_inputs(params, config, input_ids.long(), x) if config.hidden_size_per_layer_input else None
 
     scratch_cache = kv_cache is None
     if scratch_cache:
@@ -308,13 +323,15 @@ def forward_gemma4_text(
         if cache_mode != "append":
             raise ValueError("write_pos is only used in append mode")
         key_mask = kv_cache.key_mask
-        key_mask.scatter_(1, write_pos[:, None].long(), attention_mask)
+        if not fused_prologue:
+            key_mask.scatter_(1, write_pos[:, None].long(), attention_mask)
         slot = write_pos
     else:
         key_mask = kv_cache.key_mask.clone()
         key_mask[:, length:length + S] = attention_mask
         slot = length
-    rot = {t: rotary_tables(pw.inv_freq[t], position_ids) for t in (SLIDING, FULL)}
+    if not fused_prologue:
+        rot = {t: rotary_tables(pw.inv_freq[t], position_ids) for t in (SLIDING, FULL)}
     sources = kv_source_layers(config)
 
     flags_q = _lib.G4_APPEND_NORM_Q | _lib.G4_APPEND_ROPE_Q

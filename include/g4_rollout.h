@@ -266,6 +266,38 @@ int g4_residual_norm_splitk(int rows, int cols, const float* partials, int kspli
                             void* residual_out, void* next_out, void* stream);
 
 /*
+ * One decode step's input glue in one launch. Replaces the embedding lookup and scale
+ * (model.py:599-600), the key-mask update at the write slot (model.py:608-610) and the rotary
+ * tables of forward_gemma4_text (model.py:288-306, 624-627) for S = 1:
+ *   x_out[b]       = bf16(f32(embed[tokens[b]]) * embed_scale)      (ids clamped to the table)
+ *   key_mask[b, slot[b]] = active[b]                                 (slots outside the row: no write)
+ *   cos_out[i][b, d] = cos(f32(positions[b]) * inv_freq[i][d mod rot_dim[i]/2]), sin_out likewise
+ * for n_tables <= 2 tables (one per layer type). embed [vocab, hidden] bf16, x_out [batch, hidden]
+ * bf16, both 16-byte aligned; hidden a multiple of 8; cos/sin [batch, rot_dim[i]] f32.
+ */
+typedef struct G4PrologueArgs {
+  int32_t batch;
+  int32_t hidden;
+  int32_t vocab;
+  int32_t key_mask_stride;
+  const int32_t* tokens;     /* device [B] */
+  const int32_t* positions;  /* device [B] logical RoPE positions */
+  const uint8_t* active;     /* device [B] (bool) */
+  const int32_t* slot;       /* device [B] physical write positions */
+  uint8_t* key_mask;         /* device [B, key_mask_stride] */
+  const void* embed;
+  float embed_scale;
+  int32_t n_tables;
+  int32_t rot_dim[2];
+  const float* inv_freq[2];
+  float* cos_out[2];
+  float* sin_out[2];
+  void* x_out;
+} G4PrologueArgs;
+
+int g4_decode_prologue(const G4PrologueArgs* args, void* stream);
+
+/*
  * Decode-step projection: y[m, n] = bf16(sum_k x[m, k] * w[n, k]), f32 accumulation, for the
  * rollout's decode batch (m <= 256 rows). Replaces the q/k/v, o, gate/up and down projections of
  * forward_attention / forward_mlp (model.py:463-482, 500, 393-396) at S = 1, where the reference's

@@ -204,6 +204,27 @@ def test_residual_norm_splitk_rejects_invalid_arguments(override, match):
     assert re.search(match, _lib.lib().g4_last_error().decode())
 
 
+def test_decode_prologue_rejects_invalid_arguments():
+    L = _lib.lib()
+
+    def args(**kw):
+        base = dict(batch=2, hidden=64, vocab=10, key_mask_stride=8, tokens=16, positions=16, active=16, slot=16,
+                    key_mask=16, embed=16, embed_scale=8.0, n_tables=1, x_out=16)
+        base.update(kw)
+        a = _lib.G4PrologueArgs(**base)
+        a.rot_dim[0], a.inv_freq[0], a.cos_out[0], a.sin_out[0] = 64, 16, 16, 16
+        return a
+
+    for kw, match in [(dict(hidden=60), "hidden 60"), (dict(tokens=None), "NULL"), (dict(embed=8), "alignment"),
+                      (dict(n_tables=3), "n_tables 3"), (dict(key_mask_stride=0), "key_mask_stride")]:
+        assert L.g4_decode_prologue(ctypes.byref(args(**kw)), None) == _lib.G4_ERR_INVALID
+        assert re.search(match, L.g4_last_error().decode())
+    a = args()
+    a.rot_dim[0] = 63
+    assert L.g4_decode_prologue(ctypes.byref(a), None) == _lib.G4_ERR_INVALID
+    assert re.search("rotary table 0", L.g4_last_error().decode())
+
+
 def test_linear_workspace_size():
     L = _lib.lib()
     assert L.g4_linear_workspace_size(ctypes.byref(_linear_args())) == 0
