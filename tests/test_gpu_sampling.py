@@ -147,3 +147,19 @@ def test_generate_matches_oracle_rollout(device, temperature, top_k, top_p):
     np.testing.assert_array_equal(rb.completion_ids.cpu().numpy(), orb.completion_ids)
     # the fp32 model bar (2e-5 x max|logit|) at logits bounded by the soft-cap 30
     np.testing.assert_allclose(rb.rollout_logps.cpu().numpy(), orb.rollout_logps, rtol=0, atol=2e-5 * 30)
+
+
+@pytest.mark.parametrize("scale", [1.0, 4.0])
+def test_draws_over_long_rows_follow_the_jax_stream(device, scale):
+    """Rows of 32776 columns (32 full steps of the vectorized loop and a partial one), normal
+    logits of standard deviation 1 and 4: the noise of columns that provably stay below the wave's
+    best perturbed score is skipped, which must not change a single draw."""
+
+    rng = np.random.default_rng(5)
+    x = (scale * rng.standard_normal((48, 32776))).astype(np.float32)
+    key = _key([3, 99], device)
+    tok, logp = kernels.sample_tokens(torch.from_numpy(x).to(device), softcap=None, temperature=1.0, key=key)
+    _, sub = JR.split(np.uint32([3, 99]))
+    want_tok, want_logp = O.sample_token(x, temperature=1.0, key=sub)
+    np.testing.assert_array_equal(tok.cpu().numpy(), want_tok)
+    np.testing.assert_allclose(logp.cpu().numpy(), want_logp, rtol=0, atol=LOGP_ATOL)
