@@ -24,6 +24,8 @@ G4_APPEND_NORM_Q = 8
 G4_APPEND_ROPE_Q = 16
 G4_DECODE_SPLIT_KEYS = -1
 G4_DECODE_TWO_PASS = -2
+G4_LINEAR_PLAIN = 0
+G4_LINEAR_GELU_MUL = 1
 G4_ERR_INVALID = -1
 G4_ERR_UNSUPPORTED = -2
 G4_ERR_LAUNCH = -3
@@ -75,6 +77,7 @@ class G4LinearArgs(ctypes.Structure):
     _fields_ = [
         ("x", c_void_p), ("w", c_void_p), ("y", c_void_p), ("m", c_int32), ("n", c_int32), ("k", c_int32),
         ("ldy", c_int32), ("ksplit", c_int32), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+        ("epilogue", c_int32),
     ]
 
 

@@ -89,6 +89,15 @@ __device__ __forceinline__ u32x4 load16(const uint16_t* p) { return *reinterpret
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// gelu_tanh(g) * u in f32 (model.py:393-396; jax.nn.gelu(approximate=True)), g and u already
+// rounded to the activation dtype; shared by the MLP activation kernel and the gate/up epilogue.
+__device__ __forceinline__ float gelu_tanh_mul(float g, float u) {
+  const float kBeta = 0.7978845608028654f;  // sqrt(2 / pi)
+  const float kKappa = 0.044715f;
+  const float inner = kBeta * (g + kKappa * g * g * g);
+  return 0.5f * g * (1.0f + tanhf(inner)) * u;
+}
+
 // 8 bf16 values (one 16-byte word) <-> 8 floats (exact widening; narrowing rounds to nearest even).
 __device__ __forceinline__ void unpack8(u32x4 w, float (&f)[8]) {
 #pragma unroll

@@ -120,15 +120,11 @@ __global__ __launch_bounds__(kFuseThreads) void gelu_mul_kernel(int64_t n, int c
                                                                 void* out) {
   using E = Elem<BF16>;
   using T = typename E::T;
-  const float kBeta = 0.7978845608028654f;  // sqrt(2 / pi)
-  const float kKappa = 0.044715f;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t row = i / cols, c = i - row * cols;
     const float g = E::load(reinterpret_cast<const T*>(gate_up), row * 2 * cols + c);
     const float u = E::load(reinterpret_cast<const T*>(gate_up), row * 2 * cols + cols + c);
-    const float inner = kBeta * (g + kKappa * g * g * g);
-    const float gelu = 0.5f * g * (1.0f + tanhf(inner));
-    E::store(reinterpret_cast<T*>(out), i, gelu * u);
+    E::store(reinterpret_cast<T*>(out), i, gelu_tanh_mul(g, u));
   }
 }
 
@@ -295,18 +291,13 @@ __global__ __launch_bounds__(kRowThreads) void residual_norm_row_kernel(int cols
 // out = round(gelu_tanh(gate) * up), 8 columns per thread per step (bf16, cols % 8 == 0)
 __global__ __launch_bounds__(kFuseThreads) void gelu_mul_vec_kernel(int64_t n8, int cols8, const uint16_t* gate_up,
                                                                     uint16_t* out) {
-  const float kBeta = 0.7978845608028654f;  // sqrt(2 / pi)
-  const float kKappa = 0.044715f;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t row = i / cols8, c8 = i - row * cols8;
     float g[8], u[8], y[8];
     unpack8(load16(gate_up + (row * 2 * cols8 + c8) * 8), g);
     unpack8(load16(gate_up + (row * 2 * cols8 + cols8 + c8) * 8), u);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float inner = kBeta * (g[e] + kKappa * g[e] * g[e] * g[e]);
-      y[e] = 0.5f * g[e] * (1.0f + tanhf(inner)) * u[e];
-    }
+    for (int e = 0; e < 8; ++e) y[e] = gelu_tanh_mul(g[e], u[e]);
     *reinterpret_cast<u32x4*>(out + 8 * i) = pack8(y);
   }
 }

@@ -42,18 +42,20 @@ typedef unsigned char StageBuf[kStageBytes];
 
 // DMA of stage `st` (K offset k0) into `buf`: wave w moves groups w, w + 4, ... of X then of W.
 // Lane l of a group instruction takes row 8 g + l / 8 and the 16-byte piece (l % 8) ^ (row % 8) of
-// its 128-byte K slice. Past the last stage every load reads beyond its resource (zeros, no
+// its 128-byte K slice. W group j (rows 8 j .. 8 j + 7 of the tile) starts at weight row
+// wrow[j >> 2] + 8 (j & 3). Past the last stage every load reads beyond its resource (zeros, no
 // memory request), so every wave always issues kDmaPerWave loads per stage.
 __device__ __forceinline__ void gemm_dma(unsigned char* __restrict__ buf, __amdgpu_buffer_rsrc_t rx,
                                          __amdgpu_buffer_rsrc_t rw, int K, int k0, bool live, uint32_t oob_x,
-                                         uint32_t oob_w, int w, int lane) {
+                                         uint32_t oob_w, int w, int lane, int wrow0, int wrow1) {
   const int rl = lane >> 3;                       // row within the group
   const int kc = (lane & 7) ^ rl;                 // 16-byte piece this lane fetches (row % 8 == rl)
 #pragma unroll
   for (int i = 0; i < kDmaPerWave; ++i) {
     const int g = w + 4 * i;  // groups 0..31: X, 32..39: W
     const bool is_x = g < kXGroups;
-    const int row = 8 * (is_x ? g : g - kXGroups) + rl;
+    const int gw = g - kXGroups;
+    const int row = is_x ? 8 * g + rl : (gw < 4 ? wrow0 : wrow1) + 8 * (gw & 3) + rl;
     const uint32_t off = (uint32_t)(row * K + k0 + 8 * kc) * 2u;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(is_x ? rx : rw,
                                              (__attribute__((address_space(3))) void*)(buf + g * kGroupBytes), 16,
@@ -91,15 +93,16 @@ __device__ __forceinline__ void gemm_step(unsigned char* __restrict__ cur, unsig
                                           unsigned char* __restrict__ fre, floatx4 (&acc)[4][4],
                                           __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw, int K, int kbeg,
                                           int s, int nst, uint32_t oob_x, uint32_t oob_w, int w, int lane, int col,
-                                          int grp) {
+                                          int grp, int wrow0, int wrow1) {
   (void)nxt;
   // this wave's DMAs of stage s have landed (stage s + 1's may not have), then every wave's
   __asm__ volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kDmaPerWave) : "memory");
-  gemm_dma(fre, rx, rw, K, kbeg + (s + 2) * kGemmKT, s + 2 < nst, oob_x, oob_w, w, lane);
+  gemm_dma(fre, rx, rw, K, kbeg + (s + 2) * kGemmKT, s + 2 < nst, oob_x, oob_w, w, lane, wrow0, wrow1);
   gemm_compute(cur, acc, w, col, grp);
 }
 
-// grid: (N / 64) x ksplit. K / ksplit must be a multiple of 64.
+// grid: (N / 64) x ksplit. K / ksplit must be a multiple of 64. With the gated-GELU epilogue the
+// workgroup's 64 weight rows are 32 gate rows and the 32 up rows of the same output columns.
 __global__ __launch_bounds__(kGemmThreads) void linear_bf16_kernel(G4LinearArgs a, float* partials) {
   __shared__ __attribute__((aligned(1024))) StageBuf b0, b1, b2;
   const int lane = threadIdx.x & 63;
@@ -112,9 +115,14 @@ __global__ __launch_bounds__(kGemmThreads) void linear_bf16_kernel(G4LinearArgs 
   const int kbeg = split * kper;
   const int nst = kper / kGemmKT;
   const uint32_t xbytes = (uint32_t)a.m * (uint32_t)K * 2u;  // rows >= M read as zeros
-  const uint32_t wbytes = (uint32_t)kGemmCols * (uint32_t)K * 2u;
+  const uint32_t wbytes = (uint32_t)a.n * (uint32_t)K * 2u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, xbytes);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(reinterpret_cast<const uint16_t*>(a.w) + (int64_t)n0 * K, wbytes);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, wbytes);
+  const bool gelu = a.epilogue == G4_LINEAR_GELU_MUL;
+  const int half = a.n / 2;
+  // weight rows of tile groups 0..3 and 4..7
+  const int wrow0 = gelu ? (int)blockIdx.x * 32 : n0;
+  const int wrow1 = gelu ? half + (int)blockIdx.x * 32 : n0 + 32;
 
   floatx4 acc[4][4];
 #pragma unroll
@@ -122,16 +130,35 @@ __global__ __launch_bounds__(kGemmThreads) void linear_bf16_kernel(G4LinearArgs 
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  gemm_dma(b0, rx, rw, K, kbeg, true, xbytes, wbytes, w, lane);
-  gemm_dma(b1, rx, rw, K, kbeg + kGemmKT, nst > 1, xbytes, wbytes, w, lane);
+  gemm_dma(b0, rx, rw, K, kbeg, true, xbytes, wbytes, w, lane, wrow0, wrow1);
+  gemm_dma(b1, rx, rw, K, kbeg + kGemmKT, nst > 1, xbytes, wbytes, w, lane, wrow0, wrow1);
   for (int s = 0; s < nst; s += 3) {
-    gemm_step(b0, b1, b2, acc, rx, rw, K, kbeg, s, nst, xbytes, wbytes, w, lane, col, grp);
-    if (s + 1 < nst) gemm_step(b1, b2, b0, acc, rx, rw, K, kbeg, s + 1, nst, xbytes, wbytes, w, lane, col, grp);
-    if (s + 2 < nst) gemm_step(b2, b0, b1, acc, rx, rw, K, kbeg, s + 2, nst, xbytes, wbytes, w, lane, col, grp);
+    gemm_step(b0, b1, b2, acc, rx, rw, K, kbeg, s, nst, xbytes, wbytes, w, lane, col, grp, wrow0, wrow1);
+    if (s + 1 < nst)
+      gemm_step(b1, b2, b0, acc, rx, rw, K, kbeg, s + 1, nst, xbytes, wbytes, w, lane, col, grp, wrow0, wrow1);
+    if (s + 2 < nst)
+      gemm_step(b2, b0, b1, acc, rx, rw, K, kbeg, s + 2, nst, xbytes, wbytes, w, lane, col, grp, wrow0, wrow1);
   }
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the trailing (zero) DMAs
 
   // lane (grp, col) holds Y[m = 64 w + 16 rb + col][n = n0 + 16 cb + 4 grp + j]
+  if (gelu) {  // cb 0, 1: gate columns; cb 2, 3: the up columns of the same outputs
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const int m = 64 * w + 16 * rb + col;
+      if (m < a.m) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          float y[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) y[j] = gelu_tanh_mul(round_bf16(acc[rb][cb][j]), round_bf16(acc[rb][cb + 2][j]));
+          uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + (int64_t)m * a.ldy + (int)blockIdx.x * 32 + 16 * cb + 4 * grp;
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb) {
     const int m = 64 * w + 16 * rb + col;
@@ -182,9 +209,14 @@ extern "C" int g4_linear_bf16(const G4LinearArgs* args, void* stream) {
   if (a.ksplit < 1 || a.ksplit > 64) return fail(G4_ERR_INVALID, "g4_linear_bf16: ksplit %d (1..64)", a.ksplit);
   if (a.k <= 0 || a.k % (kGemmKT * a.ksplit))
     return fail(G4_ERR_UNSUPPORTED, "g4_linear_bf16: k %d (a multiple of %d x ksplit %d)", a.k, kGemmKT, a.ksplit);
-  if ((int64_t)a.m * a.k * 2 >= (int64_t)1 << 31 || (int64_t)kGemmCols * a.k * 2 >= (int64_t)1 << 31)
+  if ((int64_t)a.m * a.k * 2 >= (int64_t)1 << 31 || (int64_t)a.n * a.k * 2 >= (int64_t)1 << 31)
     return fail(G4_ERR_UNSUPPORTED, "g4_linear_bf16: operands beyond 2 GiB");
-  if (a.y && (a.ldy < a.n || a.ldy % 4))
+  if (a.epilogue != G4_LINEAR_PLAIN && a.epilogue != G4_LINEAR_GELU_MUL)
+    return fail(G4_ERR_INVALID, "g4_linear_bf16: epilogue %d", a.epilogue);
+  if (a.epilogue == G4_LINEAR_GELU_MUL && (a.ksplit != 1 || !a.y))
+    return fail(G4_ERR_UNSUPPORTED, "g4_linear_bf16: the gated-GELU epilogue needs ksplit 1 and y");
+  const int ycols = a.epilogue == G4_LINEAR_GELU_MUL ? a.n / 2 : a.n;
+  if (a.y && (a.ldy < ycols || a.ldy % 4))
     return fail(G4_ERR_INVALID, "g4_linear_bf16: ldy %d (>= n, a multiple of 4)", a.ldy);
   if ((reinterpret_cast<uintptr_t>(a.y) & 7) || (reinterpret_cast<uintptr_t>(a.x) & 15) ||
       (reinterpret_cast<uintptr_t>(a.w) & 15))

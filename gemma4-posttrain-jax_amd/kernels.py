@@ -367,17 +367,19 @@ def decode_prologue(embed: torch.Tensor, tokens: torch.Tensor, positions: torch.
     return x, tables
 
 
-def _linear_call(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None, ksplit: int) -> torch.Tensor | None:
+def _linear_call(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None, ksplit: int,
+                 epilogue: int = _lib.G4_LINEAR_PLAIN) -> torch.Tensor | None:
     if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or x.dim() != 2 or w.dim() != 2:
         raise ValueError("linear needs 2-D bf16 x and w")
     if not x.is_contiguous() or not w.is_contiguous() or x.shape[1] != w.shape[1]:
         raise ValueError(f"x {tuple(x.shape)} and w {tuple(w.shape)} must be contiguous with equal k")
     m, k = x.shape
     n = w.shape[0]
-    if out is not None and (out.dtype != x.dtype or out.dim() != 2 or tuple(out.shape) != (m, n) or out.stride(1) != 1):
-        raise ValueError("out must be a bf16 [m, n] tensor with unit inner stride")
+    ny = n // 2 if epilogue == _lib.G4_LINEAR_GELU_MUL else n
+    if out is not None and (out.dtype != x.dtype or out.dim() != 2 or tuple(out.shape) != (m, ny) or out.stride(1) != 1):
+        raise ValueError(f"out must be a bf16 [{m}, {ny}] tensor with unit inner stride")
     a = _lib.G4LinearArgs(x=_ptr(x), w=_ptr(w), y=_ptr(out), m=m, n=n, k=k, ldy=out.stride(0) if out is not None else 0,
-                          ksplit=ksplit, workspace=None, workspace_bytes=0)
+                          ksplit=ksplit, workspace=None, workspace_bytes=0, epilogue=epilogue)
     need = _lib.lib().g4_linear_workspace_size(ctypes.byref(a))
     ws = None
     if need:
@@ -395,6 +397,16 @@ def linear(x: torch.Tensor, w: torch.Tensor, *, out: torch.Tensor | None = None,
     if out is None:
         out = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=x.device)
     _linear_call(x, w, out, ksplit)
+    return out
+
+
+def linear_gelu(x: torch.Tensor, w_gate_up: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """g4_linear_bf16 with the gated-GELU epilogue: ``w_gate_up [2F, k]`` = gate rows then up rows;
+    returns ``bf16(gelu_tanh(g) * u)`` ``[m, F]`` with g / u the bf16 gate / up products."""
+
+    if out is None:
+        out = torch.empty((x.shape[0], w_gate_up.shape[0] // 2), dtype=x.dtype, device=x.device)
+    _linear_call(x, w_gate_up, out, 1, _lib.G4_LINEAR_GELU_MUL)
     return out
 
 

@@ -208,6 +208,16 @@ def _split_down(act: torch.Tensor, w_t: torch.Tensor) -> bool:
             and k % (64 * DOWN_KSPLIT) == 0 and act.is_contiguous() and w_t.is_contiguous())
 
 
+def _native_gate_up(h: torch.Tensor, w_t: torch.Tensor) -> bool:
+    """Whether the gate/up projection + gated GELU run as one g4_linear_bf16 launch (its
+    gated-GELU epilogue): a bf16 decode batch of at most 256 rows and shapes the kernel takes."""
+
+    n, k = w_t.shape
+    rows = h.numel() // h.shape[-1]
+    return (h.dtype == torch.bfloat16 and rows <= 256 and n % 64 == 0 and k % 64 == 0 and h.is_contiguous()
+            and w_t.is_contiguous())
+
+
 def _proj(x: torch.Tensor, w_t: torch.Tensor) -> torch.Tensor:
     """``x [T, K] . w_t[N, K]^T`` in x's dtype (hipBLASLt; the [N, K] weight layout is its faster
     one for the prefill shapes and equal at decode)."""
@@ -387,8 +397,11 @@ def forward_gemma4_text(
         # post-attention norm + residual, then the pre-feedforward norm (one pass)
         x, h = kernels.residual_norm(o, lp.post_attention_norm.weight, x, scalar=None,
                                      next_weight=lp.pre_feedforward_norm.weight, eps=eps)
-        gu = _proj(h.reshape(B * S, -1), pk.w_gate_up_t)
-        act = kernels.gelu_mul(gu)
+        if _native_gate_up(h, pk.w_gate_up_t):  # decode batch: projection and activation in one launch
+            act = kernels.linear_gelu(h.reshape(B * S, -1), pk.w_gate_up_t)
+        else:
+            gu = _proj(h.reshape(B * S, -1), pk.w_gate_up_t)
+            act = kernels.gelu_mul(gu)
         next_w = params.layers[i + 1].input_norm.weight if i + 1 < n_layers else params.final_norm.weight
         if lp.per_layer_input is None and _split_down(act, pk.w_down_t):
             # decode batch: the down projection's split-K partial sums go straight into the

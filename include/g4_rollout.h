@@ -307,7 +307,13 @@ int g4_decode_prologue(const G4PrologueArgs* args, void* stream);
  * workgroups per column block; their f32 partial sums are added in split order (workspace
  * [ksplit][m][n] f32, g4_linear_workspace_size bytes). With ksplit > 1 and y == NULL the partial
  * sums are left in the workspace (for g4_residual_norm_splitk).
+ * epilogue G4_LINEAR_GELU_MUL (ksplit 1): w holds n = 2F rows, gate rows [0, F) then up rows
+ * [F, 2F) (the packed gate/up weight); y [m, F] = bf16(gelu_tanh(g) * u) with g, u the bf16-rounded
+ * gate / up products -- forward_mlp's projection and activation (model.py:393-396) in one launch.
  */
+#define G4_LINEAR_PLAIN 0
+#define G4_LINEAR_GELU_MUL 1
+
 typedef struct G4LinearArgs {
   const void* x;
   const void* w;
@@ -319,6 +325,7 @@ typedef struct G4LinearArgs {
   int32_t ksplit;
   void* workspace;
   size_t workspace_bytes;
+  int32_t epilogue;  /* G4_LINEAR_PLAIN or G4_LINEAR_GELU_MUL */
 } G4LinearArgs;
 
 size_t g4_linear_workspace_size(const G4LinearArgs* args);

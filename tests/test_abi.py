@@ -163,7 +163,8 @@ def test_decode_two_pass_workspace():
 
 
 def _linear_args(**kw):
-    base = dict(x=16, w=16, y=16, m=256, n=2048, k=8192, ldy=2048, ksplit=1, workspace=None, workspace_bytes=0)
+    base = dict(x=16, w=16, y=16, m=256, n=2048, k=8192, ldy=2048, ksplit=1, workspace=None, workspace_bytes=0,
+                epilogue=_lib.G4_LINEAR_PLAIN)
     base.update(kw)
     return _lib.G4LinearArgs(**base)
 
@@ -179,6 +180,9 @@ def _linear_args(**kw):
     (dict(ldy=1024), "ldy"),
     (dict(y=18), "alignment"),
     (dict(ksplit=8), "workspace"),
+    (dict(epilogue=2), "epilogue 2"),
+    (dict(epilogue=_lib.G4_LINEAR_GELU_MUL, ksplit=2, workspace=16, workspace_bytes=1 << 30), "gated-GELU"),
+    (dict(epilogue=_lib.G4_LINEAR_GELU_MUL, ldy=1020), "ldy 1020"),
 ])
 def test_linear_rejects_invalid_arguments(override, match):
     a = _linear_args(**override)

@@ -65,3 +65,24 @@ def test_residual_norm_splitk_equals_unfused(device, rows, cols, k, ksplit, with
     x2, h2 = kernels.residual_norm(y, bw, res, scalar=scalar, next_weight=nw, eps=1e-6)
     assert torch.equal(x1.view(torch.int16), x2.view(torch.int16))
     assert torch.equal(h1.view(torch.int16), h2.view(torch.int16))
+
+
+@pytest.mark.parametrize("m,f,k", [(256, 8192, 2048), (19, 96, 320)])
+def test_linear_gelu_epilogue(device, m, f, k):
+    """The gated-GELU epilogue equals g4_linear_bf16's own gate/up product followed by
+    g4_gelu_mul bit for bit, and the fp32 reference within the bf16 bar."""
+
+    g = torch.Generator(device="cuda").manual_seed(m + f)
+    x = torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn((2 * f, k), device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+    act = kernels.linear_gelu(x, w)
+    ref = kernels.gelu_mul(kernels.linear(x, w))
+    assert torch.equal(act.view(torch.int16), ref.view(torch.int16))
+    gu = (x.double().cpu() @ w.double().cpu().T).to(torch.bfloat16).double()
+    gg, uu = gu[:, :f], gu[:, f:]
+    want = 0.5 * gg * (1 + torch.tanh(0.7978845608028654 * (gg + 0.044715 * gg ** 3))) * uu
+    # g and u may round one bf16 ulp (2^-8 relative) away from the f64 products' rounding, which
+    # moves gelu(g) * u by up to about 2^-7 |g u|: the bar is 2^-6 (|want| + |g u|)
+    err = (act.double().cpu() - want).abs()
+    bar = (want.abs() + (gg * uu).abs()) * 2.0 ** -6 + 1e-5
+    assert torch.all(err <= bar), float((err - bar).max())
