@@ -5,11 +5,11 @@
 // At M = 256 the projection is a stream of the weight matrix: every weight byte is used by all
 // 256 rows once. One workgroup owns all M rows and 64 columns of W, so W is read from HBM exactly
 // once, and X (shared by every workgroup) comes from L2. K is walked in stages of 64: the X
-// stage (256 x 64) and the W stage (64 x 64) are DMA'd into a 3-deep LDS ring
-// (buffer_load ... lds), two stages in flight while the third is multiplied.
+// stage (256 x 64) and the W stage (64 x 64) are DMA'd into a 4-deep LDS ring
+// (buffer_load ... lds), three stages in flight while the fourth is multiplied.
 //
 // LDS layout of a stage: groups of 8 rows x 128 bytes (one DMA instruction: 64 lanes x 16 bytes,
-// 8 full 128-byte lines of the row-major operand) padded to 1088 bytes; within a group, row r's
+// 8 full 128-byte lines of the row-major operand); within a group, row r's
 // 16-byte piece kc sits at slot kc ^ r, so the 16 rows an MFMA operand read touches fall on
 // different banks. Each lane DMAs the piece that belongs at its slot.
 //
@@ -32,7 +32,7 @@ constexpr int kGemmRows = 256;  // M rows per workgroup (all of them)
 constexpr int kGemmCols = 64;   // N columns per workgroup
 constexpr int kGemmKT = 64;     // K per stage
 constexpr int kGemmThreads = 256;
-constexpr int kGroupBytes = 1024 + 64;              // 8 rows x 128 B + padding
+constexpr int kGroupBytes = 1024;                   // 8 rows x 128 B (a 4-stage ring fills the 160 KiB)
 constexpr int kXGroups = kGemmRows / 8;             // 32
 constexpr int kWGroups = kGemmCols / 8;             // 8
 constexpr int kStageBytes = (kXGroups + kWGroups) * kGroupBytes;
@@ -63,48 +63,62 @@ __device__ __forceinline__ void gemm_dma(unsigned char* __restrict__ buf, __amdg
   }
 }
 
-// 16-byte MFMA operand of row `row` (within the X or W part of a stage), K piece kc.
-__device__ __forceinline__ bf16x8 gemm_operand(const unsigned char* __restrict__ part, int row, int kc) {
+// LDS byte offset of the 16-byte MFMA operand piece kc of row `row` (within the X or W part of a
+// stage).
+__device__ __forceinline__ uint32_t gemm_operand_at(uint32_t part, int row, int kc) {
   const int r = row & 7;
-  return as_bf16x8(*reinterpret_cast<const u32x4*>(part + (row >> 3) * kGroupBytes + (8 * r + (kc ^ r)) * 16));
+  return part + (uint32_t)((row >> 3) * kGroupBytes + (8 * r + (kc ^ r)) * 16);
+}
+
+// The operand reads are issued as ds_read_b128 in inline assembly and waited for explicitly
+// (lgkmcnt, tied to the eight operand registers). Read through C++, the compiler cannot tell the
+// stage being multiplied from the stages the DMA is still filling, and at some steps of the ring
+// waited for every DMA in flight (vmcnt(0)); the stage's own DMAs are already covered by the
+// s_waitcnt vmcnt + s_barrier that starts each step.
+__device__ __forceinline__ u32x4 lds_read16(uint32_t addr) {
+  u32x4 v;
+  __asm__ volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
 }
 
 __device__ __forceinline__ void gemm_compute(const unsigned char* __restrict__ buf, floatx4 (&acc)[4][4], int w,
                                              int col, int grp) {
-  const unsigned char* xs = buf;
-  const unsigned char* ws = buf + kXGroups * kGroupBytes;
+  const uint32_t xs = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)buf;
+  const uint32_t ws = xs + kXGroups * kGroupBytes;
 #pragma unroll
   for (int kh = 0; kh < 2; ++kh) {
-    bf16x8 a[4], b[4];
+    u32x4 a[4], b[4];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) a[cb] = gemm_operand(ws, 16 * cb + col, 4 * kh + grp);
+    for (int cb = 0; cb < 4; ++cb) a[cb] = lds_read16(gemm_operand_at(ws, 16 * cb + col, 4 * kh + grp));
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) b[rb] = gemm_operand(xs, 64 * w + 16 * rb + col, 4 * kh + grp);
+    for (int rb = 0; rb < 4; ++rb) b[rb] = lds_read16(gemm_operand_at(xs, 64 * w + 16 * rb + col, 4 * kh + grp));
+    __asm__ volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = mfma16x16x32(a[cb], b[rb], acc[rb][cb]);
+      for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = mfma16x16x32(as_bf16x8(a[cb]), as_bf16x8(b[rb]), acc[rb][cb]);
   }
 }
 
-// One pipeline step: stage s is in `cur`; `nxt` holds stage s + 1 (in flight); stage s + 2 is
-// requested into `fre` (the buffer of stage s - 1, which every wave has finished with).
+// One pipeline step: stage s is in `cur`; `nxt` holds stage s + 1 (in flight, with s + 2); stage
+// s + 3 is requested into `fre` (the buffer of stage s - 1, which every wave has finished with).
 __device__ __forceinline__ void gemm_step(unsigned char* __restrict__ cur, unsigned char* __restrict__ nxt,
                                           unsigned char* __restrict__ fre, floatx4 (&acc)[4][4],
                                           __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw, int K, int kbeg,
                                           int s, int nst, uint32_t oob_x, uint32_t oob_w, int w, int lane, int col,
                                           int grp, int wrow0, int wrow1) {
   (void)nxt;
-  // this wave's DMAs of stage s have landed (stage s + 1's may not have), then every wave's
-  __asm__ volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kDmaPerWave) : "memory");
-  gemm_dma(fre, rx, rw, K, kbeg + (s + 2) * kGemmKT, s + 2 < nst, oob_x, oob_w, w, lane, wrow0, wrow1);
+  // this wave's DMAs of stage s have landed (stages s + 1, s + 2 may not have), then every wave's
+  __asm__ volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * kDmaPerWave) : "memory");
+  gemm_dma(fre, rx, rw, K, kbeg + (s + 3) * kGemmKT, s + 3 < nst, oob_x, oob_w, w, lane, wrow0, wrow1);
   gemm_compute(cur, acc, w, col, grp);
 }
 
 // grid: (N / 64) x ksplit. K / ksplit must be a multiple of 64. With the gated-GELU epilogue the
 // workgroup's 64 weight rows are 32 gate rows and the 32 up rows of the same output columns.
 __global__ __launch_bounds__(kGemmThreads) void linear_bf16_kernel(G4LinearArgs a, float* partials) {
-  __shared__ __attribute__((aligned(1024))) StageBuf b0, b1, b2;
+  __shared__ __attribute__((aligned(1024))) StageBuf b0, b1, b2, b3;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, grp = lane >> 4;
@@ -132,12 +146,15 @@ __global__ __launch_bounds__(kGemmThreads) void linear_bf16_kernel(G4LinearArgs 
 
   gemm_dma(b0, rx, rw, K, kbeg, true, xbytes, wbytes, w, lane, wrow0, wrow1);
   gemm_dma(b1, rx, rw, K, kbeg + kGemmKT, nst > 1, xbytes, wbytes, w, lane, wrow0, wrow1);
-  for (int s = 0; s < nst; s += 3) {
-    gemm_step(b0, b1, b2, acc, rx, rw, K, kbeg, s, nst, xbytes, wbytes, w, lane, col, grp, wrow0, wrow1);
+  gemm_dma(b2, rx, rw, K, kbeg + 2 * kGemmKT, nst > 2, xbytes, wbytes, w, lane, wrow0, wrow1);
+  for (int s = 0; s < nst; s += 4) {
+    gemm_step(b0, b1, b3, acc, rx, rw, K, kbeg, s, nst, xbytes, wbytes, w, lane, col, grp, wrow0, wrow1);
     if (s + 1 < nst)
       gemm_step(b1, b2, b0, acc, rx, rw, K, kbeg, s + 1, nst, xbytes, wbytes, w, lane, col, grp, wrow0, wrow1);
     if (s + 2 < nst)
-      gemm_step(b2, b0, b1, acc, rx, rw, K, kbeg, s + 2, nst, xbytes, wbytes, w, lane, col, grp, wrow0, wrow1);
+      gemm_step(b2, b3, b1, acc, rx, rw, K, kbeg, s + 2, nst, xbytes, wbytes, w, lane, col, grp, wrow0, wrow1);
+    if (s + 3 < nst)
+      gemm_step(b3, b0, b2, acc, rx, rw, K, kbeg, s + 3, nst, xbytes, wbytes, w, lane, col, grp, wrow0, wrow1);
   }
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the trailing (zero) DMAs
 
