@@ -98,6 +98,35 @@ __device__ __forceinline__ float gelu_tanh_mul(float g, float u) {
   return 0.5f * g * (1.0f + tanhf(inner)) * u;
 }
 
+// 16-byte LDS read issued from inline assembly, for operand tiles that buffer_load ... lds fills:
+// the compiler does not see the read, so it adds no wait for DMAs in flight into other buffers (it
+// cannot always tell them apart and then waits for all of them). The caller orders the read after
+// its own wait for the tile's DMA and waits for the read with lgkm_wait before using the value.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+__device__ __forceinline__ u32x4 lds_read16(uint32_t addr) {
+  u32x4 v;
+  __asm__ volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// s_waitcnt lgkmcnt(n), tied to `v` so that no use of v is scheduled before it (n a constant once
+// the caller's loop is unrolled; LDS reads complete in issue order).
+__device__ __forceinline__ void lgkm_wait(int n, u32x4& v) {
+  switch (n) {
+    case 0: __asm__ volatile("s_waitcnt lgkmcnt(0)" : "+v"(v)); break;
+    case 1: __asm__ volatile("s_waitcnt lgkmcnt(1)" : "+v"(v)); break;
+    case 2: __asm__ volatile("s_waitcnt lgkmcnt(2)" : "+v"(v)); break;
+    case 3: __asm__ volatile("s_waitcnt lgkmcnt(3)" : "+v"(v)); break;
+    case 4: __asm__ volatile("s_waitcnt lgkmcnt(4)" : "+v"(v)); break;
+    case 5: __asm__ volatile("s_waitcnt lgkmcnt(5)" : "+v"(v)); break;
+    case 6: __asm__ volatile("s_waitcnt lgkmcnt(6)" : "+v"(v)); break;
+    default: __asm__ volatile("s_waitcnt lgkmcnt(7)" : "+v"(v)); break;
+  }
+}
+
 // 8 bf16 values (one 16-byte word) <-> 8 floats (exact widening; narrowing rounds to nearest even).
 __device__ __forceinline__ void unpack8(u32x4 w, float (&f)[8]) {
 #pragma unroll

@@ -70,20 +70,15 @@ __device__ __forceinline__ uint32_t gemm_operand_at(uint32_t part, int row, int 
   return part + (uint32_t)((row >> 3) * kGroupBytes + (8 * r + (kc ^ r)) * 16);
 }
 
-// The operand reads are issued as ds_read_b128 in inline assembly and waited for explicitly
-// (lgkmcnt, tied to the eight operand registers). Read through C++, the compiler cannot tell the
-// stage being multiplied from the stages the DMA is still filling, and at some steps of the ring
-// waited for every DMA in flight (vmcnt(0)); the stage's own DMAs are already covered by the
-// s_waitcnt vmcnt + s_barrier that starts each step.
-__device__ __forceinline__ u32x4 lds_read16(uint32_t addr) {
-  u32x4 v;
-  __asm__ volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
-  return v;
-}
+// The operand reads are issued as ds_read_b128 in inline assembly (lds_read16) and waited for
+// explicitly (lgkmcnt, tied to the eight operand registers). Read through C++, the compiler cannot
+// tell the stage being multiplied from the stages the DMA is still filling, and at some steps of
+// the ring waited for every DMA in flight (vmcnt(0)); the stage's own DMAs are already covered by
+// the s_waitcnt vmcnt + s_barrier that starts each step.
 
 __device__ __forceinline__ void gemm_compute(const unsigned char* __restrict__ buf, floatx4 (&acc)[4][4], int w,
                                              int col, int grp) {
-  const uint32_t xs = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)buf;
+  const uint32_t xs = lds_addr(buf);
   const uint32_t ws = xs + kXGroups * kGroupBytes;
 #pragma unroll
   for (int kh = 0; kh < 2; ++kh) {

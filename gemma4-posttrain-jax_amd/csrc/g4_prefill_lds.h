@@ -141,11 +141,20 @@ __global__ __launch_bounds__(NW * 64) void prefill_bf16_lds_kernel(G4PrefillArgs
       floatx4 x[NB];
 #pragma unroll
       for (int cb = 0; cb < NB; ++cb) x[cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+      // the K tiles are read by inline-assembly LDS reads, each waited for right before its MFMAs
+      // (the DMA of this chunk is covered by wait_chunk's vmcnt + barrier)
+      constexpr int KG = KS < 4 ? KS : 4;  // tiles read ahead (bounds the registers they hold)
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const bf16x8 kop = as_bf16x8(*reinterpret_cast<const u32x4*>(&kt[bb * KS + s][16 * lane]));
+      for (int s0 = 0; s0 < KS; s0 += KG) {
+        u32x4 kv[KG];
 #pragma unroll
-        for (int cb = 0; cb < NB; ++cb) x[cb] = mfma16x16x32(kop, qop[cb][s], x[cb]);
+        for (int j = 0; j < KG; ++j) kv[j] = lds_read16(lds_addr(&kt[bb * KS + s0 + j][16 * lane]));
+#pragma unroll
+        for (int j = 0; j < KG; ++j) {
+          lgkm_wait(KG - 1 - j, kv[j]);
+#pragma unroll
+          for (int cb = 0; cb < NB; ++cb) x[cb] = mfma16x16x32(as_bf16x8(kv[j]), qop[cb][s0 + j], x[cb]);
+        }
       }
 #pragma unroll
       for (int cb = 0; cb < NB; ++cb) acc[cb][bb] = x[cb];
@@ -276,11 +285,14 @@ __global__ __launch_bounds__(NW * 64) void prefill_bf16_lds_kernel(G4PrefillArgs
 #pragma unroll
     for (int i0 = 0; i0 < S_::VT; i0 += GRP) {
       __builtin_amdgcn_sched_barrier(0);
+      u32x4 vv[GRP];
+#pragma unroll
+      for (int i = i0; i < i0 + GRP && i < S_::VT; ++i) vv[i - i0] = lds_read16(lds_addr(&vt[i][16 * lane]));
 #pragma unroll
       for (int i = i0; i < i0 + GRP && i < S_::VT; ++i) {
-        const bf16x8 vop = as_bf16x8(*reinterpret_cast<const u32x4*>(&vt[i][16 * lane]));
+        lgkm_wait((i0 + GRP < S_::VT ? i0 + GRP : S_::VT) - 1 - i, vv[i - i0]);
 #pragma unroll
-        for (int cb = 0; cb < NB; ++cb) oacc[cb][i] = mfma16x16x32(vop, pop[cb], oacc[cb][i]);
+        for (int cb = 0; cb < NB; ++cb) oacc[cb][i] = mfma16x16x32(as_bf16x8(vv[i - i0]), pop[cb], oacc[cb][i]);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
