@@ -51,7 +51,15 @@ class G4DecodeArgs(ctypes.Structure):
         ("q_pos_scalar", c_int32), ("q_pos", c_void_p), ("key_mask", c_void_p), ("key_mask_stride", c_int32),
         ("q", c_void_p), ("cache_k", c_void_p), ("cache_vt", c_void_p), ("cache_k_w", c_void_p),
         ("new_k", c_void_p), ("new_v", c_void_p), ("out", c_void_p), ("workspace", c_void_p),
-        ("workspace_bytes", c_size_t), ("num_splits", c_int32),
+        ("workspace_bytes", c_size_t), ("prep", c_void_p), ("num_splits", c_int32),
+    ]
+
+
+class G4DecodePrep(ctypes.Structure):
+    _fields_ = [
+        ("q_raw", c_void_p), ("k_raw", c_void_p), ("v_raw", c_void_p), ("in_row_stride", c_int64),
+        ("q_norm_weight", c_void_p), ("k_norm_weight", c_void_p), ("rope_cos", c_void_p), ("rope_sin", c_void_p),
+        ("eps", c_float), ("flags", c_int32),
     ]
 
 
@@ -158,6 +166,6 @@ def ring_slot_positions(last_written: int, window_capacity: int) -> list[int]:
 
 
 __all__ = [
-    "G4AppendArgs", "G4DecodeArgs", "G4PrefillArgs", "G4LinearArgs", "G4PrologueArgs", "G4Error", "PROTOTYPES", "LIB_PATH", "lib", "check",
+    "G4AppendArgs", "G4DecodeArgs", "G4PrefillArgs", "G4LinearArgs", "G4PrologueArgs", "G4DecodePrep", "G4Error", "PROTOTYPES", "LIB_PATH", "lib", "check",
     "kv_source_layers", "ring_slot_positions", "c_uint8",
 ]

@@ -10,60 +10,12 @@
 
 #include "g4_common.h"
 #include "g4_internal.h"
+#include "g4_prep.h"
 
 namespace g4 {
 namespace {
 
 enum VecKind { kQ = 0, kK = 1, kV = 2 };
-
-// PER consecutive elements in one access (PER = 2, 4 or 8; the address aligned to the access)
-template <int PER>
-__device__ __forceinline__ void ld_bf16(const uint16_t* p, float (&x)[PER]) {
-  uint32_t w[PER / 2];
-  if constexpr (PER == 2) {
-    w[0] = *reinterpret_cast<const uint32_t*>(p);
-  } else if constexpr (PER == 4) {
-    const uint2 v = *reinterpret_cast<const uint2*>(p);
-    w[0] = v.x, w[1] = v.y;
-  } else {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = v[i];
-  }
-#pragma unroll
-  for (int i = 0; i < PER / 2; ++i) {
-    x[2 * i] = __uint_as_float(w[i] << 16);
-    x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-  }
-}
-
-template <int PER>
-__device__ __forceinline__ void st_bf16(uint16_t* p, const float (&x)[PER]) {
-  uint32_t w[PER / 2];
-#pragma unroll
-  for (int i = 0; i < PER / 2; ++i) w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
-  if constexpr (PER == 2) {
-    *reinterpret_cast<uint32_t*>(p) = w[0];
-  } else if constexpr (PER == 4) {
-    *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
-  } else {
-    *reinterpret_cast<u32x4*>(p) = u32x4{w[0], w[1], w[2], w[3]};
-  }
-}
-
-template <int PER>
-__device__ __forceinline__ void ld_f32(const float* p, float (&x)[PER]) {
-#pragma unroll
-  for (int i = 0; i < PER; i += 2) {
-    if constexpr (PER == 2) {
-      const float2 v = *reinterpret_cast<const float2*>(p);
-      x[0] = v.x, x[1] = v.y;
-    } else if (i % 4 == 0) {
-      const float4 v = *reinterpret_cast<const float4*>(p + i);
-      x[i] = v.x, x[i + 1] = v.y, x[i + 2] = v.z, x[i + 3] = v.w;
-    }
-  }
-}
 
 // VEC: bf16 with D >= 128 and every row aligned to its lane's PER elements (checked on the host):
 // each lane's elements move in one access per array instead of one per element.
@@ -132,60 +84,8 @@ __global__ __launch_bounds__(1024) void append_kernel(G4AppendArgs a) {
     const T* w = norm ? (kind == kQ ? reinterpret_cast<const T*>(a.q_norm_weight)
                                     : (kind == kK ? reinterpret_cast<const T*>(a.k_norm_weight) : nullptr))
                       : nullptr;
-    // Every input of the vector (its elements, norm weights, cos / sin) is requested before any
-    // arithmetic: one memory round trip per vector.
-    float x[PER], wv[PER], cv[PER], sv[PER];
-    if constexpr (VEC) {
-      ld_bf16<PER>(reinterpret_cast<const uint16_t*>(src) + lane * PER, x);
-#pragma unroll
-      for (int e = 0; e < PER; ++e) wv[e] = 1.f, cv[e] = sv[e] = 0.f;
-      if (w) ld_bf16<PER>(reinterpret_cast<const uint16_t*>(w) + lane * PER, wv);
-      if (rope) {
-        ld_f32<PER>(a.rope_cos + rope_base + lane * PER, cv);
-        ld_f32<PER>(a.rope_sin + rope_base + lane * PER, sv);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        const int d = lane * PER + e;
-        x[e] = lane_on ? E::load(src, d) : 0.f;
-        wv[e] = (w && lane_on) ? E::load(w, d) : 1.f;
-        cv[e] = (rope && lane_on) ? a.rope_cos[rope_base + d] : 0.f;
-        sv[e] = (rope && lane_on) ? a.rope_sin[rope_base + d] : 0.f;
-      }
-    }
-
-    if (norm) {
-      // forward_rms_norm (model.py:278-285): f32 statistics, x * (mean(x^2) + eps)^-0.5 * w.
-      float ss = 0.f;
-#pragma unroll
-      for (int e = 0; e < PER; ++e) ss += x[e] * x[e];
-      ss = wave_sum(ss);
-      const float inv = 1.0f / __fsqrt_rn(ss / (float)D + a.eps);
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        float y = x[e] * inv;
-        if (w) y = y * wv[e];
-        x[e] = E::round(y);
-      }
-    }
-
-    if (rope) {
-      // x*cos + rotate_half(x)*sin with cos/sin first rounded to the activation dtype
-      // (model.py:309-317); products and sum are rounded separately (no FMA contraction).
-#pragma clang fp contract(off)
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        const int d = lane * PER + e;
-        const float partner = __shfl_xor(x[e], PARTNER, 64);
-        const float rot = d < D / 2 ? -partner : partner;
-        const float c = E::round(cv[e]);
-        const float sn = E::round(sv[e]);
-        const float t0 = x[e] * c;  // plain operators: the pragma above keeps them unfused
-        const float t1 = rot * sn;
-        x[e] = E::round(t0 + t1);
-      }
-    }
+    float x[PER];
+    prep_head<BF16, D, VEC>(src, w, norm, rope, a.rope_cos + rope_base, a.rope_sin + rope_base, a.eps, lane, x);
 
     const int64_t bh = (int64_t)b * H + head;
     if (!lane_on) continue;

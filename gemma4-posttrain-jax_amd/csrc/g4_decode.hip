@@ -16,6 +16,7 @@
 // f32 path: a VALU kernel with the same two-phase structure (the tiny fp32 configs).
 #include "g4_common.h"
 #include "g4_internal.h"
+#include "g4_prep.h"
 
 namespace g4 {
 namespace {
@@ -27,6 +28,14 @@ struct KeyRange {
   int n_keys;        // slots scanned: ring slots 0..min(q, Wc-1), or 0..min(q, C-1) for a linear cache
   int64_t new_slot;  // slot of the fused append (-1: none)
 };
+
+// Slot the token at position q is appended to: q mod Wc for a ring, q clamped to [0, C-1] for a
+// linear cache (model.py:373-390).
+__device__ __forceinline__ int64_t append_slot(const G4DecodeArgs& a, int64_t q) {
+  if (a.kind == G4_CACHE_RING) return floor_mod(q, a.capacity);
+  const int64_t s = q < 0 ? 0 : q;
+  return s > a.capacity - 1 ? a.capacity - 1 : s;
+}
 
 __device__ __forceinline__ KeyRange key_range(const G4DecodeArgs& a, int b) {
   KeyRange kr;
@@ -40,16 +49,7 @@ __device__ __forceinline__ KeyRange key_range(const G4DecodeArgs& a, int b) {
     int64_t last = kr.q < (int64_t)a.capacity - 1 ? kr.q : (int64_t)a.capacity - 1;
     kr.n_keys = last < 0 ? 0 : (int)(last + 1);
   }
-  if (a.new_k) {
-    if (ring) {
-      kr.new_slot = floor_mod(kr.q, a.capacity);
-    } else {
-      int64_t s = kr.q < 0 ? 0 : kr.q;
-      kr.new_slot = s > a.capacity - 1 ? a.capacity - 1 : s;
-    }
-  } else {
-    kr.new_slot = -1;
-  }
+  kr.new_slot = a.new_k ? append_slot(a, kr.q) : -1;
   return kr;
 }
 
@@ -255,7 +255,7 @@ bool two_pass_applies(const G4DecodeArgs& a) {
 
 bool use_two_pass(const G4DecodeArgs& a) {
   if (!two_pass_applies(a)) return false;
-  if (a.num_splits == G4_DECODE_TWO_PASS) return true;
+  if (a.num_splits == G4_DECODE_TWO_PASS || a.prep) return true;  // only this path fuses the preparation
   return a.num_splits == 0 && (int64_t)a.batch * a.kv_heads >= kTwoPassMinPairs;
 }
 
@@ -272,8 +272,12 @@ int launch_two_pass(const G4DecodeArgs& a, hipStream_t st) {
   const int parts = (cap_chunks + kTpWavesS - 1) / kTpWavesS;
   const int row_slots = twopass_row_slots(a.capacity);
   uint16_t* ws = reinterpret_cast<uint16_t*>(a.workspace);
-  hipLaunchKernelGGL(decode_bf16_tp_scores_kernel<D>, dim3((unsigned)(npairs * parts)), dim3(kTpWavesS * 64), 0, st, a,
-                     ws, parts, row_slots);
+  if (a.prep)
+    hipLaunchKernelGGL((decode_bf16_tp_scores_kernel<D, true>), dim3((unsigned)(npairs * parts)), dim3(kTpWavesS * 64),
+                       0, st, a, ws, parts, row_slots, *a.prep);
+  else
+    hipLaunchKernelGGL((decode_bf16_tp_scores_kernel<D, false>), dim3((unsigned)(npairs * parts)),
+                       dim3(kTpWavesS * 64), 0, st, a, ws, parts, row_slots, G4DecodePrep{});
   if (cap_chunks <= 16)
     launch_tp_values<D, 16>(a, ws, row_slots, st);
   else if (cap_chunks <= 24)
@@ -309,13 +313,36 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
   if (a.capacity <= 0 || a.slot_stride < a.capacity || a.slot_stride % 64)
     return fail(G4_ERR_INVALID, "g4_decode_attention: capacity %d / slot_stride %d", a.capacity, a.slot_stride);
   if (a.kind == G4_CACHE_RING && a.window <= 0) return fail(G4_ERR_INVALID, "g4_decode_attention: ring needs window > 0");
-  if (!a.q || !a.cache_k || !a.cache_vt || !a.out || !a.key_mask)
-    return fail(G4_ERR_INVALID, "g4_decode_attention: NULL q/cache/out/key_mask");
+  if (!a.cache_k || !a.cache_vt || !a.out || !a.key_mask)
+    return fail(G4_ERR_INVALID, "g4_decode_attention: NULL cache/out/key_mask");
   if (a.kind == G4_CACHE_LINEAR && a.key_mask_stride < a.capacity)
     return fail(G4_ERR_INVALID, "g4_decode_attention: key_mask_stride %d < capacity %d", a.key_mask_stride, a.capacity);
   if (a.key_mask_stride <= 0) return fail(G4_ERR_INVALID, "g4_decode_attention: key_mask_stride must be positive");
   if ((a.new_k == nullptr) != (a.new_v == nullptr))
     return fail(G4_ERR_INVALID, "g4_decode_attention: new_k and new_v must be given together");
+  if (a.prep) {
+    const G4DecodePrep& p = *a.prep;
+    if (!two_pass_applies(a) || a.num_splits == G4_DECODE_SPLIT_KEYS || a.num_splits > 0)
+      return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: fused preparation needs the two-launch path (bf16, head_dim "
+                  "128/256, capacity <= %d, num_splits 0 or G4_DECODE_TWO_PASS)", kTpMaxSlots);
+    if (a.new_k || a.new_v) return fail(G4_ERR_INVALID, "g4_decode_attention: prep replaces new_k / new_v");
+    if (!p.q_raw || (p.k_raw == nullptr) != (p.v_raw == nullptr) || (p.k_raw && !a.cache_k_w))
+      return fail(G4_ERR_INVALID, "g4_decode_attention: prep needs q_raw, k_raw with v_raw, and cache_k_w to append");
+    if (p.in_row_stride < (int64_t)a.kv_heads * a.group * a.head_dim)
+      return fail(G4_ERR_INVALID, "g4_decode_attention: prep in_row_stride %lld too small", (long long)p.in_row_stride);
+    if (((p.flags & G4_APPEND_NORM_Q) && !p.q_norm_weight) || ((p.flags & G4_APPEND_NORM_K) && !p.k_norm_weight) ||
+        ((p.flags & (G4_APPEND_ROPE_Q | G4_APPEND_ROPE_K)) && (!p.rope_cos || !p.rope_sin)))
+      return fail(G4_ERR_INVALID, "g4_decode_attention: prep flags %d need their weights / rotary tables", p.flags);
+    const uintptr_t al = (uintptr_t)(a.head_dim / 64) * 2;
+    for (const void* ptr : {p.q_raw, p.k_raw, p.v_raw, p.q_norm_weight, p.k_norm_weight})
+      if (reinterpret_cast<uintptr_t>(ptr) % al)
+        return fail(G4_ERR_INVALID, "g4_decode_attention: prep rows need %zu-byte alignment", (size_t)al);
+    if ((p.in_row_stride * 2) % (int64_t)al || (reinterpret_cast<uintptr_t>(p.rope_cos) % 16) ||
+        (reinterpret_cast<uintptr_t>(p.rope_sin) % 16))
+      return fail(G4_ERR_INVALID, "g4_decode_attention: prep row stride / rotary tables misaligned");
+  } else if (!a.q) {
+    return fail(G4_ERR_INVALID, "g4_decode_attention: NULL q");
+  }
   if (a.new_k && !a.cache_k_w) return fail(G4_ERR_INVALID, "g4_decode_attention: fused append needs cache_k_w");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int t_alloc = (a.capacity + 31) / 32 * 32;

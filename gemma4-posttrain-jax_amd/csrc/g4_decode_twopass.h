@@ -32,40 +32,100 @@ __host__ __device__ inline size_t twopass_workspace_bytes(int npairs, int R, int
 
 // grid: pairs x parts, parts = ceil(ceil(capacity / 32) / kTpWavesS); wave w of part p takes chunk
 // kTpWavesS * p + w.
-template <int D>
+//
+// PREP: the launch also does g4_kv_append's work from the raw projection rows (G4DecodePrep). The
+// waves of a workgroup prepare the pair's R query heads once (prep_head: g4_kv_append's own
+// arithmetic) into LDS, where every wave reads its MFMA operand; in the workgroup whose chunks hold
+// the appended slot, waves 0 and 1 also prepare the new K row (staged in LDS for the substitution,
+// and stored to the cache) and the new V row (stored as the V^T column the values launch reads).
+// The K chunk is requested before any of this, so the preparation runs while it is in flight.
+template <int D, bool PREP>
 __global__ __launch_bounds__(kTpWavesS * 64) void decode_bf16_tp_scores_kernel(G4DecodeArgs a, uint16_t* ws,
-                                                                              int parts, int row_slots) {
+                                                                              int parts, int row_slots,
+                                                                              G4DecodePrep pp) {
+  constexpr int PER = D / 64;
+  __shared__ __attribute__((aligned(16))) uint16_t q_lds[PREP ? 16 * D : 1];  // [R][D] prepared q
+  __shared__ __attribute__((aligned(16))) uint16_t nk_lds[PREP ? D : 1];      // prepared new K row
   const int R = a.group;
   const int pair = (int)(blockIdx.x / parts), part = (int)(blockIdx.x % parts);
   const int b = pair / a.kv_heads;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const KeyRange kr = key_range(a, b);
+  KeyRange kr = key_range(a, b);
+  if (PREP) kr.new_slot = pp.k_raw ? append_slot(a, kr.q) : -1;  // the append comes from the raw rows
   const int n_chunks = (kr.n_keys + 31) >> 5;
   const int chunk = part * kTpWavesS + w;
-  const bool writer = kr.new_slot >= 0 && (int)(kr.new_slot >> 5) == chunk;  // stores the appended slot
-  const uint16_t* nk = reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D;
+  const int new_chunk = kr.new_slot >= 0 ? (int)(kr.new_slot >> 5) : -1;
+  const bool writer = new_chunk == chunk;  // the wave that scores the appended slot's chunk
+  const uint16_t* nk = PREP ? nk_lds : reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D;
 
+  u32x4 kv[2][D / 32];
   if (chunk < n_chunks) {
     const __amdgpu_buffer_rsrc_t rk =
         make_rsrc(reinterpret_cast<const uint16_t*>(a.cache_k) + (int64_t)pair * a.slot_stride * D,
                   (uint32_t)a.slot_stride * D * 2u);
-    u32x4 kv[2][D / 32];
     load_k_chunk<D>(kv, rk, chunk << 5, col, grp);
+  }
+  if constexpr (PREP) {
+    const int h = pair - b * a.kv_heads;
+    const uint16_t* row = reinterpret_cast<const uint16_t*>(pp.q_raw) + (int64_t)b * pp.in_row_stride;
+    const float* rc = pp.rope_cos + (int64_t)b * D;
+    const float* rs = pp.rope_sin + (int64_t)b * D;
+    for (int r = w; r < R; r += kTpWavesS) {
+      float x[PER];
+      prep_head<true, D, true>(row + (int64_t)(h * R + r) * D, reinterpret_cast<const uint16_t*>(pp.q_norm_weight),
+                               (pp.flags & G4_APPEND_NORM_Q) != 0, (pp.flags & G4_APPEND_ROPE_Q) != 0, rc, rs, pp.eps,
+                               lane, x);
+      st_bf16<PER>(q_lds + r * D + lane * PER, x);
+    }
+    // the appended slot's K / V rows (the workgroup whose chunks hold it)
+    const bool has_slot = pp.k_raw && new_chunk >= part * kTpWavesS && new_chunk < (part + 1) * kTpWavesS;
+    if (has_slot && w < 2) {
+      const uint16_t* src = reinterpret_cast<const uint16_t*>(w == 0 ? pp.k_raw : pp.v_raw) +
+                            (int64_t)b * pp.in_row_stride + (int64_t)h * D;
+      float x[PER];
+      if (w == 0) {
+        prep_head<true, D, true>(src, reinterpret_cast<const uint16_t*>(pp.k_norm_weight),
+                                 (pp.flags & G4_APPEND_NORM_K) != 0, (pp.flags & G4_APPEND_ROPE_K) != 0, rc, rs,
+                                 pp.eps, lane, x);
+        st_bf16<PER>(nk_lds + lane * PER, x);
+        st_bf16<PER>(reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D +
+                         lane * PER,
+                     x);
+      } else {
+        prep_head<true, D, true>(src, nullptr, (pp.flags & G4_APPEND_NORM_V) != 0, false, rc, rs, pp.eps, lane, x);
+        uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride + kr.new_slot;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) cv[(int64_t)(lane * PER + e) * a.slot_stride] = (uint16_t)f32_to_bf16_bits(x[e]);
+      }
+    }
+    wg_barrier();  // prepared q rows (and the new K row) are in LDS
+  }
+
+  if (chunk < n_chunks) {
     bf16x8 qop[D / 32];
 #pragma unroll
-    for (int s = 0; s < D / 32; ++s) qop[s] = q_operand_global(a, pair, R, D, col, grp, s);
+    for (int s = 0; s < D / 32; ++s) {
+      if constexpr (PREP) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (col < R) v = *reinterpret_cast<const u32x4*>(q_lds + col * D + 32 * s + 8 * grp);
+        qop[s] = as_bf16x8(v);
+      } else {
+        qop[s] = q_operand_global(a, pair, R, D, col, grp, s);
+      }
+    }
     uint8_t mb;
     const bool ok = slot_valid_flat(a, b, kr, (chunk << 5) + (lane & 31), mb);
     const uint64_t vbits = __ballot(ok && mb != 0);
-    if (writer) patch_k_sel<D>(kv, nk, kr.new_slot, chunk << 5, col, grp);
+    if (writer && (!PREP || pp.k_raw)) patch_k_sel<D>(kv, nk, kr.new_slot, chunk << 5, col, grp);
     score_to_lds<D>(kv, qop, vbits, ws + (int64_t)pair * R * row_slots, row_slots, chunk << 5, R, col, grp,
                     kBf16Min);
   }
-  // the fused append's cache write: the K row after this wave's K loads have been consumed (no
-  // other wave of the launch reads that chunk); the V^T column is read only by the values launch
-  if (writer) {
+  // the fused append's cache write (prepared rows given): the K row after this wave's K loads have
+  // been consumed (no other wave of the launch reads that chunk); the V^T column is read only by
+  // the values launch
+  if (!PREP && writer) {
     uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
     if (lane < D / 8) *reinterpret_cast<u32x4*>(ck + 8 * lane) = load16(nk + 8 * lane);
     uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride + kr.new_slot;

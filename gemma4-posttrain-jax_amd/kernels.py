@@ -189,7 +189,7 @@ def decode_attention(
         group=R, head_dim=D, capacity=layer.capacity, slot_stride=layer.slot_stride, window=window,
         q_pos_scalar=qp_scalar, q_pos=qp_ptr, key_mask=_ptr(key_mask), key_mask_stride=key_mask.stride(0),
         q=_ptr(q), cache_k=_ptr(layer.key), cache_vt=_ptr(layer.value_t), cache_k_w=_ptr(layer.key),
-        new_k=_ptr(new_k), new_v=_ptr(new_v), out=_ptr(out), workspace=None, workspace_bytes=0,
+        new_k=_ptr(new_k), new_v=_ptr(new_v), out=_ptr(out), workspace=None, workspace_bytes=0, prep=None,
         num_splits=num_splits,
     )
     need = _lib.lib().g4_decode_workspace_size(ctypes.byref(a))
@@ -197,6 +197,64 @@ def decode_attention(
     if need:
         ws = torch.empty(need, dtype=torch.uint8, device=q.device)
         a.workspace, a.workspace_bytes = ws.data_ptr(), need
+    _lib.check(_lib.lib().g4_decode_attention(ctypes.byref(a), _stream()), "g4_decode_attention")
+    return out
+
+
+def decode_attention_fused(
+    layer: LayerKVCache,
+    q_raw: torch.Tensor,
+    key_mask: torch.Tensor,
+    *,
+    q_pos: torch.Tensor,
+    window: int,
+    k_raw: torch.Tensor | None,
+    v_raw: torch.Tensor | None,
+    q_norm_weight: torch.Tensor | None,
+    k_norm_weight: torch.Tensor | None,
+    rope_cos: torch.Tensor,
+    rope_sin: torch.Tensor,
+    eps: float,
+    flags: int,
+) -> torch.Tensor:
+    """g4_decode_attention with G4DecodePrep: the raw projection rows in, g4_kv_append's work (q / k
+    norm + RoPE, v norm, and with k_raw / v_raw the append into ``layer``; a kv-shared layer passes
+    its source cache and no k / v) done inside the two-launch attention. q_raw ``[B, Hkv, R, D]`` and
+    k_raw / v_raw ``[B, Hkv, D]`` are views of the projection output sharing one batch-row stride;
+    rope_cos / rope_sin f32 ``[B, D]``. Returns ``[B, Hkv, R, D]``."""
+
+    B, H, R, D = q_raw.shape
+    stride = q_raw.stride(0)
+    if q_raw.dtype != layer.key.dtype or q_raw.stride(3) != 1 or q_raw.stride(2) != D or q_raw.stride(1) != R * D:
+        raise ValueError("q_raw must hold [Hkv, R, D] contiguous rows in the cache dtype")
+    for name, t in (("k_raw", k_raw), ("v_raw", v_raw)):
+        if t is not None and (tuple(t.shape) != (B, H, D) or t.stride(0) != stride or t.stride(1) != D
+                              or t.stride(2) != 1 or t.dtype != q_raw.dtype):
+            raise ValueError(f"{name} must be [B, Hkv, D] rows sharing q_raw's batch stride")
+    if (k_raw is None) != (v_raw is None):
+        raise ValueError("k_raw and v_raw go together")
+    for name, t in (("rope_cos", rope_cos), ("rope_sin", rope_sin)):
+        if t.dtype != torch.float32 or t.numel() != B * D or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous f32 [B, D] table")
+    if key_mask.dtype != torch.bool or key_mask.dim() != 2 or key_mask.shape[0] != B or key_mask.stride(1) != 1:
+        raise ValueError("key_mask must be a [B, C] bool tensor with unit inner stride")
+    if q_pos.dtype != torch.int32 or tuple(q_pos.shape) != (B,) or not q_pos.is_contiguous():
+        raise ValueError("q_pos must be a contiguous int32 [B] tensor")
+    out = torch.empty((B, H, R, D), dtype=q_raw.dtype, device=q_raw.device)
+    prep = _lib.G4DecodePrep(q_raw=_ptr(q_raw), k_raw=_ptr(k_raw), v_raw=_ptr(v_raw), in_row_stride=stride,
+                             q_norm_weight=_ptr(q_norm_weight), k_norm_weight=_ptr(k_norm_weight),
+                             rope_cos=_ptr(rope_cos), rope_sin=_ptr(rope_sin), eps=eps, flags=flags)
+    a = _lib.G4DecodeArgs(
+        dtype=_code(q_raw), kind=_lib.G4_CACHE_RING if layer.ring else _lib.G4_CACHE_LINEAR, batch=B, kv_heads=H,
+        group=R, head_dim=D, capacity=layer.capacity, slot_stride=layer.slot_stride, window=window,
+        q_pos_scalar=0, q_pos=_ptr(q_pos), key_mask=_ptr(key_mask), key_mask_stride=key_mask.stride(0),
+        q=None, cache_k=_ptr(layer.key), cache_vt=_ptr(layer.value_t), cache_k_w=_ptr(layer.key),
+        new_k=None, new_v=None, out=_ptr(out), workspace=None, workspace_bytes=0,
+        prep=ctypes.cast(ctypes.pointer(prep), ctypes.c_void_p), num_splits=0,
+    )
+    need = _lib.lib().g4_decode_workspace_size(ctypes.byref(a))
+    ws = torch.empty(need, dtype=torch.uint8, device=q_raw.device)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), need
     _lib.check(_lib.lib().g4_decode_attention(ctypes.byref(a), _stream()), "g4_decode_attention")
     return out
 

@@ -208,6 +208,15 @@ def _split_down(act: torch.Tensor, w_t: torch.Tensor) -> bool:
             and k % (64 * DOWN_KSPLIT) == 0 and act.is_contiguous() and w_t.is_contiguous())
 
 
+def _fused_decode_prep(x: torch.Tensor, pairs: int, head_dim: int, cache) -> bool:
+    """Whether a decode layer's q/k/v preparation and append run inside the two-launch attention
+    (G4DecodePrep): the path the library takes at the rollout batch (>= 256 (b, kv head) pairs,
+    rows of at most 1024 slots, head dims 128 / 256, bf16)."""
+
+    return (x.dtype == torch.bfloat16 and pairs >= 256 and head_dim in (128, 256) and cache is not None
+            and cache.capacity <= 1024)
+
+
 def _native_gate_up(h: torch.Tensor, w_t: torch.Tensor) -> bool:
     """Whether the gate/up projection + gated GELU run as one g4_linear_bf16 launch (its
     gated-GELU epilogue): a bf16 decode batch of at most 256 rows and shapes the kernel takes."""
@@ -356,43 +365,61 @@ def forward_gemma4_text(
         H, R, D = pk.heads, pk.group, pk.head_dim
         qkv = _proj(h.reshape(B * S, -1), pk.w_qkv_t).reshape(B, S, -1)
         q = qkv[..., : H * R * D].view(B, S, H, R, D)
-        q_out = torch.empty((B, S, H, R, D), dtype=x.dtype, device=dev)
         cos, sin = rot[lt]
         layer_cache = kv_cache.layers[i]
-        if is_kv_shared(config, i):
-            kernels.prepare_q(q, q_out, q_norm_weight=lp.attention.q_norm.weight, eps=eps, rope_cos=cos,
-                              rope_sin=sin, flags=flags_q)
-            src = sources[i]
-            src_cache = new_layers[src]
-            new_layers.append(None)
-        else:
-            k = qkv[..., H * R * D: (H * R + H) * D].view(B, S, H, D)
-            v = qkv[..., (H * R + H) * D:].view(B, S, H, D) if pk.has_v else k
-            k_out = vt_out = None
-            if cache_mode == "prefill" and layer_cache.ring:
-                sp = slot_stride_for(S)
-                k_out = torch.empty((B, H, sp, D), dtype=x.dtype, device=dev)
-                vt_out = torch.zeros((B, H, D, sp), dtype=x.dtype, device=dev)
-            kernels.kv_append(layer_cache, k, v, write_pos=slot, flags=flags_q | flags_kv, eps=eps, q=q,
-                              q_out=q_out, q_norm_weight=lp.attention.q_norm.weight,
-                              k_norm_weight=lp.attention.k_norm.weight, rope_cos=cos, rope_sin=sin, k_out=k_out,
-                              vt_out=vt_out)
-            if k_out is not None:
-                prompt_kv[i] = (k_out, vt_out)
-            src = i
-            src_cache = layer_cache
-            new_layers.append(layer_cache)
-        if cache_mode == "prefill":
-            if length != 0:
-                raise NotImplementedError("prefill into a non-empty cache is not supported")
-            if src in prompt_kv:
-                kk, vt = prompt_kv[src]
+        shared = is_kv_shared(config, i)
+        if write_pos is not None and _fused_decode_prep(x, B * H, D, new_layers[sources[i]] if shared else layer_cache):
+            # graphed decode step at the rollout batch: g4_kv_append's work runs inside the
+            # two-launch attention (G4DecodePrep) on the raw projection rows
+            if shared:
+                src_cache, kr, vr, flags = new_layers[sources[i]], None, None, flags_q
+                new_layers.append(None)
             else:
-                kk, vt = src_cache.key, src_cache.value_t
-            attn = kernels.prefill_attention(q_out, kk, vt, key_mask, window=window)
+                k = qkv[..., H * R * D: (H * R + H) * D].view(B, S, H, D)
+                v = qkv[..., (H * R + H) * D:].view(B, S, H, D) if pk.has_v else k
+                src_cache, kr, vr, flags = layer_cache, k[:, 0], v[:, 0], flags_q | flags_kv
+                new_layers.append(layer_cache)
+            attn = kernels.decode_attention_fused(
+                src_cache, q[:, 0], key_mask, q_pos=slot, window=config.sliding_window, k_raw=kr, v_raw=vr,
+                q_norm_weight=lp.attention.q_norm.weight,
+                k_norm_weight=None if lp.attention.k_norm is None else lp.attention.k_norm.weight,
+                rope_cos=cos[:, 0], rope_sin=sin[:, 0], eps=eps, flags=flags).view(B, 1, H, R, D)
         else:
-            attn = kernels.decode_attention(src_cache, q_out.view(B, H, R, D), key_mask, q_pos=slot,
-                                            window=config.sliding_window).view(B, 1, H, R, D)
+            q_out = torch.empty((B, S, H, R, D), dtype=x.dtype, device=dev)
+            if shared:
+                kernels.prepare_q(q, q_out, q_norm_weight=lp.attention.q_norm.weight, eps=eps, rope_cos=cos,
+                                  rope_sin=sin, flags=flags_q)
+                src = sources[i]
+                src_cache = new_layers[src]
+                new_layers.append(None)
+            else:
+                k = qkv[..., H * R * D: (H * R + H) * D].view(B, S, H, D)
+                v = qkv[..., (H * R + H) * D:].view(B, S, H, D) if pk.has_v else k
+                k_out = vt_out = None
+                if cache_mode == "prefill" and layer_cache.ring:
+                    sp = slot_stride_for(S)
+                    k_out = torch.empty((B, H, sp, D), dtype=x.dtype, device=dev)
+                    vt_out = torch.zeros((B, H, D, sp), dtype=x.dtype, device=dev)
+                kernels.kv_append(layer_cache, k, v, write_pos=slot, flags=flags_q | flags_kv, eps=eps, q=q,
+                                  q_out=q_out, q_norm_weight=lp.attention.q_norm.weight,
+                                  k_norm_weight=lp.attention.k_norm.weight, rope_cos=cos, rope_sin=sin, k_out=k_out,
+                                  vt_out=vt_out)
+                if k_out is not None:
+                    prompt_kv[i] = (k_out, vt_out)
+                src = i
+                src_cache = layer_cache
+                new_layers.append(layer_cache)
+            if cache_mode == "prefill":
+                if length != 0:
+                    raise NotImplementedError("prefill into a non-empty cache is not supported")
+                if src in prompt_kv:
+                    kk, vt = prompt_kv[src]
+                else:
+                    kk, vt = src_cache.key, src_cache.value_t
+                attn = kernels.prefill_attention(q_out, kk, vt, key_mask, window=window)
+            else:
+                attn = kernels.decode_attention(src_cache, q_out.view(B, H, R, D), key_mask, q_pos=slot,
+                                                window=config.sliding_window).view(B, 1, H, R, D)
         o = _proj(attn.reshape(B * S, H * R * D), pk.w_o_t).reshape(B, S, -1)
         # post-attention norm + residual, then the pre-feedforward norm (one pass)
         x, h = kernels.residual_norm(o, lp.post_attention_norm.weight, x, scalar=None,

@@ -112,6 +112,28 @@ int g4_kv_append(const G4AppendArgs* args, void* stream);
  * With new_k/new_v set, the kernel first stores this token's K/V row (prepared, [B, Hkv, D])
  * at position q_pos[b] — the fused append — and attends over the updated cache.
  */
+/*
+ * Optional fused preparation for g4_decode_attention (the two-launch path only): instead of
+ * prepared q / new_k / new_v, the raw projection rows, and the launch does g4_kv_append's work
+ * itself -- q norm + RoPE, k norm + RoPE, the unscaled v norm (model.py:463-482) and the cache
+ * append (model.py:368-390) -- with the same arithmetic. q_raw [B, Hkv, R, D], k_raw / v_raw
+ * [B, Hkv, D] with in_row_stride elements between batch rows (the q/k/v projection output);
+ * k_raw = NULL for a kv-shared layer (no append). rope_cos / rope_sin [B, D] f32 at the query
+ * positions; flags as g4_kv_append's. Rows aligned to D/64 elements, cos / sin to 16 bytes.
+ */
+typedef struct G4DecodePrep {
+  const void* q_raw;
+  const void* k_raw;
+  const void* v_raw;
+  int64_t in_row_stride;
+  const void* q_norm_weight;
+  const void* k_norm_weight;
+  const float* rope_cos;
+  const float* rope_sin;
+  float eps;
+  int32_t flags;
+} G4DecodePrep;
+
 typedef struct G4DecodeArgs {
   int32_t dtype;
   int32_t kind;
@@ -135,6 +157,7 @@ typedef struct G4DecodeArgs {
   void* out;            /* [B, Hkv, R, D] */
   void* workspace;      /* split-K scratch, >= g4_decode_workspace_size(args) bytes */
   size_t workspace_bytes;
+  const G4DecodePrep* prep; /* optional (NULL: q / new_k / new_v are prepared); needs the two-launch path */
   int32_t num_splits;   /* 0 = choose automatically; 1 or 2 = workgroups per (b, kv head), one
                            pass, each owning a slice of the head dim (2: head dim 256);
                            G4_DECODE_SPLIT_KEYS = split the key range (bf16, head dims 128/256);

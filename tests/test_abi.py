@@ -90,7 +90,7 @@ def _decode_args(**kw):
     base = dict(dtype=_lib.G4_DTYPE_BF16, kind=_lib.G4_CACHE_RING, batch=2, kv_heads=2, group=4, head_dim=256,
                 capacity=512, slot_stride=512, window=512, q_pos_scalar=0, q_pos=None, key_mask=1,
                 key_mask_stride=2048, q=1, cache_k=1, cache_vt=1, cache_k_w=1, new_k=None, new_v=None, out=1,
-                workspace=None, workspace_bytes=0, num_splits=0)
+                workspace=None, workspace_bytes=0, prep=None, num_splits=0)
     base.update(kw)
     return _lib.G4DecodeArgs(**base)
 
@@ -140,6 +140,35 @@ def test_decode_split_keys_workspace():
     # ring rows of 512 slots and one-pass choices need none
     assert L.g4_decode_workspace_size(ctypes.byref(_decode_args())) == 0
     assert L.g4_decode_workspace_size(ctypes.byref(_decode_args(**long_rows, num_splits=1))) == 0
+
+
+def test_decode_prep_rejections():
+    """The fused preparation runs only on the two-launch path and needs its inputs."""
+
+    L = _lib.lib()
+    prep = _lib.G4DecodePrep(q_raw=16, k_raw=16, v_raw=16, in_row_stride=12 * 256, q_norm_weight=16,
+                             k_norm_weight=16, rope_cos=16, rope_sin=16, eps=1e-6, flags=0)
+    pp = ctypes.cast(ctypes.pointer(prep), ctypes.c_void_p)
+    cases = [
+        (dict(prep=pp, head_dim=64), "two-launch path"),
+        (dict(prep=pp, num_splits=2), "two-launch path"),
+        (dict(prep=pp, new_k=16, new_v=16), "replaces new_k"),
+    ]
+    for kw, match in cases:
+        a = _decode_args(**kw)
+        assert L.g4_decode_attention(ctypes.byref(a), None) in (_lib.G4_ERR_INVALID, _lib.G4_ERR_UNSUPPORTED)
+        assert re.search(match, L.g4_last_error().decode()), L.g4_last_error().decode()
+    prep.in_row_stride = 100
+    a = _decode_args(prep=pp)
+    assert L.g4_decode_attention(ctypes.byref(a), None) == _lib.G4_ERR_INVALID
+    assert re.search("in_row_stride", L.g4_last_error().decode())
+    prep.in_row_stride, prep.flags, prep.q_norm_weight = 12 * 256, _lib.G4_APPEND_NORM_Q, None
+    a = _decode_args(prep=pp)
+    assert L.g4_decode_attention(ctypes.byref(a), None) == _lib.G4_ERR_INVALID
+    assert re.search("flags", L.g4_last_error().decode())
+    # with the preparation the library always asks for the two-launch workspace, also below 256 pairs
+    prep.flags, prep.q_norm_weight = 0, 16
+    assert L.g4_decode_workspace_size(ctypes.byref(_decode_args(prep=pp))) == 2 * 2 * 4 * 512 * 2
 
 
 def test_decode_two_pass_workspace():
