@@ -60,6 +60,26 @@ __global__ __launch_bounds__(kTpWavesS * 64) void decode_bf16_tp_scores_kernel(G
   const bool writer = new_chunk == chunk;  // the wave that scores the appended slot's chunk
   const uint16_t* nk = PREP ? nk_lds : reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D;
 
+  // PREP: the preparation's loads go out first (they return before the K chunk: vector loads
+  // complete in issue order), so its arithmetic runs while the K chunk is in flight
+  const int h = pair - b * a.kv_heads;
+  const bool has_slot = PREP && pp.k_raw && new_chunk >= part * kTpWavesS && new_chunk < (part + 1) * kTpWavesS;
+  const bool kv_wave = has_slot && w < 2;  // wave 0: the new K row, wave 1: the new V row
+  PrepIn<true, D> pq, pkv;
+  const uint16_t* qrow = reinterpret_cast<const uint16_t*>(pp.q_raw) + (int64_t)b * pp.in_row_stride;
+  const float* rc = pp.rope_cos + (int64_t)b * D;
+  const float* rs = pp.rope_sin + (int64_t)b * D;
+  if constexpr (PREP) {
+    if (w < R)
+      prep_load<true, D, true>(pq, qrow + (int64_t)(h * R + w) * D, reinterpret_cast<const uint16_t*>(pp.q_norm_weight),
+                               (pp.flags & G4_APPEND_ROPE_Q) != 0, rc, rs, lane);
+    if (kv_wave)
+      prep_load<true, D, true>(pkv,
+                               reinterpret_cast<const uint16_t*>(w == 0 ? pp.k_raw : pp.v_raw) +
+                                   (int64_t)b * pp.in_row_stride + (int64_t)h * D,
+                               w == 0 ? reinterpret_cast<const uint16_t*>(pp.k_norm_weight) : nullptr,
+                               w == 0 && (pp.flags & G4_APPEND_ROPE_K) != 0, rc, rs, lane);
+  }
   u32x4 kv[2][D / 32];
   if (chunk < n_chunks) {
     const __amdgpu_buffer_rsrc_t rk =
@@ -68,36 +88,31 @@ __global__ __launch_bounds__(kTpWavesS * 64) void decode_bf16_tp_scores_kernel(G
     load_k_chunk<D>(kv, rk, chunk << 5, col, grp);
   }
   if constexpr (PREP) {
-    const int h = pair - b * a.kv_heads;
-    const uint16_t* row = reinterpret_cast<const uint16_t*>(pp.q_raw) + (int64_t)b * pp.in_row_stride;
-    const float* rc = pp.rope_cos + (int64_t)b * D;
-    const float* rs = pp.rope_sin + (int64_t)b * D;
-    for (int r = w; r < R; r += kTpWavesS) {
+    if (w < R) {
+      prep_math<true, D>(pq, (pp.flags & G4_APPEND_NORM_Q) != 0, pp.q_norm_weight != nullptr,
+                         (pp.flags & G4_APPEND_ROPE_Q) != 0, pp.eps);
+      st_bf16<PER>(q_lds + w * D + lane * PER, pq.x);
+    }
+    for (int r = w + kTpWavesS; r < R; r += kTpWavesS) {  // more than one head per wave (R > 4)
       float x[PER];
-      prep_head<true, D, true>(row + (int64_t)(h * R + r) * D, reinterpret_cast<const uint16_t*>(pp.q_norm_weight),
+      prep_head<true, D, true>(qrow + (int64_t)(h * R + r) * D, reinterpret_cast<const uint16_t*>(pp.q_norm_weight),
                                (pp.flags & G4_APPEND_NORM_Q) != 0, (pp.flags & G4_APPEND_ROPE_Q) != 0, rc, rs, pp.eps,
                                lane, x);
       st_bf16<PER>(q_lds + r * D + lane * PER, x);
     }
-    // the appended slot's K / V rows (the workgroup whose chunks hold it)
-    const bool has_slot = pp.k_raw && new_chunk >= part * kTpWavesS && new_chunk < (part + 1) * kTpWavesS;
-    if (has_slot && w < 2) {
-      const uint16_t* src = reinterpret_cast<const uint16_t*>(w == 0 ? pp.k_raw : pp.v_raw) +
-                            (int64_t)b * pp.in_row_stride + (int64_t)h * D;
-      float x[PER];
+    if (kv_wave) {
       if (w == 0) {
-        prep_head<true, D, true>(src, reinterpret_cast<const uint16_t*>(pp.k_norm_weight),
-                                 (pp.flags & G4_APPEND_NORM_K) != 0, (pp.flags & G4_APPEND_ROPE_K) != 0, rc, rs,
-                                 pp.eps, lane, x);
-        st_bf16<PER>(nk_lds + lane * PER, x);
+        prep_math<true, D>(pkv, (pp.flags & G4_APPEND_NORM_K) != 0, pp.k_norm_weight != nullptr,
+                           (pp.flags & G4_APPEND_ROPE_K) != 0, pp.eps);
+        st_bf16<PER>(nk_lds + lane * PER, pkv.x);
         st_bf16<PER>(reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D +
                          lane * PER,
-                     x);
+                     pkv.x);
       } else {
-        prep_head<true, D, true>(src, nullptr, (pp.flags & G4_APPEND_NORM_V) != 0, false, rc, rs, pp.eps, lane, x);
+        prep_math<true, D>(pkv, (pp.flags & G4_APPEND_NORM_V) != 0, false, false, pp.eps);
         uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride + kr.new_slot;
 #pragma unroll
-        for (int e = 0; e < PER; ++e) cv[(int64_t)(lane * PER + e) * a.slot_stride] = (uint16_t)f32_to_bf16_bits(x[e]);
+        for (int e = 0; e < PER; ++e) cv[(int64_t)(lane * PER + e) * a.slot_stride] = (uint16_t)f32_to_bf16_bits(pkv.x[e]);
       }
     }
     wg_barrier();  // prepared q rows (and the new K row) are in LDS

@@ -59,50 +59,62 @@ __device__ __forceinline__ void ld_f32(const float* p, float (&x)[PER]) {
 }
 
 
-// Load the vector's elements, its norm weights and cos / sin row (every input requested before
-// any arithmetic: one memory round trip), then RMSNorm and RoPE with the reference's rounding
-// points. VEC: bf16, D >= 128, rows aligned to one lane's D/64 elements (checked on the host).
+// The loads of one vector (its elements, norm weights and cos / sin row), all issued before any
+// arithmetic: one memory round trip. VEC: bf16, D >= 128, rows aligned to one lane's D/64 elements
+// (checked on the host).
+template <bool BF16, int D>
+struct PrepIn {
+  static constexpr int PER = D >= 64 ? D / 64 : 1;
+  float x[PER], wv[PER], cv[PER], sv[PER];
+};
+
 template <bool BF16, int D, bool VEC>
-__device__ __forceinline__ void prep_head(const typename Elem<BF16>::T* src, const typename Elem<BF16>::T* w,
-                                          bool norm, bool rope, const float* rcos, const float* rsin, float eps,
-                                          int lane, float (&x)[D >= 64 ? D / 64 : 1]) {
+__device__ __forceinline__ void prep_load(PrepIn<BF16, D>& in, const typename Elem<BF16>::T* src,
+                                          const typename Elem<BF16>::T* w, bool rope, const float* rcos,
+                                          const float* rsin, int lane) {
   using E = Elem<BF16>;
-  constexpr int PER = D >= 64 ? D / 64 : 1;
-  constexpr int PARTNER = D >= 64 ? 32 : D / 2;
+  constexpr int PER = PrepIn<BF16, D>::PER;
   const bool lane_on = D >= 64 || lane < D;
-  float wv[PER], cv[PER], sv[PER];
   if constexpr (VEC) {
-    ld_bf16<PER>(reinterpret_cast<const uint16_t*>(src) + lane * PER, x);
+    ld_bf16<PER>(reinterpret_cast<const uint16_t*>(src) + lane * PER, in.x);
 #pragma unroll
-    for (int e = 0; e < PER; ++e) wv[e] = 1.f, cv[e] = sv[e] = 0.f;
-    if (w) ld_bf16<PER>(reinterpret_cast<const uint16_t*>(w) + lane * PER, wv);
+    for (int e = 0; e < PER; ++e) in.wv[e] = 1.f, in.cv[e] = in.sv[e] = 0.f;
+    if (w) ld_bf16<PER>(reinterpret_cast<const uint16_t*>(w) + lane * PER, in.wv);
     if (rope) {
-      ld_f32<PER>(rcos + lane * PER, cv);
-      ld_f32<PER>(rsin + lane * PER, sv);
+      ld_f32<PER>(rcos + lane * PER, in.cv);
+      ld_f32<PER>(rsin + lane * PER, in.sv);
     }
   } else {
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
       const int d = lane * PER + e;
-      x[e] = lane_on ? E::load(src, d) : 0.f;
-      wv[e] = (w && lane_on) ? E::load(w, d) : 1.f;
-      cv[e] = (rope && lane_on) ? rcos[d] : 0.f;
-      sv[e] = (rope && lane_on) ? rsin[d] : 0.f;
+      in.x[e] = lane_on ? E::load(src, d) : 0.f;
+      in.wv[e] = (w && lane_on) ? E::load(w, d) : 1.f;
+      in.cv[e] = (rope && lane_on) ? rcos[d] : 0.f;
+      in.sv[e] = (rope && lane_on) ? rsin[d] : 0.f;
     }
   }
+}
 
+// RMSNorm and RoPE of the loaded vector with the reference's rounding points; the result in in.x.
+template <bool BF16, int D>
+__device__ __forceinline__ void prep_math(PrepIn<BF16, D>& in, bool norm, bool has_w, bool rope, float eps) {
+  using E = Elem<BF16>;
+  constexpr int PER = PrepIn<BF16, D>::PER;
+  constexpr int PARTNER = D >= 64 ? 32 : D / 2;
+  const int lane = threadIdx.x & 63;
   if (norm) {
     // forward_rms_norm (model.py:278-285): f32 statistics, x * (mean(x^2) + eps)^-0.5 * w.
     float ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < PER; ++e) ss += x[e] * x[e];
+    for (int e = 0; e < PER; ++e) ss += in.x[e] * in.x[e];
     ss = wave_sum(ss);
     const float inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
-      float y = x[e] * inv;
-      if (w) y = y * wv[e];
-      x[e] = E::round(y);
+      float y = in.x[e] * inv;
+      if (has_w) y = y * in.wv[e];
+      in.x[e] = E::round(y);
     }
   }
 
@@ -113,15 +125,27 @@ __device__ __forceinline__ void prep_head(const typename Elem<BF16>::T* src, con
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
       const int d = lane * PER + e;
-      const float partner = __shfl_xor(x[e], PARTNER, 64);
+      const float partner = __shfl_xor(in.x[e], PARTNER, 64);
       const float rot = d < D / 2 ? -partner : partner;
-      const float c = E::round(cv[e]);
-      const float sn = E::round(sv[e]);
-      const float t0 = x[e] * c;  // plain operators: the pragma above keeps them unfused
+      const float c = E::round(in.cv[e]);
+      const float sn = E::round(in.sv[e]);
+      const float t0 = in.x[e] * c;  // plain operators: the pragma above keeps them unfused
       const float t1 = rot * sn;
-      x[e] = E::round(t0 + t1);
+      in.x[e] = E::round(t0 + t1);
     }
   }
+}
+
+// prep_load + prep_math; x receives the prepared vector.
+template <bool BF16, int D, bool VEC>
+__device__ __forceinline__ void prep_head(const typename Elem<BF16>::T* src, const typename Elem<BF16>::T* w,
+                                          bool norm, bool rope, const float* rcos, const float* rsin, float eps,
+                                          int lane, float (&x)[D >= 64 ? D / 64 : 1]) {
+  PrepIn<BF16, D> in;
+  prep_load<BF16, D, VEC>(in, src, w, rope, rcos, rsin, lane);
+  prep_math<BF16, D>(in, norm, w != nullptr, rope, eps);
+#pragma unroll
+  for (int e = 0; e < PrepIn<BF16, D>::PER; ++e) x[e] = in.x[e];
 }
 
 }  // namespace g4
