@@ -118,6 +118,7 @@ PROTOTYPES = {
     "g4_linear_bf16": (c_int32, [POINTER(G4LinearArgs), c_void_p]),
     "g4_convert_f32_to_bf16": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "g4_convert_bf16_to_f32": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p]),
+    "g4_init": (c_int32, []),
     "g4_last_error": (c_char_p, []),
     "g4_version": (c_char_p, []),
 }
@@ -151,6 +152,22 @@ def check(rc: int, what: str) -> None:
         raise G4Error(f"{what} failed ({rc}): {msg}")
 
 
+_ready_devices: set = set()
+
+
+def init_device(index: int) -> None:
+    """g4_init on device ``index`` (made current around the call), once per process and device:
+    the library's one-time kernel set-up, done before any graph capture needs it."""
+
+    if index in _ready_devices:
+        return
+    import torch
+
+    with torch.cuda.device(index):
+        check(lib().g4_init(), "g4_init")
+    _ready_devices.add(index)
+
+
 def kv_source_layers(layer_types: list[int], num_kv_shared_layers: int) -> list[int]:
     n = len(layer_types)
     arr_in = (c_int32 * n)(*layer_types)
@@ -166,6 +183,6 @@ def ring_slot_positions(last_written: int, window_capacity: int) -> list[int]:
 
 
 __all__ = [
-    "G4AppendArgs", "G4DecodeArgs", "G4PrefillArgs", "G4LinearArgs", "G4PrologueArgs", "G4DecodePrep", "G4Error", "PROTOTYPES", "LIB_PATH", "lib", "check",
+    "G4AppendArgs", "G4DecodeArgs", "G4PrefillArgs", "G4LinearArgs", "G4PrologueArgs", "G4DecodePrep", "G4Error", "PROTOTYPES", "LIB_PATH", "lib", "check", "init_device",
     "kv_source_layers", "ring_slot_positions", "c_uint8",
 ]

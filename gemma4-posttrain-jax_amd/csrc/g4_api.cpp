@@ -4,6 +4,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "g4_common.h"
 #include "g4_internal.h"
 
@@ -25,9 +27,34 @@ int check_launch(const char* what) {
   return G4_OK;
 }
 
+namespace {
+
+std::once_flag g_setup_once[kMaxDevices];
+int g_setup_status[kMaxDevices];
+char g_setup_error[kMaxDevices][512];
+
+}  // namespace
+
+int device_setup(int* device) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(G4_ERR_LAUNCH, "g4_init: no current HIP device (or ordinal %d >= %d)", dev, kMaxDevices);
+  std::call_once(g_setup_once[dev], [dev] {
+    int rc = setup_decode_kernels(dev);
+    if (rc == G4_OK) rc = setup_prefill_kernels(dev);
+    if (rc != G4_OK) snprintf(g_setup_error[dev], sizeof(g_setup_error[dev]), "%s", g_error);
+    g_setup_status[dev] = rc;
+  });
+  if (device) *device = dev;
+  if (g_setup_status[dev] != G4_OK) return fail(g_setup_status[dev], "%s", g_setup_error[dev]);
+  return G4_OK;
+}
+
 }  // namespace g4
 
 extern "C" {
+
+int g4_init(void) { return g4::device_setup(nullptr); }
 
 const char* g4_last_error(void) { return g4::g_error; }
 

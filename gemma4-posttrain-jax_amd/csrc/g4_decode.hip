@@ -169,13 +169,8 @@ size_t stage_lds_bytes(int R) { return (size_t)R * kStageStride * 2 + (size_t)kD
 
 template <int D, int NSPLIT>
 int launch_stage(const G4DecodeArgs& a, hipStream_t st) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)decode_bf16_stage_kernel<D, NSPLIT>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)stage_lds_bytes(16)) != hipSuccess)
-      return fail(G4_ERR_LAUNCH, "g4_decode_attention: cannot raise the LDS limit");
-    attr_set = true;
-  }
+  const int setup = device_setup(nullptr);  // raised LDS limits
+  if (setup != G4_OK) return setup;
   const int64_t npairs = (int64_t)a.batch * a.kv_heads;
   const int64_t blocks = NSPLIT == 1 ? npairs : (npairs + 7) / 8 * 8 * NSPLIT;
   hipLaunchKernelGGL((decode_bf16_stage_kernel<D, NSPLIT>), dim3((unsigned)blocks), dim3(kDecodeWaves * 64),
@@ -185,13 +180,8 @@ int launch_stage(const G4DecodeArgs& a, hipStream_t st) {
 
 template <int D, int NSPLIT, bool LONG>
 int launch_fast(const G4DecodeArgs& a, int t_alloc, size_t lds, hipStream_t st) {
-  static bool attr_set = false;  // raise the dynamic-LDS limit once per instantiation
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)decode_bf16_fast_kernel<D, NSPLIT, LONG>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLdsFast) != hipSuccess)
-      return fail(G4_ERR_LAUNCH, "g4_decode_attention: cannot raise the LDS limit");
-    attr_set = true;
-  }
+  const int setup = device_setup(nullptr);  // raised LDS limits
+  if (setup != G4_OK) return setup;
   const int64_t npairs = (int64_t)a.batch * a.kv_heads;
   const int64_t blocks = NSPLIT == 1 ? npairs : (npairs + 7) / 8 * 8 * NSPLIT;
   hipLaunchKernelGGL((decode_bf16_fast_kernel<D, NSPLIT, LONG>), dim3((unsigned)blocks), dim3(kDecodeWaves * 64), lds, st,
@@ -218,15 +208,8 @@ bool use_split_keys(const G4DecodeArgs& a) {
 
 template <int D>
 int launch_split_keys(const G4DecodeArgs& a, hipStream_t st) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)decode_bf16_splitk_scores_kernel<D>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)stage_lds_bytes(16)) != hipSuccess ||
-        hipFuncSetAttribute((const void*)decode_bf16_splitk_values_kernel<D>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)stage_lds_bytes(16)) != hipSuccess)
-      return fail(G4_ERR_LAUNCH, "g4_decode_attention: cannot raise the LDS limit");
-    attr_set = true;
-  }
+  const int setup = device_setup(nullptr);  // raised LDS limits
+  if (setup != G4_OK) return setup;
   const int64_t npairs = (int64_t)a.batch * a.kv_heads;
   SplitKWorkspace ws;
   ws.n_splits = (a.capacity + kSplitSlots - 1) / kSplitSlots;
@@ -288,6 +271,37 @@ int launch_two_pass(const G4DecodeArgs& a, hipStream_t st) {
 }
 
 }  // namespace
+}  // namespace g4
+
+namespace g4 {
+
+// Raises the dynamic-LDS limit of every decode kernel launched with more than the 64 KiB default
+// (run once per device by device_setup, before any of them launches on it).
+int setup_decode_kernels(int) {
+  const int stage = (int)stage_lds_bytes(16);
+  const struct {
+    const void* fn;
+    int bytes;
+  } kernels[] = {
+      {(const void*)decode_bf16_stage_kernel<128, 1>, stage},
+      {(const void*)decode_bf16_stage_kernel<256, 2>, stage},
+      {(const void*)decode_bf16_fast_kernel<128, 1, true>, (int)kMaxLdsFast},
+      {(const void*)decode_bf16_fast_kernel<128, 1, false>, (int)kMaxLdsFast},
+      {(const void*)decode_bf16_fast_kernel<256, 2, true>, (int)kMaxLdsFast},
+      {(const void*)decode_bf16_fast_kernel<256, 2, false>, (int)kMaxLdsFast},
+      {(const void*)decode_bf16_fast_kernel<256, 1, true>, (int)kMaxLdsFast},
+      {(const void*)decode_bf16_fast_kernel<256, 1, false>, (int)kMaxLdsFast},
+      {(const void*)decode_bf16_splitk_scores_kernel<128>, stage},
+      {(const void*)decode_bf16_splitk_scores_kernel<256>, stage},
+      {(const void*)decode_bf16_splitk_values_kernel<128>, stage},
+      {(const void*)decode_bf16_splitk_values_kernel<256>, stage},
+  };
+  for (const auto& k : kernels)
+    if (hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize, k.bytes) != hipSuccess)
+      return fail(G4_ERR_LAUNCH, "g4_init: cannot raise the LDS limit of a decode kernel to %d B", k.bytes);
+  return G4_OK;
+}
+
 }  // namespace g4
 
 extern "C" size_t g4_decode_workspace_size(const G4DecodeArgs* args) {
@@ -352,6 +366,8 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
   if (a.num_splits == G4_DECODE_TWO_PASS && !two_pass_applies(a))
     return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: two-pass needs bf16, head_dim 128/256, capacity <= %d",
                 kTpMaxSlots);
+  if (a.dtype == G4_DTYPE_BF16 && a.head_dim > 256)
+    return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: bf16 head_dim %d (bf16 decode covers 32..256)", a.head_dim);
   if (use_two_pass(a)) {
     const size_t need = twopass_workspace_bytes(a.batch * a.kv_heads, a.group, a.capacity);
     if (!a.workspace || a.workspace_bytes < need)

@@ -13,6 +13,19 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Maps a hipError_t of the launch just made to G4_OK / G4_ERR_LAUNCH.
 int check_launch(const char* what);
 
+// Devices the per-device set-up tracks (device ordinals 0 .. kMaxDevices - 1).
+constexpr int kMaxDevices = 64;
+
+// The library's one-time set-up of the current device (g4_init): raises the dynamic-LDS limit of
+// every kernel that launches with more than the 64 KiB default. Runs once per device (std::call_once,
+// so concurrent first calls wait for one set-up); later calls only read the recorded result.
+// Returns G4_OK or the set-up's error code (message via g4_last_error), and the device ordinal.
+int device_setup(int* device);
+
+// Per-source set-up steps run by device_setup for `device` (the current device).
+int setup_decode_kernels(int device);
+int setup_prefill_kernels(int device);
+
 // Head dims with an instantiated kernel: powers of two 8..512 (bf16 attention: 32..256).
 inline bool supported_head_dim(int d) { return d >= 8 && d <= 512 && (d & (d - 1)) == 0; }
 

@@ -202,29 +202,30 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(G4PrefillArgs a, int t
 
 constexpr int kLdsBytes = 160 * 1024;  // gfx950 LDS per workgroup
 
-// Largest key-mask row the LDS-staged kernel can hold next to its static tile buffers (bytes;
-// 0 when the limit cannot be raised). Queried and set once per instantiation.
 // Two waves per SIMD, two 16-row column blocks each (measured per 32-key chunk against one wave per
 // SIMD with three or four blocks, which reuse each LDS tile more but leave a lone wave to overlap
 // its own MFMA, LDS and vector work: 1.85 ms vs 2.04 / 2.66 ms for the config-4 global layer).
 constexpr int kPfBlocks = 2;  // 16-row column blocks per wave
 constexpr int kPfWaves = 8;   // waves per workgroup
 
+// Largest key-mask row (bytes) the LDS-staged kernel of head dim 128 / 256 can hold next to its
+// static tile buffers on each device; 0 when the limit could not be raised. Written once per device
+// by setup_prefill_kernels (under device_setup's std::call_once), read after it.
+int g_lds_max_seq[kMaxDevices][2];
+
 template <int D>
-int prefill_lds_max_seq() {
-  static int max_seq = -1;
-  if (max_seq < 0) {
-    hipFuncAttributes attr;
-    max_seq = 0;
-    if (hipFuncGetAttributes(&attr, (const void*)prefill_bf16_lds_kernel<D, kPfBlocks, kPfWaves>) == hipSuccess) {
-      const int room = (kLdsBytes - (int)attr.sharedSizeBytes) / 16 * 16;
-      const int cap = room < kPfMaxSeq ? room : kPfMaxSeq;
-      if (cap > 0 && hipFuncSetAttribute((const void*)prefill_bf16_lds_kernel<D, kPfBlocks, kPfWaves>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, cap) == hipSuccess)
-        max_seq = cap;
-    }
-  }
-  return max_seq;
+int raise_prefill_lds_limit(int device) {
+  int& max_seq = g_lds_max_seq[device][D == 256];
+  max_seq = 0;
+  hipFuncAttributes attr;
+  if (hipFuncGetAttributes(&attr, (const void*)prefill_bf16_lds_kernel<D, kPfBlocks, kPfWaves>) != hipSuccess)
+    return fail(G4_ERR_LAUNCH, "g4_init: cannot query the prefill kernel's attributes");
+  const int room = (kLdsBytes - (int)attr.sharedSizeBytes) / 16 * 16;
+  const int cap = room < kPfMaxSeq ? room : kPfMaxSeq;
+  if (cap > 0 && hipFuncSetAttribute((const void*)prefill_bf16_lds_kernel<D, kPfBlocks, kPfWaves>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, cap) == hipSuccess)
+    max_seq = cap;
+  return G4_OK;
 }
 
 template <int D>
@@ -236,6 +237,12 @@ void launch_prefill_lds(const G4PrefillArgs& a, hipStream_t st) {
 }
 
 }  // namespace
+
+int setup_prefill_kernels(int device) {
+  const int rc = raise_prefill_lds_limit<128>(device);
+  return rc != G4_OK ? rc : raise_prefill_lds_limit<256>(device);
+}
+
 }  // namespace g4
 
 extern "C" int g4_prefill_attention(const G4PrefillArgs* args, void* stream) {
@@ -255,12 +262,18 @@ extern "C" int g4_prefill_attention(const G4PrefillArgs* args, void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (a.dtype == G4_DTYPE_BF16) {
     if (16 % a.group) return fail(G4_ERR_UNSUPPORTED, "g4_prefill_attention: bf16 needs group dividing 16");
+    if (a.head_dim > 256)
+      return fail(G4_ERR_UNSUPPORTED, "g4_prefill_attention: bf16 head_dim %d (bf16 prefill covers 32..256)",
+                  a.head_dim);
+    int dev = 0;
+    const int rc = device_setup(&dev);
+    if (rc != G4_OK) return rc;
     // head dims 128/256: K/V chunks staged through LDS, when the row's key mask fits next to them
-    if (a.head_dim == 256 && a.seq <= prefill_lds_max_seq<256>()) {
+    if (a.head_dim == 256 && a.seq <= g_lds_max_seq[dev][1]) {
       launch_prefill_lds<256>(a, st);
       return check_launch("g4_prefill_attention");
     }
-    if (a.head_dim == 128 && a.seq <= prefill_lds_max_seq<128>()) {
+    if (a.head_dim == 128 && a.seq <= g_lds_max_seq[dev][0]) {
       launch_prefill_lds<128>(a, st);
       return check_launch("g4_prefill_attention");
     }

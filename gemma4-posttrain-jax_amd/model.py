@@ -171,6 +171,10 @@ def pack_weights(params: Gemma4TextParams, config: Gemma4TextConfig) -> PackedWe
     for i, lp in enumerate(params.layers):
         a = lp.attention
         M, R, H, D = a.q_proj.shape
+        if params.embed_tokens.dtype == torch.bfloat16 and D > 256:
+            raise ValueError(
+                f"layer {i}: head dim {D} with bf16 parameters is not supported by the native kernels (bf16 "
+                "attention covers head dims 32..256); set global_head_dim <= 256 or run the layer in float32")
         wq = a.q_proj.permute(0, 2, 1, 3).reshape(M, H * R * D)
         parts = [wq]
         has_k = a.k_proj is not None

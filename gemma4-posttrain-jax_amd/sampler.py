@@ -17,7 +17,7 @@ from typing import Any, NamedTuple, Protocol
 
 import torch
 
-from . import kernels
+from . import _lib, kernels
 from .config import Gemma4TextConfig
 from .kvcache import KVCache, init_kv_cache
 from .model import Gemma4Output, Gemma4TextParams, _proj, forward_gemma4_lm, forward_gemma4_text
@@ -150,6 +150,7 @@ class GraphedDecodeStep:
         self.token_out = torch.zeros(B, dtype=torch.int32, device=dev)
         self.logp_out = torch.zeros(B, dtype=torch.float32, device=dev)
         saved_key = None if key is None else key.clone()
+        _lib.init_device(dev.index if dev.index is not None else torch.cuda.current_device())
         self._forward()  # eager warm-up: its key split is undone below
         if key is not None:
             key.copy_(saved_key)
@@ -249,7 +250,9 @@ def _proposal(logits32: torch.Tensor, temperature: float, top_k: int,
     if top_p < 1:
         w = torch.exp(scores - scores.max(dim=-1, keepdim=True).values)
         probs = w / w.sum(dim=-1, keepdim=True)
-        previous = torch.cumsum(probs, dim=-1) - probs
+        # mass before each column: 0 followed by the cumulative sum without its last entry, as
+        # sampler.py:172-174 forms it (cumsum - probs can round one ulp lower at the boundary)
+        previous = torch.cat([torch.zeros_like(probs[:, :1]), torch.cumsum(probs, dim=-1)[:, :-1]], dim=-1)
         keep = (previous < top_p) | (torch.arange(scores.shape[-1], device=scores.device)[None, :] == 0)
         scores = torch.where(keep, scores, torch.full_like(scores, -math.inf))
     return scores.contiguous(), indices.to(torch.int32).contiguous()
@@ -333,8 +336,11 @@ def generate(
         completion_ids[:, step] = token
         completion_mask[:, step] = active
         rollout_logps[:, step] = logp
-        next_active = active & ~torch.isin(token.long(), eos) if len(sc.eos_ids) else active
-        any_active = bool(next_active.any())  # the only host sync per step (while_loop's cond)
+        if len(sc.eos_ids):
+            next_active = active & ~torch.isin(token.long(), eos)
+            any_active = bool(next_active.any())  # the only host sync per step (while_loop's cond)
+        else:  # without EOS ids no row finishes: the loop runs all N steps and never waits on the device
+            next_active, any_active = active, True
         if step + 1 < N and any_active:
             pos = (prompt_lengths + step).to(torch.int32)
             if fused:

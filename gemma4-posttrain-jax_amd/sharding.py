@@ -48,6 +48,22 @@ def tree_leaves(tree: Any) -> list[torch.Tensor]:
     return out
 
 
+def constrain_batch(x: torch.Tensor, mesh=None) -> torch.Tensor:
+    """sharding.py:186-189: the batch-axis sharding constraint. On one GPU the whole batch is
+    already on the device, so this is the identity (``mesh`` must be None)."""
+
+    _no_mesh(mesh)
+    return x
+
+
+def constrain_batch_tree(tree: Any, mesh=None) -> Any:
+    """sharding.py:192-199: ``constrain_batch`` over every leaf of a pytree; the identity on one
+    GPU (``mesh`` must be None). The tree is returned as is, leaves of any type included."""
+
+    _no_mesh(mesh)
+    return tree
+
+
 def _cast(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     if t.dtype == dtype:
         return t.clone()  # a new tree, as the reference's astype inside jit returns new buffers

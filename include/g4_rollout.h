@@ -5,9 +5,11 @@
  * The reference has no native layer: each entry point below replaces an XLA-lowered JAX
  * expression of gemma4_posttrain_jax/model.py, cited per function. All entry points are
  * stream-ordered on the `hipStream_t` passed as `stream`, launch nothing else, allocate
- * nothing, never synchronise the device, and keep no state between calls (reentrant). They
- * return 0 on success or a negative G4_ERR_* code after a host-side argument check, before any
- * launch; `g4_last_error()` then describes the failure (thread-local text).
+ * nothing, never synchronise the device, and keep no state between calls (reentrant). The one
+ * piece of library state is the per-device set-up of g4_init, done once per device and guarded
+ * against concurrent first calls. They return 0 on success or a negative G4_ERR_* code after a
+ * host-side argument check, before any launch; `g4_last_error()` then describes the failure
+ * (thread-local text).
  *
  * Device data layout (per cache layer, element type = `dtype`):
  *   cache_k   [B, Hkv, slot_stride, D]   key rows, head-major; row b,h,slot at
@@ -38,6 +40,17 @@ enum {
   G4_ERR_LAUNCH = -3,      /* the HIP launch itself failed */
   G4_ERR_WORKSPACE = -4    /* workspace missing or too small */
 };
+
+/*
+ * One-time set-up of the current HIP device: raises the dynamic-LDS limit of the decode and
+ * prefill kernels that launch with more than the 64 KiB default (hipFuncSetAttribute). The first
+ * call on a device does the work (std::call_once: concurrent first calls wait for it), later calls
+ * return its recorded result. g4_decode_attention and g4_prefill_attention call it themselves
+ * before their first launch on a device; a caller that captures those calls into a HIP graph calls
+ * g4_init once per device beforehand, so that no set-up call falls inside the capture. No
+ * reference counterpart: XLA sets kernel attributes when it compiles the module.
+ */
+int g4_init(void);
 
 enum { G4_DTYPE_F32 = 0, G4_DTYPE_BF16 = 1 };
 enum { G4_CACHE_LINEAR = 0, G4_CACHE_RING = 1 };
@@ -140,7 +153,7 @@ typedef struct G4DecodeArgs {
   int32_t batch;
   int32_t kv_heads;
   int32_t group;        /* R <= 16 */
-  int32_t head_dim;     /* 64, 128, 256 or 512 */
+  int32_t head_dim;     /* bf16: 32, 64, 128 or 256; f32: 8 .. 512 */
   int32_t capacity;     /* C or Wc */
   int32_t slot_stride;
   int32_t window;       /* sliding window W (ring caches); ignored for linear */
@@ -195,8 +208,8 @@ typedef struct G4PrefillArgs {
   int32_t batch;
   int32_t seq;          /* S (queries = keys) */
   int32_t kv_heads;
-  int32_t group;        /* R */
-  int32_t head_dim;
+  int32_t group;        /* R (bf16: a divisor of 16) */
+  int32_t head_dim;     /* bf16: 32, 64, 128 or 256; f32: 8 .. 512 */
   int32_t window;       /* 0 = global (causal only) */
   const uint8_t* key_mask;   /* [B, key_mask_stride] */
   int32_t key_mask_stride;

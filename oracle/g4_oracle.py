@@ -243,10 +243,16 @@ def init_params(
     std: float = 0.02,
     norm_std: float = 0.0,
     layer_scalar_min: float = 1.0,
+    qk_norm_scale: float = 1.0,
 ) -> Params:
     """Seeded random weights ~N(0, std); norms ``1 + norm_std*N``; ``layer_scalar`` U[min, 1]
     (the recipe of tests/conftest.py:67-87 with BASELINE's N(0, 0.02) default). Values are
-    rounded to ``dtype``. Generation order is fixed so the GPU tests can rebuild the same weights."""
+    rounded to ``dtype``. Generation order is fixed so the GPU tests can rebuild the same weights.
+
+    ``qk_norm_scale`` multiplies the q / k norm weights (drawn as above). With weights near 1 the
+    normed q and k have unit RMS and the scale-1.0 scores reach ~sqrt(D) in magnitude, where one
+    bf16 ulp of a score moves a probability by several percent; bf16 test models that must be
+    determined to 2e-2 at the logits use ~0.35, which keeps scores O(1)."""
 
     rng = np.random.default_rng(seed)
     M, Hq = cfg.hidden_size, cfg.num_attention_heads
@@ -273,8 +279,8 @@ def init_params(
         k = None if shared else w(M, H, D)
         v = None if (shared or not layer_has_v_proj(cfg, i)) else w(M, H, D)
         o = w(R, H, D, M)
-        qn = norm(D)
-        kn = None if shared else norm(D)
+        qn = cast(norm(D) * np.float32(qk_norm_scale), dtype)
+        kn = None if shared else cast(norm(D) * np.float32(qk_norm_scale), dtype)
         F = layer_intermediate_size(cfg, i)
         mlp = MLPParams(w(M, F), w(M, F), w(F, M))
         ple = PLEParams(w(M, P), w(P, M), norm(M)) if P else None
@@ -517,27 +523,31 @@ def attention_core(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask: np.ndarray
     q ``[B,S,R,H,D]``, k/v ``[B,T,H,D]``, mask broadcastable to ``[B,1,1,S,T]`` (or ``[B,R,H,S,T]``).
     scores = einsum in ``dtype`` (f32 accumulation, one rounding); masked -> ``finfo(dtype).min``;
     softmax in f32; probs rounded to ``dtype``; ``probs @ v`` accumulated in f32, rounded once.
+    Under ``accumulate_f64`` both products accumulate in f64 (then round through f32), which gives
+    the rounding of the exact dot product wherever f32 accumulation orders disagree near a bf16
+    rounding boundary.
     A fully-masked row therefore averages all T keys (every score equals the fill value).
     Pinned against a float64 textbook softmax-attention and the fully-masked / single-key closed
     forms in tests/test_oracle_attention.py."""
 
     B, S, R, H, D = q.shape
     T = k.shape[1]
+    acc = _ACCUMULATE[-1]  # f32, or f64 under accumulate_f64 (the exactly rounded products)
     out = np.empty((B, S, R, H, D), np.float32)
-    qt = q.astype(np.float32).transpose(0, 2, 3, 1, 4)  # [B,R,H,S,D]
-    kt = k.astype(np.float32).transpose(0, 2, 3, 1)  # [B,H,D,T]
-    vt = v.astype(np.float32).transpose(0, 2, 1, 3)  # [B,H,T,D]
+    qt = q.astype(acc).transpose(0, 2, 3, 1, 4)  # [B,R,H,S,D]
+    kt = k.astype(acc).transpose(0, 2, 3, 1)  # [B,H,D,T]
+    vt = v.astype(acc).transpose(0, 2, 1, 3)  # [B,H,T,D]
     mask = np.broadcast_to(mask, (B, R, H, S, T)) if mask.shape[1] != R else mask
     fill = fill_min(dtype)
     blk = max(1, min(S, (1 << 24) // max(1, B * R * H * T)))
     for s0 in range(0, S, blk):
         s1 = min(S, s0 + blk)
-        sc = cast(np.matmul(qt[:, :, :, s0:s1], kt[:, None]), dtype)  # [B,R,H,s,T]
+        sc = cast(np.matmul(qt[:, :, :, s0:s1], kt[:, None]).astype(np.float32), dtype)  # [B,R,H,s,T]
         sc = np.where(np.broadcast_to(mask, (B, R, H, S, T))[:, :, :, s0:s1], sc, fill)
         m = sc.max(axis=-1, keepdims=True)
         e = np.exp(sc - m)
         p = cast(e / e.sum(axis=-1, keepdims=True, dtype=np.float32), dtype)
-        o = cast(np.matmul(p, vt[:, None]), dtype)  # [B,R,H,s,D]
+        o = cast(np.matmul(p.astype(acc), vt[:, None]).astype(np.float32), dtype)  # [B,R,H,s,D]
         out[:, s0:s1] = o.transpose(0, 3, 1, 2, 4)
     return out
 

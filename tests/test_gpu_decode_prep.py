@@ -19,14 +19,17 @@ FLAGS_Q = _lib.G4_APPEND_NORM_Q | _lib.G4_APPEND_ROPE_Q
 FLAGS_KV = _lib.G4_APPEND_NORM_K | _lib.G4_APPEND_ROPE_K | _lib.G4_APPEND_NORM_V
 
 
-@pytest.mark.parametrize("B,D,ring,cap,shared", [(8, 256, True, 512, False), (8, 256, False, 768, False),
-                                                 (256, 256, True, 512, False), (8, 256, True, 512, True),
-                                                 (6, 128, False, 300, False)])
-def test_decode_fused_prep_matches_append_then_attention(device, B, D, ring, cap, shared):
-    H, R = 2, 4
+@pytest.mark.parametrize("B,H,R,D,ring,cap,shared", [
+    (8, 2, 4, 256, True, 512, False), (8, 2, 4, 256, False, 768, False), (256, 2, 4, 256, True, 512, False),
+    (8, 2, 4, 256, True, 512, True), (6, 2, 4, 128, False, 300, False),
+    # R != 4: waves with no q head of their own (R < 4) and the loop over heads w + 4.. (R > 4), at
+    # and beyond 256 (b, kv head) pairs
+    (128, 2, 1, 256, True, 512, False), (64, 4, 2, 256, False, 768, False), (128, 2, 8, 256, True, 512, False),
+    (128, 2, 8, 128, True, 512, True), (32, 8, 16, 128, False, 600, False), (8, 2, 16, 256, True, 512, False)])
+def test_decode_fused_prep_matches_append_then_attention(device, B, H, R, D, ring, cap, shared):
     W = 512 if ring else 0
-    g = torch.Generator(device="cuda").manual_seed(B + cap + shared)
-    rng = np.random.default_rng(B + cap)
+    g = torch.Generator(device="cuda").manual_seed(B + cap + shared + 100 * R)
+    rng = np.random.default_rng(B + cap + R)
     qkv = torch.randn((B, 1, (H * R + 2 * H) * D), device="cuda", generator=g).to(torch.bfloat16)
     q = qkv[..., :H * R * D].view(B, 1, H, R, D)
     k = qkv[..., H * R * D:(H * R + H) * D].view(B, 1, H, D)
@@ -118,3 +121,103 @@ def test_graphed_decode_with_fused_preparation_matches_unfused(device, monkeypat
     for i, (x, y) in enumerate(zip(ca.layers, cb.layers)):
         if x is not None:
             assert torch.equal(x.key, y.key) and torch.equal(x.value_t, y.value_t), f"layer {i}"
+
+
+ROLLOUT_CFG = dict(
+    vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=5, num_attention_heads=16,
+    num_key_value_heads=2, head_dim=128, global_head_dim=128,
+    layer_types=["sliding_attention", "sliding_attention", "full_attention", "sliding_attention", "full_attention"],
+    sliding_window=16, num_kv_shared_layers=2, hidden_size_per_layer_input=0, final_logit_softcapping=30.0,
+)
+
+
+def test_graphed_rollout_batch_step_matches_oracle(device):
+    """The composition the B=256 rollout runs, on a small model that takes every one of its
+    kernels: 128 rows x 2 kv heads = 256 pairs (the fused q/k/v preparation inside the two-launch
+    attention), R = 8, intermediate 512 (the gated-GELU gate/up GEMM and the split-K down
+    projection into g4_residual_norm_splitk), kv-shared layers, a 16-slot ring that wraps, a
+    left-padded row and a row that finishes. Each graphed step runs on the oracle's exact cache
+    state: the logits graph's logits within max-abs 2e-2 of the oracle's decode_step
+    (model.py:571-709), and the sampling graph's tokens equal the oracle's categorical draw
+    (sampler.py:145-183, 265) over the same logits and key, logp within 2e-6. One step is also
+    replayed eagerly, kernel by kernel (tests/kernel_trace.py): bitwise the graph's logits and
+    caches, every kernel within one bf16 rounding of the oracle on its recorded inputs."""
+
+    import sys
+    from pathlib import Path
+
+    sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
+    from gpu_util import TOL, load_oracle_cache, model_bars, to_np
+    from kernel_trace import KernelTrace, check_trace
+    from oracle import g4_oracle as O
+    from oracle import jax_random as JR
+
+    from gemma4_posttrain_jax_amd import config as C
+    from gemma4_posttrain_jax_amd import model as M
+    from gemma4_posttrain_jax_amd import sampler as SMP
+
+    ocfg = O.config_from_hf(ROLLOUT_CFG)
+    # weights N(0, 0.02) and q/k norm weights ~0.25 keep the logits below 1.5 (one bf16 ulp 0.0078)
+    # and the model determined to 2e-2: the oracle's own f32-vs-f64 spread on this prefill is 0.014
+    # (0.023 at std 0.03 / q/k 0.35, where logits reach 2.2 and one ulp is 0.0156)
+    oparams = O.init_params(ocfg, seed=8, dtype=O.BF16, std=0.02, norm_std=0.05, layer_scalar_min=0.8,
+                            qk_norm_scale=0.25)
+    cfg = C.config_from_hf(ROLLOUT_CFG)
+    params = M.params_from_numpy(oparams, cfg, dtype=torch.bfloat16, device=device)
+    B, P, N = 128, 10, 12
+    rng = np.random.default_rng(14)
+    ids = rng.integers(3, 512, (B, P)).astype(np.int32)
+    mask = np.ones_like(ids, dtype=bool)
+    mask[1, :4] = False
+    ids[1, :4] = 0
+    ids_d, mask_d = torch.from_numpy(ids).to(device), torch.from_numpy(mask).to(device)
+    out_l = SMP.prefill(params, cfg, ids_d, mask_d, max_new_tokens=N)
+    out_s = SMP.prefill(params, cfg, ids_d, mask_d, max_new_tokens=N)
+    ref, _, rc = O.prefill(oparams, ocfg, ids, mask, max_new_tokens=N, dtype=O.BF16)
+    err = float(np.abs(to_np(out_l.logits) - ref).max())
+    assert err <= TOL[O.BF16], f"prefill logits: {err}"
+    key = SMP.key_tensor(21, device)
+    key_host = JR.prng_key(21)
+    eng_l = SMP.GraphedDecodeStep(params, cfg, out_l.kv_cache)
+    eng_s = SMP.GraphedDecodeStep(params, cfg, out_s.kv_cache, temperature=1.0, key=key)
+    assert M._fused_decode_prep(eng_l.cache.layers[0].key, B * 2, 128, eng_l.cache.layers[0])
+    pos = mask.sum(-1).astype(np.int32)
+    tok = ref[:, -1].argmax(-1).astype(np.int32)
+    results = []
+    traced = False
+    for step in range(N - 1):  # 10 prompt slots + 11 steps: the 16-slot ring wraps
+        am = np.ones(B, bool)
+        am[2] = step < 4  # row 2 finishes
+        c_l = load_oracle_cache(eng_l.cache, rc, O.BF16)
+        c_s = load_oracle_cache(eng_s.cache, rc, O.BF16)
+        assert eng_l.length == eng_s.length == c_l.length == c_s.length
+        t, p, a = (torch.from_numpy(x).to(device) for x in (tok, pos + step, am))
+        logits = to_np(eng_l.step(t, p, a))
+        s_tok, s_logp = (x.cpu().numpy().copy() for x in eng_s.step_sample(t, p, a))
+        if step == 7 and not traced:  # after the ring wrap: the same step eagerly, kernel by kernel
+            graph_layers = [None if l is None else (l.key.clone(), l.value_t.clone()) for l in eng_l.cache.layers]
+            c_l = load_oracle_cache(eng_l.cache, rc, O.BF16)
+            slot = torch.full((B,), c_l.length, dtype=torch.int32, device=device)
+            with KernelTrace([0, 1, 2, 127], B) as trace:
+                eager = M.forward_gemma4_lm(params, t[:, None], p[:, None], config=cfg, attention_mask=a[:, None],
+                                            kv_cache=c_l, cache_mode="append", logits_to_keep=1, write_pos=slot)
+            np.testing.assert_array_equal(to_np(eager.logits[:, -1]), logits)
+            for g_, l_ in zip(graph_layers, eager.kv_cache.layers):
+                if l_ is not None:
+                    assert torch.equal(g_[0], l_.key) and torch.equal(g_[1], l_.value_t)
+            check_trace(trace, window=cfg.sliding_window)
+            traced = True
+        with O.accumulate_f64():
+            ref64, _, _ = O.decode_step(oparams, ocfg, tok, pos + step, rc, attention_mask=am, dtype=O.BF16)
+        ref, _, rc = O.decode_step(oparams, ocfg, tok, pos + step, rc, attention_mask=am, dtype=O.BF16)
+        results.append(model_bars(O.BF16, logits, ref[:, -1], ref64[:, -1]))
+        key_host, sample_key = JR.split(key_host)
+        want_tok, want_logp = O.sample_token(logits, temperature=1.0, key=sample_key)
+        np.testing.assert_array_equal(s_tok, want_tok, err_msg=f"step {step}")
+        np.testing.assert_allclose(s_logp, want_logp, rtol=0, atol=2e-6, err_msg=f"step {step}")
+        tok = ref[:, -1].argmax(-1).astype(np.int32)
+    assert traced
+    assert [int(w) & 0xFFFFFFFF for w in key.cpu().tolist()] == [int(w) for w in key_host]
+    print("steps (error, bar, oracle spread):", [tuple(round(v, 5) for v in r) for r in results])
+    for i, (err, bar, spread) in enumerate(results):
+        assert err <= bar, f"step {i}: max |logits - oracle| = {err} > {bar} (oracle spread {spread})"

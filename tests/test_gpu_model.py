@@ -82,19 +82,21 @@ def test_cfg1_greedy_rollout_matches_hf_golden_and_oracle(device):
     assert cache.length == ref_cache.length == 24 + 31
 
 
-@pytest.mark.parametrize("seed", [3, 6])
+@pytest.mark.parametrize("seed", [3, 6, 12])
 def test_bf16_prefill_and_decode_calls_match_oracle(device, seed):
     """bf16 model with kv-shared layers, left padding, a row that finishes, ring wrap. Every call
     (prefill, then six decode steps) runs on the oracle's exact inputs (its cache state is loaded
-    into the device cache), and its logits must lie within 2e-2 of the oracle's plus the oracle's
-    own f32-vs-f64 accumulation spread on that call (gpu_util.model_bars). The cache the call
-    writes must match the oracle's to the same bar."""
+    into the device cache); its logits must lie within max-abs 2e-2 of the oracle's, and so must
+    the cache it writes. The oracle's own f32-vs-f64 accumulation spread on each call is printed
+    next to the error (gpu_util.model_bars)."""
 
     ocfg = O.config_from_hf(SMALL_BF16)
-    # the reference's well-conditioned recipe (grad_tiny, tests/conftest.py:112-125): random bf16
-    # models with larger norm spreads are chaotic, so a last-bit GEMM difference in layer 0 grows
-    # by 2-4x per layer for any two implementations, the oracle against itself included
-    oparams = O.init_params(ocfg, seed=seed, dtype=O.BF16, std=0.03, norm_std=0.05, layer_scalar_min=0.8)
+    # the reference's well-conditioned recipe (grad_tiny, tests/conftest.py:112-125), with the q/k
+    # norm weights scaled to 0.35: at weight ~1 the scale-1.0 scores reach ~8 and one bf16 ulp of a
+    # score moves a probability by ~6 %, so a last-bit GEMM difference in layer 0 grows by 2-4x per
+    # layer for any two implementations, the oracle against itself included
+    oparams = O.init_params(ocfg, seed=seed, dtype=O.BF16, std=0.03, norm_std=0.05, layer_scalar_min=0.8,
+                            qk_norm_scale=0.35)
     cfg = C.config_from_hf(SMALL_BF16)
     params = M.params_from_numpy(oparams, cfg, dtype=torch.bfloat16, device=device)
     rng = np.random.default_rng(7 + seed)
@@ -120,16 +122,17 @@ def test_bf16_prefill_and_decode_calls_match_oracle(device, seed):
             ref64, _, rc64 = O.decode_step(oparams, ocfg, tok, pos + step, rc, attention_mask=am, dtype=O.BF16)
         ref, _, rc = O.decode_step(oparams, ocfg, tok, pos + step, rc, attention_mask=am, dtype=O.BF16)
         results.append(model_bars(O.BF16, to_np(dec.logits)[am], ref[am], ref64[am]))
-        for i, (ours, theirs, theirs64) in enumerate(zip(dec.kv_cache.layers, rc.layers, rc64.layers)):
+        for i, (ours, theirs) in enumerate(zip(dec.kv_cache.layers, rc.layers)):
             if ours is not None:
                 gk, gv = cache_to_ref(ours)
-                for got, want, want64 in ((gk, theirs.key, theirs64.key), (gv, theirs.value, theirs64.value)):
-                    err, bar = model_bars(O.BF16, got, want, want64)
-                    assert err <= bar, f"step {step} layer {i} cache: {err} > {bar}"
+                for got, want in ((gk, theirs.key), (gv, theirs.value)):
+                    err = float(np.abs(got - want).max())
+                    assert err <= TOL[O.BF16], f"step {step} layer {i} cache: {err}"
         cache = dec.kv_cache
         tok = ref[:, -1].argmax(-1).astype(np.int32)
-    for i, (err, bar) in enumerate(results):
-        assert err <= bar, f"call {i}: max |logits - oracle| = {err} > {bar}; all: {results}"
+    print("calls (error, bar, oracle spread):", [tuple(round(v, 5) for v in r) for r in results])
+    for i, (err, bar, spread) in enumerate(results):
+        assert err <= bar, f"call {i}: max |logits - oracle| = {err} > {bar} (oracle spread {spread}); all: {results}"
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
