@@ -103,6 +103,7 @@ PROTOTYPES = {
     "g4_kv_append": (c_int32, [POINTER(G4AppendArgs), c_void_p]),
     "g4_decode_workspace_size": (c_size_t, [POINTER(G4DecodeArgs)]),
     "g4_decode_attention": (c_int32, [POINTER(G4DecodeArgs), c_void_p]),
+    "g4_decode_attention_noalloc": (c_int32, [POINTER(G4DecodeArgs), c_void_p]),
     "g4_prefill_attention": (c_int32, [POINTER(G4PrefillArgs), c_void_p]),
     "g4_kv_source_layers": (c_int32, [c_int32, c_int32, POINTER(c_int32), POINTER(c_int32)]),
     "g4_ring_slot_positions": (c_int32, [c_int32, c_int32, POINTER(c_int32)]),

@@ -275,9 +275,23 @@ int launch_two_pass(const G4DecodeArgs& a, hipStream_t st) {
 
 namespace g4 {
 
+// Scratch of g4_decode_attention_noalloc: the workspace of the two-launch and split-K paths held by
+// the library, one copy per device for the life of the process. In host code `scratch` names a
+// host-side stand-in, not device memory: kernels get the per-device address that
+// hipGetSymbolAddress returns at set-up (g_scratch).
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+void* g_scratch[kMaxDevices];
+
 // Raises the dynamic-LDS limit of every decode kernel launched with more than the 64 KiB default
-// (run once per device by device_setup, before any of them launches on it).
-int setup_decode_kernels(int) {
+// and records this device's address of `scratch` (run once per device by device_setup, with the
+// device current, before any of them launches on it).
+int setup_decode_kernels(int device) {
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !ptr)
+    return fail(G4_ERR_LAUNCH, "g4_init: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+  g_scratch[device] = ptr;
   const int stage = (int)stage_lds_bytes(16);
   const struct {
     const void* fn;
@@ -312,10 +326,11 @@ extern "C" size_t g4_decode_workspace_size(const G4DecodeArgs* args) {
   return splitk_workspace_bytes(args->batch * args->kv_heads, args->group, args->head_dim, args->capacity);
 }
 
-extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
-  using namespace g4;
-  if (!args) return fail(G4_ERR_INVALID, "g4_decode_attention: args is NULL");
-  const G4DecodeArgs& a = *args;
+namespace g4 {
+
+// Host-side argument checks of g4_decode_attention (everything but the workspace, whose need
+// depends on the path these arguments select).
+int validate_decode_args(const G4DecodeArgs& a) {
   if (a.dtype != G4_DTYPE_F32 && a.dtype != G4_DTYPE_BF16)
     return fail(G4_ERR_INVALID, "g4_decode_attention: dtype %d", a.dtype);
   if (a.kind != G4_CACHE_LINEAR && a.kind != G4_CACHE_RING)
@@ -358,9 +373,6 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
     return fail(G4_ERR_INVALID, "g4_decode_attention: NULL q");
   }
   if (a.new_k && !a.cache_k_w) return fail(G4_ERR_INVALID, "g4_decode_attention: fused append needs cache_k_w");
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int t_alloc = (a.capacity + 31) / 32 * 32;
-  const dim3 grid((unsigned)((int64_t)a.batch * a.kv_heads));
   if (a.num_splits < G4_DECODE_TWO_PASS || a.num_splits > 2)
     return fail(G4_ERR_INVALID, "g4_decode_attention: num_splits %d", a.num_splits);
   if (a.num_splits == G4_DECODE_TWO_PASS && !two_pass_applies(a))
@@ -368,6 +380,22 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
                 kTpMaxSlots);
   if (a.dtype == G4_DTYPE_BF16 && a.head_dim > 256)
     return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: bf16 head_dim %d (bf16 decode covers 32..256)", a.head_dim);
+  return G4_OK;
+}
+
+}  // namespace g4
+
+extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
+  using namespace g4;
+  if (!args) return fail(G4_ERR_INVALID, "g4_decode_attention: args is NULL");
+  const G4DecodeArgs& a = *args;
+  {
+    const int rc = validate_decode_args(a);
+    if (rc != G4_OK) return rc;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int t_alloc = (a.capacity + 31) / 32 * 32;
+  const dim3 grid((unsigned)((int64_t)a.batch * a.kv_heads));
   if (use_two_pass(a)) {
     const size_t need = twopass_workspace_bytes(a.batch * a.kv_heads, a.group, a.capacity);
     if (!a.workspace || a.workspace_bytes < need)
@@ -444,4 +472,30 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
     }
   }
   return check_launch("g4_decode_attention");
+}
+
+extern "C" int g4_decode_attention_noalloc(const G4DecodeArgs* args, void* stream) {
+  using namespace g4;
+  if (!args) return fail(G4_ERR_INVALID, "g4_decode_attention_noalloc: args is NULL");
+  if (args->workspace || args->workspace_bytes)
+    return fail(G4_ERR_INVALID, "g4_decode_attention_noalloc: workspace must be NULL / 0 (the library's scratch is used)");
+  {
+    const int rc = validate_decode_args(*args);
+    if (rc != G4_OK) return rc;
+  }
+  G4DecodeArgs a = *args;
+  const size_t need = g4_decode_workspace_size(&a);
+  if (need > kNoAllocScratchBytes)
+    return fail(G4_ERR_WORKSPACE,
+                "g4_decode_attention_noalloc: the call needs %zu B of scratch, more than the %zu B the library holds "
+                "per device; call g4_decode_attention with a workspace",
+                need, kNoAllocScratchBytes);
+  if (need) {
+    int dev = 0;
+    const int rc = device_setup(&dev);
+    if (rc != G4_OK) return rc;
+    a.workspace = g_scratch[dev];
+    a.workspace_bytes = kNoAllocScratchBytes;
+  }
+  return g4_decode_attention(&a, stream);
 }

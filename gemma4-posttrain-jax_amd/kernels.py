@@ -157,12 +157,15 @@ def decode_attention(
     new_k: torch.Tensor | None = None,
     new_v: torch.Tensor | None = None,
     num_splits: int = 0,
+    no_alloc: bool = False,
 ) -> torch.Tensor:
     """g4_decode_attention: q ``[B, Hkv, R, D]`` against ``layer``; returns ``[B, Hkv, R, D]``.
     With ``new_k``/``new_v`` (``[B, Hkv, D]``) the token's K/V is stored at ``q_pos`` first.
     ``num_splits``: 0 lets the library choose; 1 or 2 workgroups per (b, kv head) in one pass;
     ``_lib.G4_DECODE_SPLIT_KEYS`` splits the key range (long rows). A workspace of the size the
-    library asks for is allocated from torch's caching allocator on the current stream."""
+    library asks for is allocated from torch's caching allocator on the current stream; with
+    ``no_alloc`` the call goes to g4_decode_attention_noalloc, which uses the library's own
+    per-device scratch (``out`` must then be given for the call to allocate nothing at all)."""
 
     B, H, R, D = q.shape
     if not q.is_contiguous() or q.dtype != layer.key.dtype:
@@ -192,6 +195,9 @@ def decode_attention(
         new_k=_ptr(new_k), new_v=_ptr(new_v), out=_ptr(out), workspace=None, workspace_bytes=0, prep=None,
         num_splits=num_splits,
     )
+    if no_alloc:
+        _lib.check(_lib.lib().g4_decode_attention_noalloc(ctypes.byref(a), _stream()), "g4_decode_attention_noalloc")
+        return out
     need = _lib.lib().g4_decode_workspace_size(ctypes.byref(a))
     ws = None
     if need:

@@ -196,6 +196,21 @@ size_t g4_decode_workspace_size(const G4DecodeArgs* args);
 int g4_decode_attention(const G4DecodeArgs* args, void* stream);
 
 /*
+ * g4_decode_attention without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference: XLA allocates the scratch of its fused computations itself.
+ * Same arguments, semantics and results as g4_decode_attention, except that `workspace` must be NULL
+ * and `workspace_bytes` 0: the two-launch and split-K paths use a scratch array the library holds,
+ * one copy of 32 MiB per device until the process ends (its address is resolved per device by
+ * g4_init). A call needing more (g4_decode_workspace_size > 32 MiB, e.g. split-K over more than
+ * ~64 (b, kv head) pairs of 32768 slots) is rejected with G4_ERR_WORKSPACE before any launch. Allocates
+ * nothing. Every call on a device shares that device's scratch and the scratch keeps no state between
+ * calls, so calls that overlap on one GPU (on different streams, or on one stream from different
+ * threads without ordering) race; calls ordered on one stream do not.
+ */
+int g4_decode_attention_noalloc(const G4DecodeArgs* args, void* stream);
+
+/*
  * Causal (optionally sliding-window) prefill attention on the chunk's own K/V. Replaces
  * make_qk_masks (model.py:320-335) + the attention einsums of forward_attention
  * (model.py:496-499) in prefill mode (model.py:455-457, 621-623). Query s of row b attends key
