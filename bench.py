@@ -64,6 +64,17 @@ def measured_traffic() -> int | None:
         return None
 
 
+def prefill_counters() -> dict | None:
+    """Counter-based MFMA figures of the config-4 prefill kernel from the committed rocprofv3 --pmc
+    summary (MFMA busy fraction, executed bf16 TFLOP per layer); None when it is absent."""
+
+    path = ROOT / "profiles" / "prefill_attention_config4_mfma.json"
+    try:
+        return json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+
+
 def cpu_info() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -536,6 +547,12 @@ def main() -> int:
             **{f"{k}_ms": round(v["ms"], 3) for k, v in pf.items()},
             **{f"{k}_TFLOP/s": round(v["tflops"], 1) for k, v in pf.items()},
             **{f"{k}_frac_mfma_peak": round(v["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4) for k, v in pf.items()}}
+        pc = prefill_counters()
+        if pc is not None:  # rocprofv3 PMC: SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_BF16
+            for k in ("global", "sliding"):
+                line["prefill_attention"][f"{k}_mfma_busy_counter"] = pc[k]["mfma_busy_frac"]
+                line["prefill_attention"][f"{k}_executed_TFLOP_counter"] = pc[k]["executed_bf16_tflop"]
+            line["prefill_attention"]["counters"] = pc["source"]
     if not args.no_e2b:
         e2b = bench_e2b_decode(args.e2b_steps, 2)
         line["decode_tok_s_b256"] = round(e2b["decode_tok_s"], 1)
