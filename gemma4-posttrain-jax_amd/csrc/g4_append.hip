@@ -104,14 +104,14 @@ __global__ __launch_bounds__(1024) void append_kernel(G4AppendArgs a) {
       if (a.k_out) store_row(reinterpret_cast<T*>(a.k_out) + (bh * a.chunk_stride + s) * D);
     } else {
       if (to_cache) {
-        T* dst = reinterpret_cast<T*>(a.cache_vt) + bh * D * a.slot_stride + slot;
+        T* dst = reinterpret_cast<T*>(a.cache_vt) + bh * D * a.slot_stride;
 #pragma unroll
-        for (int e = 0; e < PER; ++e) E::store(dst, (int64_t)(lane * PER + e) * a.slot_stride, x[e]);
+        for (int e = 0; e < PER; ++e) E::store(dst, vt_index(slot, lane * PER + e, D), x[e]);
       }
       if (a.vt_out) {
-        T* dst = reinterpret_cast<T*>(a.vt_out) + bh * D * a.chunk_stride + s;
+        T* dst = reinterpret_cast<T*>(a.vt_out) + bh * D * a.chunk_stride;
 #pragma unroll
-        for (int e = 0; e < PER; ++e) E::store(dst, (int64_t)(lane * PER + e) * a.chunk_stride, x[e]);
+        for (int e = 0; e < PER; ++e) E::store(dst, vt_index(s, lane * PER + e, D), x[e]);
       }
     }
   }

@@ -15,6 +15,19 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr float kBf16Min = -3.3895313892515355e38f;
 constexpr float kF32Min = -3.4028234663852886e38f;
 
+// Value-cache layout: per (b, kv head) a [slot_stride / 8][D][8] block. The 8 consecutive slots of
+// one value dim are contiguous (16 bytes in bf16: one MFMA operand, read with one 16-byte load), and
+// one slot's D values lie inside one 8*D-element span (4 KiB for bf16, D = 256), so appending a slot
+// touches D / 8 cache lines of 128 bytes rather than D.
+__host__ __device__ __forceinline__ int64_t vt_index(int64_t slot, int d, int D) {
+  return ((slot >> 3) * D + d) * 8 + (slot & 7);
+}
+
+// Byte offset (bf16) of the 16-byte operand of value dim d, slots [8 g, 8 g + 8).
+__host__ __device__ __forceinline__ uint32_t vt_operand_bytes(int g, int d, int D) {
+  return ((uint32_t)g * (uint32_t)D + (uint32_t)d) * 16u;
+}
+
 __host__ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
 #ifdef __HIP_DEVICE_COMPILE__
   return __uint_as_float(b << 16);

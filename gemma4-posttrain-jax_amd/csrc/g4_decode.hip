@@ -76,10 +76,10 @@ __device__ __forceinline__ void fused_append(const G4DecodeArgs& a, int pair, co
   const T* nk = reinterpret_cast<const T*>(a.new_k) + (int64_t)pair * D;
   const T* nv = reinterpret_cast<const T*>(a.new_v) + (int64_t)pair * D;
   T* ck = reinterpret_cast<T*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
-  T* cv = reinterpret_cast<T*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride + kr.new_slot;
+  T* cv = reinterpret_cast<T*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     ck[d] = nk[d];
-    cv[(int64_t)d * a.slot_stride] = nv[d];
+    cv[vt_index(kr.new_slot, d, D)] = nv[d];
   }
 }
 
@@ -140,11 +140,10 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(G4DecodeArgs a, int t_a
   for (int idx = tid; idx < R * D; idx += blockDim.x) {
     const int r = idx / D, d = idx - r * D;
     const float m = stats[2 * r], l = all_masked ? (float)a.capacity : stats[2 * r + 1];
-    const float* vrow = vbase + (int64_t)d * a.slot_stride;
     float o = 0.f;
     for (int key = 0; key < n2; ++key) {
       const float p = all_masked ? 1.0f / l : expf(sc[r * t_alloc + key] - m) / l;
-      const float v = key == kr.new_slot ? newv[d] : vrow[key];
+      const float v = key == kr.new_slot ? newv[d] : vbase[vt_index(key, d, D)];
       o = fmaf(p, v, o);
     }
     out[idx] = o;

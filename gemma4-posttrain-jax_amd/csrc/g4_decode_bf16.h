@@ -67,10 +67,10 @@ __device__ __forceinline__ void store_appended(const G4DecodeArgs& a, int pair, 
                                                const DecodeLds& L) {
   if (kr.new_slot < 0) return;
   uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
-  uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride + kr.new_slot;
+  uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     ck[d] = L.nk[d];
-    cv[(int64_t)d * a.slot_stride] = L.nv[d];
+    cv[vt_index(kr.new_slot, d, D)] = L.nv[d];
   }
 }
 
@@ -148,11 +148,10 @@ __device__ __forceinline__ bool slot_valid_flat(const G4DecodeArgs& a, int b, co
 }
 
 template <int D>
-__device__ __forceinline__ void load_v_chunk(u32x4 (&vv)[D / 16], __amdgpu_buffer_rsrc_t rv, int64_t ss, int kb,
-                                             int col) {
-  const uint32_t voff = (uint32_t)(col * ss + kb) * 2u;
+__device__ __forceinline__ void load_v_chunk(u32x4 (&vv)[D / 16], __amdgpu_buffer_rsrc_t rv, int kb, int col) {
+  const uint32_t voff = vt_operand_bytes(kb >> 3, col, D);
 #pragma unroll
-  for (int i = 0; i < D / 16; ++i) vv[i] = buffer_load16(rv, voff, (uint32_t)(16 * i * ss) * 2u);
+  for (int i = 0; i < D / 16; ++i) vv[i] = buffer_load16(rv, voff, 256u * i);  // value dims 16 i + col
 }
 
 // Replace the appended slot's value (if it falls in this lane's 8 slots) by the staged new V.
@@ -311,7 +310,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_kernel(G4Decode
   for (int c = w; c < n_chunks2; c += NW) {
     const int kb = (c << 5) + 8 * grp;
     u32x4 vv[DB];
-    load_v_chunk<D>(vv, rv, a.slot_stride, kb, col);
+    load_v_chunk<D>(vv, rv, kb, col);
     patch_v<D>(vv, L.nv, kr.new_slot, kb, col);
     pv_chunk<D>(vv, prob_operand(L.pl, t_alloc, kb, R, col), oacc);
   }

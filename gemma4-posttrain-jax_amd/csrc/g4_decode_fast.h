@@ -102,16 +102,17 @@ __device__ __forceinline__ float score_to_lds(const u32x4 (&kv)[2][D / 32], cons
 }
 
 // V^T operands of chunks [8g, 8g + 8) for d-blocks dblock0 .. dblock0 + DPW - 1.
+// (value dims 16 (dblock0 + ii) + col, slots 32 c + 8 grp .. + 7: operand group 4 c + grp)
 template <int DPW>
-__device__ __forceinline__ void fast_load_v(u32x4 (&vg)[8][DPW], __amdgpu_buffer_rsrc_t rv, int64_t ss, int g,
+__device__ __forceinline__ void fast_load_v(u32x4 (&vg)[8][DPW], __amdgpu_buffer_rsrc_t rv, int D, int g,
                                             int n_chunks, int dblock0, int col, int grp) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int c = g * 8 + i;
     if (c < n_chunks) {
-      const uint32_t voff = (uint32_t)(col * ss + (c << 5) + 8 * grp) * 2u;
+      const uint32_t voff = vt_operand_bytes(4 * c + grp, col, D);
 #pragma unroll
-      for (int ii = 0; ii < DPW; ++ii) vg[i][ii] = buffer_load16(rv, voff, (uint32_t)(16 * (dblock0 + ii) * ss) * 2u);
+      for (int ii = 0; ii < DPW; ++ii) vg[i][ii] = buffer_load16(rv, voff, 256u * (dblock0 + ii));
     }
   }
 }
@@ -119,15 +120,15 @@ __device__ __forceinline__ void fast_load_v(u32x4 (&vg)[8][DPW], __amdgpu_buffer
 // fast_load_v with every load issued (a chunk past the row re-reads the last one: an L2 hit), so the
 // number of loads behind it is fixed and later waits need not include them
 template <int DPW>
-__device__ __forceinline__ void fast_load_v_fixed(u32x4 (&vg)[8][DPW], __amdgpu_buffer_rsrc_t rv, int64_t ss, int g,
+__device__ __forceinline__ void fast_load_v_fixed(u32x4 (&vg)[8][DPW], __amdgpu_buffer_rsrc_t rv, int D, int g,
                                                   int n_chunks, int dblock0, int col, int grp) {
   const int c_last = n_chunks > 0 ? n_chunks - 1 : 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int c = g * 8 + i < n_chunks ? g * 8 + i : c_last;
-    const uint32_t voff = (uint32_t)(col * ss + (c << 5) + 8 * grp) * 2u;
+    const uint32_t voff = vt_operand_bytes(4 * c + grp, col, D);
 #pragma unroll
-    for (int ii = 0; ii < DPW; ++ii) vg[i][ii] = buffer_load16(rv, voff, (uint32_t)(16 * (dblock0 + ii) * ss) * 2u);
+    for (int ii = 0; ii < DPW; ++ii) vg[i][ii] = buffer_load16(rv, voff, 256u * (dblock0 + ii));
   }
 }
 
@@ -189,7 +190,6 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_fast_kernel(G4D
   const int col = lane & 15, grp = lane >> 4;
   const int dblock0 = h * (S::NDB / NSPLIT) + w * S::DPW;
   const KeyRange kr = key_range(a, b);
-  const int64_t ss = a.slot_stride;
   const uint32_t pair_bytes = (uint32_t)a.slot_stride * D * 2u;
   const __amdgpu_buffer_rsrc_t rk =
       make_rsrc(reinterpret_cast<const uint16_t*>(a.cache_k) + (int64_t)pair * a.slot_stride * D, pair_bytes);
@@ -237,14 +237,14 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_fast_kernel(G4D
       mx = score_to_lds<D>(k0, qop, vb0, L.sp, t_alloc, c0, R, col, grp, mx);
     }
     __builtin_amdgcn_sched_barrier(0);
-    fast_load_v<S::DPW>(va, rv, ss, 0, n_chunks, dblock0, col, grp);
+    fast_load_v<S::DPW>(va, rv, D, 0, n_chunks, dblock0, col, grp);
     __builtin_amdgcn_sched_barrier(0);
     if (w + NW < n_chunks) {
       patch_k_sel<D>(k1, L.nk, kr.new_slot, c1, col, grp);
       mx = score_to_lds<D>(k1, qop, vb1, L.sp, t_alloc, c1, R, col, grp, mx);
     }
     __builtin_amdgcn_sched_barrier(0);
-    fast_load_v<S::DPW>(vb, rv, ss, 1, n_chunks, dblock0, col, grp);
+    fast_load_v<S::DPW>(vb, rv, D, 1, n_chunks, dblock0, col, grp);
     __builtin_amdgcn_sched_barrier(0);
   } else {  // a long row (capacity beyond 2*NW chunks; its filled part may still be shorter)
     if (w < n_chunks) {
@@ -274,8 +274,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_fast_kernel(G4D
     // V of the first 16 chunks requested now, with the K registers free: it lands while the
     // softmax runs
     __builtin_amdgcn_sched_barrier(0);
-    fast_load_v_fixed<S::DPW>(va, rv, ss, 0, n_chunks, dblock0, col, grp);
-    fast_load_v_fixed<S::DPW>(vb, rv, ss, 1, n_chunks, dblock0, col, grp);
+    fast_load_v_fixed<S::DPW>(va, rv, D, 0, n_chunks, dblock0, col, grp);
+    fast_load_v_fixed<S::DPW>(vb, rv, D, 1, n_chunks, dblock0, col, grp);
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -334,8 +334,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_fast_kernel(G4D
 
   // ---- 5. value pass over this wave's d-blocks -------------------------------------------------
   if (n_chunks2 != n_chunks) {  // a fully masked row reads V over the whole capacity
-    fast_load_v<S::DPW>(va, rv, ss, 0, n_chunks2, dblock0, col, grp);
-    fast_load_v<S::DPW>(vb, rv, ss, 1, n_chunks2, dblock0, col, grp);
+    fast_load_v<S::DPW>(va, rv, D, 0, n_chunks2, dblock0, col, grp);
+    fast_load_v<S::DPW>(vb, rv, D, 1, n_chunks2, dblock0, col, grp);
   }
   floatx4 oacc[S::DPW];
 #pragma unroll
@@ -343,10 +343,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_fast_kernel(G4D
   const int n_groups = (n_chunks2 + 7) / 8;
   for (int g = 0; g < n_groups; g += 2) {
     fast_consume_v<S::DPW>(va, oacc, L, t_alloc, g, n_chunks2, R, dblock0, col, grp, kr.new_slot);
-    if (g + 2 < n_groups) fast_load_v<S::DPW>(va, rv, ss, g + 2, n_chunks2, dblock0, col, grp);
+    if (g + 2 < n_groups) fast_load_v<S::DPW>(va, rv, D, g + 2, n_chunks2, dblock0, col, grp);
     if (g + 1 < n_groups)
       fast_consume_v<S::DPW>(vb, oacc, L, t_alloc, g + 1, n_chunks2, R, dblock0, col, grp, kr.new_slot);
-    if (g + 3 < n_groups) fast_load_v<S::DPW>(vb, rv, ss, g + 3, n_chunks2, dblock0, col, grp);
+    if (g + 3 < n_groups) fast_load_v<S::DPW>(vb, rv, D, g + 3, n_chunks2, dblock0, col, grp);
   }
 
   // ---- the fused append's cache write (after every cache load of this workgroup) ---------------
@@ -356,10 +356,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_fast_kernel(G4D
   if (has_new) {
     constexpr int DS = D / NSPLIT;
     uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
-    uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride + kr.new_slot;
+    uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
     for (int d = h * DS + tid; d < (h + 1) * DS; d += blockDim.x) {
       ck[d] = L.nk[d];
-      cv[(int64_t)d * a.slot_stride] = L.nv[d];
+      cv[vt_index(kr.new_slot, d, D)] = L.nv[d];
     }
   }
   // lane (grp, col < R) holds O^T[d = 16*(dblock0 + ii) + 4*grp + j][head col]

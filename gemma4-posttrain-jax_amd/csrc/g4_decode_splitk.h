@@ -136,9 +136,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_scores_k
   if (has_new) {
     uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
     if (owner && lane < D / 8) *reinterpret_cast<u32x4*>(ck + 8 * lane) = nkv;
-    uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride + kr.new_slot;
+    uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
     const uint16_t* nv = reinterpret_cast<const uint16_t*>(a.new_v) + (int64_t)pair * D;
-    for (int d = tid; d < D; d += blockDim.x) cv[(int64_t)d * a.slot_stride] = nv[d];
+    for (int d = tid; d < D; d += blockDim.x) cv[vt_index(kr.new_slot, d, D)] = nv[d];
   }
 }
 
@@ -187,7 +187,6 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_k
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const int64_t ss = a.slot_stride;
   const __amdgpu_buffer_rsrc_t rv =
       make_rsrc(reinterpret_cast<const uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride,
                 (uint32_t)a.slot_stride * D * 2u);
@@ -200,9 +199,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_k
 #pragma unroll
   for (int i = 0; i < 2 * NW; ++i) {
     if (i < n_here) {
-      const uint32_t voff = (uint32_t)(col * ss + ((cbase + i) << 5) + 8 * grp) * 2u;
+      const uint32_t voff = vt_operand_bytes(4 * (cbase + i) + grp, col, D);
 #pragma unroll
-      for (int ii = 0; ii < DPW; ++ii) vv[i][ii] = buffer_load16(rv, voff, (uint32_t)(16 * ((dh * NW + w) * DPW + ii) * ss) * 2u);
+      for (int ii = 0; ii < DPW; ++ii) vv[i][ii] = buffer_load16(rv, voff, 256u * ((dh * NW + w) * DPW + ii));
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -248,12 +247,11 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_k
     }
   }
   for (int i = n_here; i < n_mine; ++i) {  // fully masked row: slots never scanned
-    const uint32_t voff = (uint32_t)(col * ss + ((cbase + i) << 5) + 8 * grp) * 2u;
+    const uint32_t voff = vt_operand_bytes(4 * (cbase + i) + grp, col, D);
     const bf16x8 pop = prob_operand(sp, kStageStride, (i << 5) + 8 * grp, R, col);
 #pragma unroll
     for (int ii = 0; ii < DPW; ++ii)
-      oacc[ii] = mfma16x16x32(as_bf16x8(buffer_load16(rv, voff, (uint32_t)(16 * ((dh * NW + w) * DPW + ii) * ss) * 2u)), pop,
-                              oacc[ii]);
+      oacc[ii] = mfma16x16x32(as_bf16x8(buffer_load16(rv, voff, 256u * ((dh * NW + w) * DPW + ii))), pop, oacc[ii]);
   }
   // lane (grp, col < R) holds O^T[d = 16*(w*DPW + ii) + 4*grp + j][head col]
   if (col < R) {

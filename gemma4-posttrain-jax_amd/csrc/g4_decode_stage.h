@@ -63,7 +63,6 @@ __device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles* __res
   const int col = lane & 15, grp = lane >> 4;
   const int db = h * NW + w;  // this wave's d-block: value dims [16*db, 16*db + 16)
   const KeyRange kr = key_range(a, b);
-  const int64_t ss = a.slot_stride;
   const uint32_t pair_bytes = (uint32_t)a.slot_stride * D * 2u;
   const __amdgpu_buffer_rsrc_t rk =
       make_rsrc(reinterpret_cast<const uint16_t*>(a.cache_k) + (int64_t)pair * a.slot_stride * D, pair_bytes);
@@ -100,14 +99,14 @@ __device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles* __res
   load_k_chunk<D>(k1, rk, w + NW < n_chunks ? c1 : kc_last << 5, col, grp);
   // Every byte is requested before any compute: a wave stalled on a full memory queue cannot
   // compute anyway, and its K (requested first) has landed by the time its last DMA is queued.
-  const uint32_t soff = (uint32_t)(16 * db * ss) * 2u;
+  const uint32_t soff = 256u * db;  // value dims 16 db + col
   // Every wave issues all 8 DMAs of a half (a chunk past the row's last one re-reads that last
   // chunk, which stays inside the pair's slots), so the compiler knows how many loads are in
   // flight behind each K load and waits for exactly the one it needs.
   const int c_last = n_chunks > 0 ? n_chunks - 1 : 0;
   auto dma_v = [&](VtTiles& tiles, int c) {
     const int cs = c < n_chunks ? c : c_last;
-    const uint32_t voff = (uint32_t)(col * ss + (cs << 5) + 8 * grp) * 2u;
+    const uint32_t voff = vt_operand_bytes(4 * cs + grp, col, D);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&tiles[w][c & (NW - 1)][0],
                                              16, voff, soff, 0, 0);
   };
@@ -214,8 +213,7 @@ __device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles* __res
   value_half(vt_hi, NW);
   oacc += oacc1;
   for (int c = n_chunks; c < n_chunks2; ++c) {  // fully masked linear row: slots never scanned
-    const uint32_t voff = (uint32_t)(col * ss + (c << 5) + 8 * grp) * 2u;
-    const u32x4 v = buffer_load16(rv, voff, (uint32_t)(16 * db * ss) * 2u);
+    const u32x4 v = buffer_load16(rv, vt_operand_bytes(4 * c + grp, col, D), 256u * db);
     oacc = mfma16x16x32(as_bf16x8(v), prob_operand(sp, kStageStride, (c << 5) + 8 * grp, R, col), oacc);
   }
 
@@ -228,8 +226,8 @@ __device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles* __res
     uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
     if (owner && lane >= h * DS / 8 && lane < (h + 1) * DS / 8) *reinterpret_cast<u32x4*>(ck + 8 * lane) = nkv;
     if (grp == 0) {
-      uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride + kr.new_slot;
-      cv[(int64_t)(16 * db + col) * a.slot_stride] = (uint16_t)nvb;
+      uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
+      cv[vt_index(kr.new_slot, 16 * db + col, D)] = (uint16_t)nvb;
     }
   }
   // lane (grp, col < R) holds O^T[d = 16*db + 4*grp + j][head col]

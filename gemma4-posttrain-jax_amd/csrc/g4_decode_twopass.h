@@ -110,9 +110,9 @@ __global__ __launch_bounds__(kTpWavesS * 64) void decode_bf16_tp_scores_kernel(G
                      pkv.x);
       } else {
         prep_math<true, D>(pkv, (pp.flags & G4_APPEND_NORM_V) != 0, false, false, pp.eps);
-        uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride + kr.new_slot;
+        uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
 #pragma unroll
-        for (int e = 0; e < PER; ++e) cv[(int64_t)(lane * PER + e) * a.slot_stride] = (uint16_t)f32_to_bf16_bits(pkv.x[e]);
+        for (int e = 0; e < PER; ++e) cv[vt_index(kr.new_slot, lane * PER + e, D)] = (uint16_t)f32_to_bf16_bits(pkv.x[e]);
       }
     }
     wg_barrier();  // prepared q rows (and the new K row) are in LDS
@@ -143,9 +143,9 @@ __global__ __launch_bounds__(kTpWavesS * 64) void decode_bf16_tp_scores_kernel(G
   if (!PREP && writer) {
     uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
     if (lane < D / 8) *reinterpret_cast<u32x4*>(ck + 8 * lane) = load16(nk + 8 * lane);
-    uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride + kr.new_slot;
+    uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
     const uint16_t* nv = reinterpret_cast<const uint16_t*>(a.new_v) + (int64_t)pair * D;
-    for (int d = lane; d < D; d += 64) cv[(int64_t)d * a.slot_stride] = nv[d];
+    for (int d = lane; d < D; d += 64) cv[vt_index(kr.new_slot, d, D)] = nv[d];
   }
 }
 
@@ -229,7 +229,6 @@ __global__ __launch_bounds__(kTpWavesV * 64) void decode_bf16_tp_values_kernel(G
   const KeyRange kr = key_range(a, b);
   const int n_chunks = (kr.n_keys + 31) >> 5;
   const int n_scanned = n_chunks << 5;
-  const int64_t ss = a.slot_stride;
   const __amdgpu_buffer_rsrc_t rv =
       make_rsrc(reinterpret_cast<const uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride,
                 (uint32_t)a.slot_stride * D * 2u);
@@ -246,12 +245,12 @@ __global__ __launch_bounds__(kTpWavesV * 64) void decode_bf16_tp_values_kernel(G
     sv[i] = u32x4{0u, 0u, 0u, 0u};
     if (512 * i + 8 * lane < row_slots) sv[i] = load16(srow + h0 * row_slots + 512 * i + 8 * lane);
   }
-  const uint32_t soff = (uint32_t)(16 * db * ss) * 2u;
+  const uint32_t soff = 256u * db;  // value dims 16 db + col
   const uint32_t pair_bytes = (uint32_t)a.slot_stride * D * 2u;  // the resource's size: offsets from here read 0
   u32x4 vv[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
-    vv[c] = buffer_load16(rv, c < n_chunks ? (uint32_t)(col * ss + (c << 5) + 8 * grp) * 2u : pair_bytes, soff);
+    vv[c] = buffer_load16(rv, c < n_chunks ? vt_operand_bytes(4 * c + grp, col, D) : pair_bytes, soff);
 
   // exact probabilities: head w first; heads w + 4, w + 8, ... (R > 4) from rows loaded afterwards
   const bool all_masked = tp_probabilities<NB>(sv, w, w < R, sp, kStride, NCH * 32, n_scanned, a.capacity, lane);
@@ -279,7 +278,7 @@ __global__ __launch_bounds__(kTpWavesV * 64) void decode_bf16_tp_values_kernel(G
   if (all_masked) {
     const int cap_chunks = (a.capacity + 31) >> 5;
     for (int c = n_chunks; c < cap_chunks; ++c) {
-      const u32x4 v = buffer_load16(rv, (uint32_t)(col * ss + (c << 5) + 8 * grp) * 2u, soff);
+      const u32x4 v = buffer_load16(rv, vt_operand_bytes(4 * c + grp, col, D), soff);
       oacc = mfma16x16x32(as_bf16x8(v), prob_operand(sp, kStride, (c << 5) + 8 * grp, R, col), oacc);
     }
   }

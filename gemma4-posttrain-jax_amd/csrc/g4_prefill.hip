@@ -119,7 +119,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) void prefill_bf16_kernel(G4Pref
     const int kb = c0 + 8 * grp;
     u32x4 vv[DB];
 #pragma unroll
-    for (int i = 0; i < DB; ++i) vv[i] = load16(vbase + (int64_t)(16 * i + col) * a.k_stride + kb);
+    for (int i = 0; i < DB; ++i) vv[i] = load16(vbase + vt_index(kb, 16 * i + col, D));
     floatx4 acc[2];
     scores(c0, acc);
     uint32_t pw[4] = {0u, 0u, 0u, 0u};
@@ -187,11 +187,10 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(G4PrefillArgs a, int t
     const float lt = masked ? (float)S : l;
     float* orow = reinterpret_cast<float*>(a.out) + ((((int64_t)b * S + pos) * H + h) * R + r) * D;
     for (int d = lane; d < D; d += 64) {
-      const float* vrow = vbase + (int64_t)d * a.k_stride;
       float o = 0.f;
       for (int key = k0; key <= k1; ++key) {
         const float p = masked ? 1.0f / lt : expf(sc[key - kmin] - mx) / lt;
-        o = fmaf(p, vrow[key], o);
+        o = fmaf(p, vbase[vt_index(key, d, D)], o);
       }
       orow[d] = o;
     }

@@ -111,7 +111,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_bf16_lds_kernel(G4PrefillArgs
         const int t = w * S_::VT_W + i;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rv, (__attribute__((address_space(3))) void*)&vt[t][0], 16,
-            (uint32_t)((int64_t)(16 * t + col) * a.k_stride + c0 + 8 * grp) * 2u, 0, 0, 0);
+            vt_operand_bytes(4 * c + grp, 16 * t + col, D), 0, 0, 0);
       }
     }
   };

@@ -89,7 +89,7 @@ def kv_append(
         if k_out is None or vt_out is None:
             raise ValueError("k_out and vt_out go together")
         chunk_stride = k_out.shape[2]
-        if tuple(k_out.shape) != (B, H, chunk_stride, D) or tuple(vt_out.shape) != (B, H, D, chunk_stride):
+        if tuple(k_out.shape) != (B, H, chunk_stride, D) or tuple(vt_out.shape) != (B, H, chunk_stride // 8, D, 8):
             raise ValueError("k_out / vt_out shapes")
         if not (k_out.is_contiguous() and vt_out.is_contiguous()):
             raise ValueError("k_out / vt_out must be contiguous")
@@ -274,12 +274,12 @@ def prefill_attention(
     window: int,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """g4_prefill_attention: q ``[B, S, Hkv, R, D]``, k ``[B, Hkv, Sp, D]``, vt ``[B, Hkv, D, Sp]``
-    (Sp >= S, multiple of 64); returns ``[B, S, Hkv, R, D]``."""
+    """g4_prefill_attention: q ``[B, S, Hkv, R, D]``, k ``[B, Hkv, Sp, D]``, vt ``[B, Hkv, Sp / 8, D, 8]``
+    (the value cache's grouped layout; Sp >= S, multiple of 64); returns ``[B, S, Hkv, R, D]``."""
 
     B, S, H, R, D = q.shape
     Sp = k.shape[2]
-    if not q.is_contiguous() or tuple(k.shape) != (B, H, Sp, D) or tuple(vt.shape) != (B, H, D, Sp):
+    if not q.is_contiguous() or tuple(k.shape) != (B, H, Sp, D) or tuple(vt.shape) != (B, H, Sp // 8, D, 8):
         raise ValueError(f"q {tuple(q.shape)} / k {tuple(k.shape)} / vt {tuple(vt.shape)}")
     if not (k.is_contiguous() and vt.is_contiguous()) or k.dtype != q.dtype or vt.dtype != q.dtype:
         raise ValueError("k/vt must be contiguous and in q's dtype")

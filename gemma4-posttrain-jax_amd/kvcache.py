@@ -1,7 +1,10 @@
 """Device KV cache in the layout the gfx950 kernels read (mirrors model.py:238-255, 557-568).
 
 Per non-shared layer: ``key [B, Hkv, slot_stride, D]`` (head-major rows) and ``value_t
-[B, Hkv, D, slot_stride]`` (values transposed, d-major) in the parameter dtype. Sliding layers
+[B, Hkv, slot_stride / 8, D, 8]`` in the parameter dtype: the values in groups of 8 slots, each
+group stored d-major, so the 8 slots of one value dim are contiguous (one 16-byte MFMA operand in
+bf16) and one slot's D values lie in one 8 * D-element span (an append touches D / 8 cache lines).
+``value_dmajor()`` gives the plain transposed ``[B, Hkv, D, slot_stride]`` view. Sliding layers
 keep a ring of ``Wc = min(window, C)`` slots, global layers ``C = prompt + new`` slots, kv-shared
 layers ``None`` (model.py:557-568). ``slot_stride`` rounds the slot count up to 64 so every row
 is 128-byte aligned. ``key_mask [B, C]`` (bool, 1 byte per entry) records which absolute
@@ -22,9 +25,24 @@ def slot_stride_for(capacity: int) -> int:
     return (capacity + 63) // 64 * 64
 
 
+def group_values(v: torch.Tensor) -> torch.Tensor:
+    """Slot-major values ``[B, H, Sp, D]`` (Sp a multiple of 8) -> the kernels' grouped layout
+    ``[B, H, Sp / 8, D, 8]`` (contiguous copy)."""
+
+    B, H, Sp, D = v.shape
+    return v.reshape(B, H, Sp // 8, 8, D).transpose(3, 4).contiguous()
+
+
+def ungroup_values(vt: torch.Tensor) -> torch.Tensor:
+    """The grouped layout ``[B, H, G, D, 8]`` -> slot-major ``[B, H, 8 G, D]`` (copy)."""
+
+    B, H, G, D, _ = vt.shape
+    return vt.transpose(3, 4).reshape(B, H, G * 8, D)
+
+
 class LayerKVCache(NamedTuple):
     key: torch.Tensor  # [B, Hkv, slot_stride, D]
-    value_t: torch.Tensor  # [B, Hkv, D, slot_stride]
+    value_t: torch.Tensor  # [B, Hkv, slot_stride / 8, D, 8]
     capacity: int  # logical slots: C (linear) or Wc (ring)
     ring: bool
 
@@ -32,11 +50,25 @@ class LayerKVCache(NamedTuple):
     def slot_stride(self) -> int:
         return self.key.shape[2]
 
+    def value_dmajor(self) -> torch.Tensor:
+        """The values as ``[B, Hkv, D, slot_stride]`` (value dim major; a copy)."""
+
+        B, H, G, D, _ = self.value_t.shape
+        return self.value_t.permute(0, 1, 3, 2, 4).reshape(B, H, D, G * 8)
+
+    def set_values(self, v: torch.Tensor) -> None:
+        """Write ``v [B, Hkv, capacity, D]`` (slot major) into slots ``[0, capacity)`` in place."""
+
+        B, H, C, D = v.shape
+        full = self.value_t.permute(0, 1, 2, 4, 3).reshape(B, H, -1, D)  # [B, H, slot_stride, D] copy
+        full[:, :, :C] = v
+        self.value_t.copy_(full.reshape(B, H, -1, 8, D).permute(0, 1, 2, 4, 3))
+
     def reference_layout(self) -> tuple[torch.Tensor, torch.Tensor]:
         """``(key, value)`` as the reference's ``[B, capacity, Hkv, D]`` arrays (copies)."""
 
         k = self.key[:, :, : self.capacity].permute(0, 2, 1, 3).contiguous()
-        v = self.value_t[:, :, :, : self.capacity].permute(0, 3, 1, 2).contiguous()
+        v = self.value_dmajor()[:, :, :, : self.capacity].permute(0, 3, 1, 2).contiguous()
         return k, v
 
 
@@ -49,7 +81,7 @@ class KVCache(NamedTuple):
 def new_layer_cache(batch: int, kv_heads: int, head_dim: int, capacity: int, ring: bool, dtype, device) -> LayerKVCache:
     ss = slot_stride_for(capacity)
     key = torch.zeros((batch, kv_heads, ss, head_dim), dtype=dtype, device=device)
-    value_t = torch.zeros((batch, kv_heads, head_dim, ss), dtype=dtype, device=device)
+    value_t = torch.zeros((batch, kv_heads, ss // 8, head_dim, 8), dtype=dtype, device=device)
     return LayerKVCache(key, value_t, capacity, ring)
 
 
@@ -70,4 +102,5 @@ def init_kv_cache(config: Gemma4TextConfig, batch_size: int, capacity: int, dtyp
     return KVCache(tuple(layers), key_mask, 0)
 
 
-__all__ = ["LayerKVCache", "KVCache", "init_kv_cache", "new_layer_cache", "slot_stride_for", "FULL", "SLIDING"]
+__all__ = ["LayerKVCache", "KVCache", "init_kv_cache", "new_layer_cache", "slot_stride_for", "group_values",
+           "ungroup_values", "FULL", "SLIDING"]

@@ -403,7 +403,7 @@ def forward_gemma4_text(
                 if cache_mode == "prefill" and layer_cache.ring:
                     sp = slot_stride_for(S)
                     k_out = torch.empty((B, H, sp, D), dtype=x.dtype, device=dev)
-                    vt_out = torch.zeros((B, H, D, sp), dtype=x.dtype, device=dev)
+                    vt_out = torch.zeros((B, H, sp // 8, D, 8), dtype=x.dtype, device=dev)
                 kernels.kv_append(layer_cache, k, v, write_pos=slot, flags=flags_q | flags_kv, eps=eps, q=q,
                                   q_out=q_out, q_norm_weight=lp.attention.q_norm.weight,
                                   k_norm_weight=lp.attention.k_norm.weight, rope_cos=cos, rope_sin=sin, k_out=k_out,

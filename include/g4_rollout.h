@@ -14,11 +14,14 @@
  * Device data layout (per cache layer, element type = `dtype`):
  *   cache_k   [B, Hkv, slot_stride, D]   key rows, head-major; row b,h,slot at
  *             ((b*Hkv + h)*slot_stride + slot)*D
- *   cache_vt  [B, Hkv, D, slot_stride]   values stored transposed (d-major); value (b,h,slot,d)
- *             at ((b*Hkv + h)*D + d)*slot_stride + slot
+ *   cache_vt  [B, Hkv, slot_stride/8, D, 8]   values in groups of 8 slots, each group d-major;
+ *             value (b,h,slot,d) at ((b*Hkv + h)*slot_stride + (slot/8)*8)*D + d*8 + slot%8,
+ *             so the 8 slots of one value dim are contiguous (one 16-byte MFMA operand in bf16)
+ *             and one slot's D values lie in one 8*D-element span (an append touches D/8
+ *             cache lines of 128 bytes in bf16, not D)
  * `capacity` is the logical slot count: C (= prompt + new tokens) for a linear (global-layer)
  * cache, Wc = min(window, C) for a ring (sliding-layer) cache. `slot_stride` >= capacity is a
- * multiple of 64, so every K row and V^T row starts 128-byte aligned.
+ * multiple of 64, so every K row and every value group starts 128-byte aligned.
  * Query/output rows of one kv head are contiguous: q and attention output are
  * [B, S, Hkv, R, D] (R = query heads per kv head; reference head order is h*R + r).
  * key_mask is [B, key_mask_stride] uint8 over absolute positions (1 = real token).
@@ -100,10 +103,10 @@ typedef struct G4AppendArgs {
   const float* rope_cos;      /* [B, S, D] f32 (G4_APPEND_ROPE_*) */
   const float* rope_sin;      /* [B, S, D] f32 */
   void* cache_k;        /* [B, Hkv, slot_stride, D] */
-  void* cache_vt;       /* [B, Hkv, D, slot_stride] */
+  void* cache_vt;       /* [B, Hkv, slot_stride/8, D, 8] (grouped values) */
   void* q_out;          /* optional [B, S, Hkv, R, D] prepared q */
   void* k_out;          /* optional [B, Hkv, chunk_stride, D] prepared k of this chunk (prefill input) */
-  void* vt_out;         /* optional [B, Hkv, D, chunk_stride] prepared v, transposed */
+  void* vt_out;         /* optional [B, Hkv, chunk_stride/8, D, 8] prepared v, grouped like cache_vt */
   int32_t chunk_stride; /* >= S, multiple of 64; required when k_out or vt_out is set */
 } G4AppendArgs;
 
@@ -163,7 +166,7 @@ typedef struct G4DecodeArgs {
   int32_t key_mask_stride;     /* >= the largest absolute position + 1 (the full capacity C) */
   const void* q;        /* [B, Hkv, R, D] */
   const void* cache_k;  /* [B, Hkv, slot_stride, D] */
-  void* cache_vt;       /* [B, Hkv, D, slot_stride]; written only with new_v */
+  void* cache_vt;       /* [B, Hkv, slot_stride/8, D, 8]; written only with new_v */
   void* cache_k_w;      /* same as cache_k, writable; required with new_k */
   const void* new_k;    /* optional [B, Hkv, D] */
   const void* new_v;    /* optional [B, Hkv, D] */
@@ -230,7 +233,7 @@ typedef struct G4PrefillArgs {
   int32_t key_mask_stride;
   const void* q;        /* [B, S, Hkv, R, D] */
   const void* k;        /* [B, Hkv, k_stride, D] */
-  const void* vt;       /* [B, Hkv, D, k_stride] */
+  const void* vt;       /* [B, Hkv, k_stride/8, D, 8] (grouped like cache_vt) */
   int32_t k_stride;     /* >= S, multiple of 64 */
   void* out;            /* [B, S, Hkv, R, D] */
 } G4PrefillArgs;

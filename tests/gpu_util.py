@@ -35,8 +35,15 @@ def np_bits(a: np.ndarray, dtype: str) -> np.ndarray:
     return O.bf16_bits(a) if dtype == O.BF16 else np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
+def vt_slots(vt: np.ndarray) -> np.ndarray:
+    """The grouped value layout ``[B, H, G, D, 8]`` (numpy) -> slot-major ``[B, H, 8 G, D]``."""
+
+    B, H, G, D, _ = vt.shape
+    return vt.transpose(0, 1, 2, 4, 3).reshape(B, H, G * 8, D)
+
+
 def cache_to_ref(layer) -> tuple[np.ndarray, np.ndarray]:
-    """Kernel layout (key [B,H,Cp,D], value_t [B,H,D,Cp]) -> the reference's [B,C,H,D] pair."""
+    """Kernel layout (key [B,H,Cp,D], value_t [B,H,Cp/8,D,8]) -> the reference's [B,C,H,D] pair."""
 
     k, v = layer.reference_layout()
     return to_np(k), to_np(v)
@@ -172,7 +179,7 @@ def oracle_cache_rows(cache, rows) -> "O.KVCache":
             layers.append(None)
             continue
         k = layer.key.index_select(0, idx)[:, :, : layer.capacity].permute(0, 2, 1, 3)
-        v = layer.value_t.index_select(0, idx)[:, :, :, : layer.capacity].permute(0, 3, 1, 2)
+        v = layer.value_dmajor().index_select(0, idx)[:, :, :, : layer.capacity].permute(0, 3, 1, 2)
         layers.append(O.LayerKV(to_np(k.contiguous()), to_np(v.contiguous())))
     km = cache.key_mask.index_select(0, idx).cpu().numpy().astype(bool)
     return O.KVCache(tuple(layers), km, int(cache.length))
@@ -183,6 +190,6 @@ def ref_to_cache(layer, k_ref: np.ndarray, v_ref: np.ndarray, dtype: str) -> Non
 
     dev = layer.key.device
     k = to_dev(k_ref, dtype, dev).permute(0, 2, 1, 3)
-    v = to_dev(v_ref, dtype, dev).permute(0, 2, 3, 1)
+    v = to_dev(v_ref, dtype, dev).permute(0, 2, 1, 3)
     layer.key[:, :, : layer.capacity].copy_(k)
-    layer.value_t[:, :, :, : layer.capacity].copy_(v)
+    layer.set_values(v)

@@ -14,7 +14,7 @@ from gpu_util import TOL, bits, cache_to_ref, np_bits, ref_to_cache, to_dev, to_
 from oracle import g4_oracle as O
 
 from gemma4_posttrain_jax_amd import _lib, kernels
-from gemma4_posttrain_jax_amd.kvcache import new_layer_cache
+from gemma4_posttrain_jax_amd.kvcache import group_values, new_layer_cache, ungroup_values
 
 pytestmark = pytest.mark.gpu
 
@@ -96,7 +96,7 @@ def test_append_with_norms_and_q_matches_oracle(device, dtype):
     v = rows_d[:, :, (H * R + H) * D:].view(B, S, H, D)
     q_out = torch.empty((B, S, H, R, D), dtype=q.dtype, device=device)
     k_out = torch.empty((B, H, 64, D), dtype=q.dtype, device=device)
-    vt_out = torch.empty((B, H, D, 64), dtype=q.dtype, device=device)
+    vt_out = torch.empty((B, H, 8, D, 8), dtype=q.dtype, device=device)
     flags = (_lib.G4_APPEND_NORM_Q | _lib.G4_APPEND_ROPE_Q | _lib.G4_APPEND_NORM_K | _lib.G4_APPEND_ROPE_K
              | _lib.G4_APPEND_NORM_V)
     kernels.kv_append(layer, k, v, write_pos=0, flags=flags, eps=1e-6, q=q, q_out=q_out,
@@ -112,7 +112,7 @@ def test_append_with_norms_and_q_matches_oracle(device, dtype):
     tol = TOL[dtype]
     np.testing.assert_allclose(to_np(q_out), q_ref, atol=tol, rtol=0)
     np.testing.assert_allclose(to_np(k_out[:, :, :S]).transpose(0, 2, 1, 3), k_ref, atol=tol, rtol=0)
-    np.testing.assert_allclose(to_np(vt_out[:, :, :, :S]).transpose(0, 3, 1, 2), v_ref, atol=tol, rtol=0)
+    np.testing.assert_allclose(to_np(ungroup_values(vt_out)[:, :, :S]).transpose(0, 2, 1, 3), v_ref, atol=tol, rtol=0)
     ref = O.update_layer_cache(O.LayerKV(np.zeros((B, cap, H, D), np.float32), np.zeros((B, cap, H, D), np.float32)),
                                k_ref, v_ref, 0, True, dtype)
     gk, gv = cache_to_ref(layer)
@@ -334,9 +334,10 @@ def test_prefill_matches_oracle(device, dtype, D, window):
     key_mask[1, :11] = False
     td = __import__("gpu_util").TORCH_DTYPE[dtype]
     kd = torch.zeros((B, H, Sp, D), dtype=td, device=device)
-    vtd = torch.zeros((B, H, D, Sp), dtype=td, device=device)
+    vs = torch.zeros((B, H, Sp, D), dtype=td, device=device)
     kd[:, :, :S] = to_dev(k, dtype, device).permute(0, 2, 1, 3)
-    vtd[:, :, :, :S] = to_dev(v, dtype, device).permute(0, 2, 3, 1)
+    vs[:, :, :S] = to_dev(v, dtype, device).permute(0, 2, 1, 3)
+    vtd = group_values(vs)
     out = kernels.prefill_attention(to_dev(q, dtype, device), kd, vtd, torch.from_numpy(key_mask).to(device),
                                     window=window)
     masks = O.make_qk_masks(key_mask, window if window else 1 << 30, 0, S)
@@ -360,9 +361,10 @@ def test_prefill_group_sizes(device, R):
     key_mask[0, 120:125] = False
     Sp = (S + 63) // 64 * 64
     kd = torch.zeros((B, H, Sp, D), dtype=torch.bfloat16, device=device)
-    vtd = torch.zeros((B, H, D, Sp), dtype=torch.bfloat16, device=device)
+    vs = torch.zeros((B, H, Sp, D), dtype=torch.bfloat16, device=device)
     kd[:, :, :S] = to_dev(k, O.BF16, device).permute(0, 2, 1, 3)
-    vtd[:, :, :, :S] = to_dev(v, O.BF16, device).permute(0, 2, 3, 1)
+    vs[:, :, :S] = to_dev(v, O.BF16, device).permute(0, 2, 1, 3)
+    vtd = group_values(vs)
     out = kernels.prefill_attention(to_dev(q, O.BF16, device), kd, vtd, torch.from_numpy(key_mask).to(device),
                                     window=window)
     masks = O.make_qk_masks(key_mask, window, 0, S)
