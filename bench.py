@@ -242,7 +242,7 @@ def bench_prefill(reps: int = 5) -> dict:
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(4)
     q = torch.randn((Bp, S, HKV, R, D), device=dev, generator=g).to(torch.bfloat16)
-    k = torch.randn((Bp, HKV, S, D), device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn((Bp, HKV, S // 32, D // 32, 2, 16, 32), device=dev, generator=g).to(torch.bfloat16)  # key layout
     vt = torch.randn((Bp, HKV, S // 8, D, 8), device=dev, generator=g).to(torch.bfloat16)  # grouped value layout
     key_mask = torch.ones((Bp, S), dtype=torch.bool, device=dev)
     out = torch.empty_like(q)

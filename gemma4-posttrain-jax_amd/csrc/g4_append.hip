@@ -89,19 +89,21 @@ __global__ __launch_bounds__(1024) void append_kernel(G4AppendArgs a) {
 
     const int64_t bh = (int64_t)b * H + head;
     if (!lane_on) continue;
-    auto store_row = [&](T* dst) {
+    // this lane's PER consecutive elements at p (they never cross a 32-element run of the key layout)
+    auto store_run = [&](T* p) {
       if constexpr (VEC) {
-        st_bf16<PER>(reinterpret_cast<uint16_t*>(dst) + lane * PER, x);
+        st_bf16<PER>(reinterpret_cast<uint16_t*>(p), x);
       } else {
 #pragma unroll
-        for (int e = 0; e < PER; ++e) E::store(dst, lane * PER + e, x[e]);
+        for (int e = 0; e < PER; ++e) E::store(p, e, x[e]);
       }
     };
+    auto store_row = [&](T* dst) { store_run(dst + lane * PER); };
     if (kind == kQ) {
       store_row(reinterpret_cast<T*>(a.q_out) + ((((int64_t)token) * H + head) * R + r) * D);
     } else if (kind == kK) {
-      if (to_cache) store_row(reinterpret_cast<T*>(a.cache_k) + (bh * a.slot_stride + slot) * D);
-      if (a.k_out) store_row(reinterpret_cast<T*>(a.k_out) + (bh * a.chunk_stride + s) * D);
+      if (to_cache) store_run(reinterpret_cast<T*>(a.cache_k) + bh * a.slot_stride * D + kt_index(slot, lane * PER, D));
+      if (a.k_out) store_run(reinterpret_cast<T*>(a.k_out) + bh * a.chunk_stride * D + kt_index(s, lane * PER, D));
     } else {
       if (to_cache) {
         T* dst = reinterpret_cast<T*>(a.cache_vt) + bh * D * a.slot_stride;

@@ -23,6 +23,19 @@ __host__ __device__ __forceinline__ int64_t vt_index(int64_t slot, int d, int D)
   return ((slot >> 3) * D + d) * 8 + (slot & 7);
 }
 
+// Key-cache layout: per (b, kv head) a [slot_stride / 32][D / KR][2][16][KR] block, KR = min(D, 32)
+// dims per run. A 32-slot chunk's keys sit in the order of the decode / prefill MFMA's A operand:
+// block (chunk, s, bb) holds, for each of the 16 lanes col = 4 (r >> 3) + (r & 3), key slot
+// 32 chunk + r, r = 8 (col >> 2) + 4 bb + (col & 3), dims [KR s, KR s + KR). One MFMA operand load
+// (16 lanes x 4 groups of 8 dims, D >= 32) then reads one contiguous KiB (bf16), and one slot's D
+// values are D / KR runs of KR elements.
+__host__ __device__ __forceinline__ int64_t kt_index(int64_t slot, int d, int D) {
+  const int kr = D < 32 ? D : 32;
+  const int r = (int)(slot & 31);
+  const int col = ((r >> 3) << 2) | (r & 3);
+  return ((((slot >> 5) * (D / kr) + d / kr) * 2 + ((r >> 2) & 1)) * 16 + col) * kr + d % kr;
+}
+
 // Byte offset (bf16) of the 16-byte operand of value dim d, slots [8 g, 8 g + 8).
 __host__ __device__ __forceinline__ uint32_t vt_operand_bytes(int g, int d, int D) {
   return ((uint32_t)g * (uint32_t)D + (uint32_t)d) * 16u;

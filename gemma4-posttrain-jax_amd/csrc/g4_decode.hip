@@ -75,10 +75,10 @@ __device__ __forceinline__ void fused_append(const G4DecodeArgs& a, int pair, co
   if (kr.new_slot < 0) return;
   const T* nk = reinterpret_cast<const T*>(a.new_k) + (int64_t)pair * D;
   const T* nv = reinterpret_cast<const T*>(a.new_v) + (int64_t)pair * D;
-  T* ck = reinterpret_cast<T*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
+  T* ck = reinterpret_cast<T*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D;
   T* cv = reinterpret_cast<T*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    ck[d] = nk[d];
+    ck[kt_index(kr.new_slot, d, D)] = nk[d];
     cv[vt_index(kr.new_slot, d, D)] = nv[d];
   }
 }
@@ -113,10 +113,9 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(G4DecodeArgs a, int t_a
 
   for (int key = tid; key < kr.n_keys; key += blockDim.x) {
     const bool valid = key_valid(a, b, kr, key);
-    const float* kp = key == kr.new_slot ? newk : kbase + (int64_t)key * D;
     for (int r = 0; r < R; ++r) {
       float s = 0.f;
-      for (int d = 0; d < D; ++d) s = fmaf(qh[r * D + d], kp[d], s);
+      for (int d = 0; d < D; ++d) s = fmaf(qh[r * D + d], key == kr.new_slot ? newk[d] : kbase[kt_index(key, d, D)], s);
       sc[r * t_alloc + key] = valid ? s : kF32Min;
     }
   }

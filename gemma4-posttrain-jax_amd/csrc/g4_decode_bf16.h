@@ -66,10 +66,10 @@ template <int D>
 __device__ __forceinline__ void store_appended(const G4DecodeArgs& a, int pair, const KeyRange& kr,
                                                const DecodeLds& L) {
   if (kr.new_slot < 0) return;
-  uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
+  uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D;
   uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    ck[d] = L.nk[d];
+    ck[kt_index(kr.new_slot, d, D)] = L.nk[d];
     cv[vt_index(kr.new_slot, d, D)] = L.nv[d];
   }
 }
@@ -86,10 +86,10 @@ __device__ __forceinline__ void load_k_chunk(u32x4 (&kv)[2][D / 32], __amdgpu_bu
                                              int grp) {
 #pragma unroll
   for (int bb = 0; bb < 2; ++bb) {
-    const int kslot = c0 + 8 * (col >> 2) + 4 * bb + (col & 3);
-    const uint32_t voff = (uint32_t)(kslot * D + 8 * grp) * 2u;
+    // block (chunk, s, bb) of the key layout: lane (grp, col) reads 16 bytes at col * 64 + grp * 16
+    const uint32_t voff = (uint32_t)((((c0 >> 5) * (D >> 5)) * 2 + bb) * 1024 + col * 64 + grp * 16);
 #pragma unroll
-    for (int s = 0; s < D / 32; ++s) kv[bb][s] = buffer_load16(rk, voff + 64u * s, 0u);
+    for (int s = 0; s < D / 32; ++s) kv[bb][s] = buffer_load16(rk, voff + 2048u * s, 0u);
   }
 }
 

@@ -355,10 +355,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_fast_kernel(G4D
   // staged row for it, so what it reads does not matter.
   if (has_new) {
     constexpr int DS = D / NSPLIT;
-    uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
+    uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D;
     uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
     for (int d = h * DS + tid; d < (h + 1) * DS; d += blockDim.x) {
-      ck[d] = L.nk[d];
+      ck[kt_index(kr.new_slot, d, D)] = L.nk[d];
       cv[vt_index(kr.new_slot, d, D)] = L.nv[d];
     }
   }

@@ -134,8 +134,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_scores_k
   // the fused append's cache write, after this workgroup's loads; the values launch (next in
   // stream order) reads the V^T column from the cache
   if (has_new) {
-    uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
-    if (owner && lane < D / 8) *reinterpret_cast<u32x4*>(ck + 8 * lane) = nkv;
+    uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D;
+    if (owner && lane < D / 8) *reinterpret_cast<u32x4*>(ck + kt_index(kr.new_slot, 8 * lane, D)) = nkv;
     uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
     const uint16_t* nv = reinterpret_cast<const uint16_t*>(a.new_v) + (int64_t)pair * D;
     for (int d = tid; d < D; d += blockDim.x) cv[vt_index(kr.new_slot, d, D)] = nv[d];

@@ -223,8 +223,9 @@ __device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles* __res
   // it, so what it reads does not matter.
   if (has_new) {
     constexpr int DS = D / NSPLIT;  // K row elements [h*DS, (h+1)*DS): lanes holding 8 of them each
-    uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
-    if (owner && lane >= h * DS / 8 && lane < (h + 1) * DS / 8) *reinterpret_cast<u32x4*>(ck + 8 * lane) = nkv;
+    uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D;
+    if (owner && lane >= h * DS / 8 && lane < (h + 1) * DS / 8)
+      *reinterpret_cast<u32x4*>(ck + kt_index(kr.new_slot, 8 * lane, D)) = nkv;
     if (grp == 0) {
       uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
       cv[vt_index(kr.new_slot, 16 * db + col, D)] = (uint16_t)nvb;

@@ -105,8 +105,8 @@ __global__ __launch_bounds__(kTpWavesS * 64) void decode_bf16_tp_scores_kernel(G
         prep_math<true, D>(pkv, (pp.flags & G4_APPEND_NORM_K) != 0, pp.k_norm_weight != nullptr,
                            (pp.flags & G4_APPEND_ROPE_K) != 0, pp.eps);
         st_bf16<PER>(nk_lds + lane * PER, pkv.x);
-        st_bf16<PER>(reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D +
-                         lane * PER,
+        st_bf16<PER>(reinterpret_cast<uint16_t*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D +
+                         kt_index(kr.new_slot, lane * PER, D),
                      pkv.x);
       } else {
         prep_math<true, D>(pkv, (pp.flags & G4_APPEND_NORM_V) != 0, false, false, pp.eps);
@@ -141,8 +141,8 @@ __global__ __launch_bounds__(kTpWavesS * 64) void decode_bf16_tp_scores_kernel(G
   // been consumed (no other wave of the launch reads that chunk); the V^T column is read only by
   // the values launch
   if (!PREP && writer) {
-    uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + ((int64_t)pair * a.slot_stride + kr.new_slot) * D;
-    if (lane < D / 8) *reinterpret_cast<u32x4*>(ck + 8 * lane) = load16(nk + 8 * lane);
+    uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D;
+    if (lane < D / 8) *reinterpret_cast<u32x4*>(ck + kt_index(kr.new_slot, 8 * lane, D)) = load16(nk + 8 * lane);
     uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
     const uint16_t* nv = reinterpret_cast<const uint16_t*>(a.new_v) + (int64_t)pair * D;
     for (int d = lane; d < D; d += 64) cv[vt_index(kr.new_slot, d, D)] = nv[d];

@@ -63,10 +63,10 @@ __global__ __launch_bounds__(kPrefillWaves * 64) void prefill_bf16_kernel(G4Pref
   auto scores = [&](int c0, floatx4 (&acc)[2]) {
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb) {
-      const uint16_t* kp = kbase + (int64_t)(c0 + 8 * (col >> 2) + 4 * bb + (col & 3)) * D;
+      const uint16_t* kp = kbase + kt_index(c0 + 8 * (col >> 2) + 4 * bb + (col & 3), 8 * grp, D);
       u32x4 kv[KS];
 #pragma unroll
-      for (int s = 0; s < KS; ++s) kv[s] = load16(kp + 32 * s + 8 * grp);
+      for (int s = 0; s < KS; ++s) kv[s] = load16(kp + 1024 * s);  // dims 32 s + 8 grp .. + 7
       floatx4 acc_b = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KS; ++s) acc_b = mfma16x16x32(as_bf16x8(kv[s]), qop[s], acc_b);
@@ -172,8 +172,7 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(G4PrefillArgs a, int t
     float mx = kF32Min;
     for (int key = kmin + lane; key <= pos; key += 64) {
       float s = 0.f;
-      const float* kp = kbase + (int64_t)key * D;
-      for (int d = 0; d < D; ++d) s = fmaf(qrow[d], kp[d], s);
+      for (int d = 0; d < D; ++d) s = fmaf(qrow[d], kbase[kt_index(key, d, D)], s);
       s = km[key] ? s : kF32Min;
       sc[key - kmin] = s;
       mx = fmaxf(mx, s);

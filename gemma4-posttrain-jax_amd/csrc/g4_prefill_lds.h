@@ -103,7 +103,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_bf16_lds_kernel(G4PrefillArgs
       const int t = w * S_::KT_W + i, bb = t / KS, s = t - bb * KS;
       const int key = c0 + 8 * (col >> 2) + 4 * bb + (col & 3);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)&kt[t][0], 16,
-                                               (uint32_t)(key * D + 32 * s + 8 * grp) * 2u, 0, 0, 0);
+                                               (uint32_t)kt_index(key, 32 * s + 8 * grp, D) * 2u, 0, 0, 0);
     }
     if (with_v) {
 #pragma unroll

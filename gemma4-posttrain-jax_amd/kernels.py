@@ -12,7 +12,7 @@ import ctypes
 import torch
 
 from . import _lib
-from .kvcache import LayerKVCache
+from .kvcache import LayerKVCache, key_shape
 
 _DTYPES = {torch.float32: _lib.G4_DTYPE_F32, torch.bfloat16: _lib.G4_DTYPE_BF16}
 
@@ -73,7 +73,7 @@ def kv_append(
     _check_rows(v, "v", B, S, H, D, rs)
     if k.dtype != layer.key.dtype or v.dtype != k.dtype:
         raise TypeError("k/v/cache dtypes differ")
-    if tuple(layer.key.shape[:2]) != (B, H) or layer.key.shape[3] != D:
+    if tuple(layer.key.shape[:2]) != (B, H) or layer.head_dim != D:
         raise ValueError(f"cache {tuple(layer.key.shape)} does not match k {tuple(k.shape)}")
     R = 0
     if q is not None:
@@ -88,8 +88,9 @@ def kv_append(
     if k_out is not None or vt_out is not None:
         if k_out is None or vt_out is None:
             raise ValueError("k_out and vt_out go together")
-        chunk_stride = k_out.shape[2]
-        if tuple(k_out.shape) != (B, H, chunk_stride, D) or tuple(vt_out.shape) != (B, H, chunk_stride // 8, D, 8):
+        chunk_stride = k_out.shape[2] * 32
+        if (tuple(k_out.shape) != key_shape(B, H, chunk_stride, D)
+                or tuple(vt_out.shape) != (B, H, chunk_stride // 8, D, 8)):
             raise ValueError("k_out / vt_out shapes")
         if not (k_out.is_contiguous() and vt_out.is_contiguous()):
             raise ValueError("k_out / vt_out must be contiguous")
@@ -170,7 +171,7 @@ def decode_attention(
     B, H, R, D = q.shape
     if not q.is_contiguous() or q.dtype != layer.key.dtype:
         raise ValueError("q must be contiguous and in the cache dtype")
-    if tuple(layer.key.shape[:2]) != (B, H) or layer.key.shape[3] != D:
+    if tuple(layer.key.shape[:2]) != (B, H) or layer.head_dim != D:
         raise ValueError(f"cache {tuple(layer.key.shape)} does not match q {tuple(q.shape)}")
     if key_mask.dtype != torch.bool or key_mask.dim() != 2 or key_mask.shape[0] != B or key_mask.stride(1) != 1:
         raise ValueError("key_mask must be a [B, C] bool tensor with unit inner stride")
@@ -274,12 +275,14 @@ def prefill_attention(
     window: int,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """g4_prefill_attention: q ``[B, S, Hkv, R, D]``, k ``[B, Hkv, Sp, D]``, vt ``[B, Hkv, Sp / 8, D, 8]``
-    (the value cache's grouped layout; Sp >= S, multiple of 64); returns ``[B, S, Hkv, R, D]``."""
+    """g4_prefill_attention: q ``[B, S, Hkv, R, D]``, k ``key_shape(B, Hkv, Sp, D)`` and vt
+    ``[B, Hkv, Sp / 8, D, 8]`` (the caches' layouts; Sp >= S, multiple of 64); returns
+    ``[B, S, Hkv, R, D]``."""
 
     B, S, H, R, D = q.shape
-    Sp = k.shape[2]
-    if not q.is_contiguous() or tuple(k.shape) != (B, H, Sp, D) or tuple(vt.shape) != (B, H, Sp // 8, D, 8):
+    Sp = k.shape[2] * 32
+    if (not q.is_contiguous() or tuple(k.shape) != key_shape(B, H, Sp, D)
+            or tuple(vt.shape) != (B, H, Sp // 8, D, 8)):
         raise ValueError(f"q {tuple(q.shape)} / k {tuple(k.shape)} / vt {tuple(vt.shape)}")
     if not (k.is_contiguous() and vt.is_contiguous()) or k.dtype != q.dtype or vt.dtype != q.dtype:
         raise ValueError("k/vt must be contiguous and in q's dtype")

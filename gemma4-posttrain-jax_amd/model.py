@@ -35,7 +35,7 @@ from .config import (
     layer_intermediate_size,
     layer_kv_heads,
 )
-from .kvcache import KVCache, LayerKVCache, init_kv_cache, slot_stride_for
+from .kvcache import KVCache, LayerKVCache, init_kv_cache, key_shape, slot_stride_for
 
 # --- parameter pytree (model.py:193-235) -----------------------------------------------------------
 
@@ -402,7 +402,7 @@ def forward_gemma4_text(
                 k_out = vt_out = None
                 if cache_mode == "prefill" and layer_cache.ring:
                     sp = slot_stride_for(S)
-                    k_out = torch.empty((B, H, sp, D), dtype=x.dtype, device=dev)
+                    k_out = torch.empty(key_shape(B, H, sp, D), dtype=x.dtype, device=dev)
                     vt_out = torch.zeros((B, H, sp // 8, D, 8), dtype=x.dtype, device=dev)
                 kernels.kv_append(layer_cache, k, v, write_pos=slot, flags=flags_q | flags_kv, eps=eps, q=q,
                                   q_out=q_out, q_norm_weight=lp.attention.q_norm.weight,

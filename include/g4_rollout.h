@@ -12,8 +12,11 @@
  * (thread-local text).
  *
  * Device data layout (per cache layer, element type = `dtype`):
- *   cache_k   [B, Hkv, slot_stride, D]   key rows, head-major; row b,h,slot at
- *             ((b*Hkv + h)*slot_stride + slot)*D
+ *   cache_k   [B, Hkv, slot_stride/32, D/KR, 2, 16, KR], KR = min(D, 32): each 32-slot chunk in
+ *             the order of the attention MFMA's A operand; key (b,h,slot,d), r = slot%32, at
+ *             (b*Hkv + h)*slot_stride*D + ((((slot/32)*(D/KR) + d/KR)*2 + (r/4)%2)*16
+ *             + 4*(r/8) + r%4)*KR + d%KR, so one 16-lane x 32-dim operand load reads one
+ *             contiguous 1 KiB block (bf16)
  *   cache_vt  [B, Hkv, slot_stride/8, D, 8]   values in groups of 8 slots, each group d-major;
  *             value (b,h,slot,d) at ((b*Hkv + h)*slot_stride + (slot/8)*8)*D + d*8 + slot%8,
  *             so the 8 slots of one value dim are contiguous (one 16-byte MFMA operand in bf16)
@@ -102,10 +105,11 @@ typedef struct G4AppendArgs {
   const void* k_norm_weight;  /* [D] in dtype (G4_APPEND_NORM_K) */
   const float* rope_cos;      /* [B, S, D] f32 (G4_APPEND_ROPE_*) */
   const float* rope_sin;      /* [B, S, D] f32 */
-  void* cache_k;        /* [B, Hkv, slot_stride, D] */
+  void* cache_k;        /* key layout above: [B, Hkv, slot_stride/32, D/KR, 2, 16, KR] */
   void* cache_vt;       /* [B, Hkv, slot_stride/8, D, 8] (grouped values) */
   void* q_out;          /* optional [B, S, Hkv, R, D] prepared q */
-  void* k_out;          /* optional [B, Hkv, chunk_stride, D] prepared k of this chunk (prefill input) */
+  void* k_out;          /* optional prepared k of this chunk (prefill input), key layout with
+                           slot_stride = chunk_stride */
   void* vt_out;         /* optional [B, Hkv, chunk_stride/8, D, 8] prepared v, grouped like cache_vt */
   int32_t chunk_stride; /* >= S, multiple of 64; required when k_out or vt_out is set */
 } G4AppendArgs;
@@ -165,7 +169,7 @@ typedef struct G4DecodeArgs {
   const uint8_t* key_mask;     /* device [B, key_mask_stride] */
   int32_t key_mask_stride;     /* >= the largest absolute position + 1 (the full capacity C) */
   const void* q;        /* [B, Hkv, R, D] */
-  const void* cache_k;  /* [B, Hkv, slot_stride, D] */
+  const void* cache_k;  /* key layout above: [B, Hkv, slot_stride/32, D/KR, 2, 16, KR] */
   void* cache_vt;       /* [B, Hkv, slot_stride/8, D, 8]; written only with new_v */
   void* cache_k_w;      /* same as cache_k, writable; required with new_k */
   const void* new_k;    /* optional [B, Hkv, D] */
@@ -232,7 +236,7 @@ typedef struct G4PrefillArgs {
   const uint8_t* key_mask;   /* [B, key_mask_stride] */
   int32_t key_mask_stride;
   const void* q;        /* [B, S, Hkv, R, D] */
-  const void* k;        /* [B, Hkv, k_stride, D] */
+  const void* k;        /* key layout with slot_stride = k_stride */
   const void* vt;       /* [B, Hkv, k_stride/8, D, 8] (grouped like cache_vt) */
   int32_t k_stride;     /* >= S, multiple of 64 */
   void* out;            /* [B, S, Hkv, R, D] */

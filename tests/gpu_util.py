@@ -35,6 +35,15 @@ def np_bits(a: np.ndarray, dtype: str) -> np.ndarray:
     return O.bf16_bits(a) if dtype == O.BF16 else np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
+def k_slots(kt: np.ndarray) -> np.ndarray:
+    """The operand-ordered key layout ``[B, H, C, D/32, 2, 16, 32]`` (numpy) -> slot-major
+    ``[B, H, 32 C, D]``."""
+
+    B, H, C, NR = kt.shape[:4]
+    kr = kt.shape[6]
+    return kt.reshape(B, H, C, NR, 2, 4, 4, kr).transpose(0, 1, 2, 5, 4, 6, 3, 7).reshape(B, H, C * 32, NR * kr)
+
+
 def vt_slots(vt: np.ndarray) -> np.ndarray:
     """The grouped value layout ``[B, H, G, D, 8]`` (numpy) -> slot-major ``[B, H, 8 G, D]``."""
 
@@ -178,7 +187,7 @@ def oracle_cache_rows(cache, rows) -> "O.KVCache":
         if layer is None:
             layers.append(None)
             continue
-        k = layer.key.index_select(0, idx)[:, :, : layer.capacity].permute(0, 2, 1, 3)
+        k = layer.key_slots().index_select(0, idx)[:, :, : layer.capacity].permute(0, 2, 1, 3)
         v = layer.value_dmajor().index_select(0, idx)[:, :, :, : layer.capacity].permute(0, 3, 1, 2)
         layers.append(O.LayerKV(to_np(k.contiguous()), to_np(v.contiguous())))
     km = cache.key_mask.index_select(0, idx).cpu().numpy().astype(bool)
@@ -191,5 +200,5 @@ def ref_to_cache(layer, k_ref: np.ndarray, v_ref: np.ndarray, dtype: str) -> Non
     dev = layer.key.device
     k = to_dev(k_ref, dtype, dev).permute(0, 2, 1, 3)
     v = to_dev(v_ref, dtype, dev).permute(0, 2, 1, 3)
-    layer.key[:, :, : layer.capacity].copy_(k)
+    layer.set_keys(k)
     layer.set_values(v)

@@ -15,7 +15,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from gpu_util import TOL, attention_rows, to_np, ulp_stats, vt_slots
+from gpu_util import TOL, attention_rows, k_slots, to_np, ulp_stats, vt_slots
 from oracle import g4_oracle as O
 
 from gemma4_posttrain_jax_amd import kernels
@@ -57,7 +57,8 @@ class KernelTrace:
 
     def _layer(self, layer):
         idx = torch.as_tensor(self.rows, device=layer.key.device)
-        return (to_np(layer.key.index_select(0, idx)), to_np(layer.value_dmajor().index_select(0, idx)), layer.capacity,
+        return (to_np(layer.key_slots().index_select(0, idx)), to_np(layer.value_dmajor().index_select(0, idx)),
+                layer.capacity,
                 layer.ring)
 
     def _patch(self, mod, name, make):
@@ -278,7 +279,7 @@ def check_trace(trace: KernelTrace, *, window: int) -> list:
             _bar(tag + " q", q_out, q, PREP_BAR, results)
             if d["k_out"] is not None:
                 S = d["k"].shape[1]
-                _bar(tag + " k", d["k_out"][:, :, :S].transpose(0, 2, 1, 3), k, PREP_BAR, results)
+                _bar(tag + " k", k_slots(d["k_out"])[:, :, :S].transpose(0, 2, 1, 3), k, PREP_BAR, results)
                 _bar(tag + " v", vt_slots(d["vt_out"])[:, :, :S].transpose(0, 2, 1, 3), v, NORM_BAR, results)
             if k is not None:
                 ck, cvt, cap, ring = d["layer"]
@@ -291,7 +292,7 @@ def check_trace(trace: KernelTrace, *, window: int) -> list:
         elif kind == "prefill_attention":
             q = d["q"]  # [r, S, H, R, D]
             S = q.shape[1]
-            k = d["k"][:, :, :S].transpose(0, 2, 1, 3)
+            k = k_slots(d["k"])[:, :, :S].transpose(0, 2, 1, 3)
             v = vt_slots(d["vt"])[:, :, :S].transpose(0, 2, 1, 3)
             mask = O.make_qk_masks(d["km"][:, :S], d["window"] if d["window"] else 1 << 30, 0, S)[O.SLIDING]
             qr = q.transpose(0, 1, 3, 2, 4)

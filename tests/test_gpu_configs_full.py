@@ -21,7 +21,7 @@ from gpu_util import TOL, attention_rows, cache_to_ref, np_bits, to_np
 from oracle import g4_oracle as O
 
 from gemma4_posttrain_jax_amd import kernels
-from gemma4_posttrain_jax_amd.kvcache import group_values, new_layer_cache, ungroup_values
+from gemma4_posttrain_jax_amd.kvcache import group_keys, group_values, new_layer_cache, ungroup_keys, ungroup_values
 
 pytestmark = pytest.mark.gpu
 
@@ -97,7 +97,7 @@ def test_config4_prompt_append_is_bit_exact(config4, device):
     B, S, H, D = c["B"], c["S"], c["H"], c["D"]
     ring = new_layer_cache(B, H, D, 512, True, torch.bfloat16, device)
     lin = new_layer_cache(B, H, D, S, False, torch.bfloat16, device)
-    k_out = torch.empty((B, H, S, D), dtype=torch.bfloat16, device=device)
+    k_out = torch.empty((B, H, S // 32, D // 32, 2, 16, 32), dtype=torch.bfloat16, device=device)
     vt_out = torch.empty((B, H, S // 8, D, 8), dtype=torch.bfloat16, device=device)
     kernels.kv_append(ring, c["k"], c["v"], write_pos=0, k_out=k_out, vt_out=vt_out)
     kernels.kv_append(lin, c["k"], c["v"], write_pos=0)
@@ -113,7 +113,7 @@ def test_config4_prompt_append_is_bit_exact(config4, device):
     gk, gv = cache_to_ref(lin)
     np.testing.assert_array_equal(np_bits(gk, O.BF16), np_bits(want_lin.key, O.BF16))
     np.testing.assert_array_equal(np_bits(gv, O.BF16), np_bits(want_lin.value, O.BF16))
-    np.testing.assert_array_equal(np_bits(to_np(k_out).transpose(0, 2, 1, 3), O.BF16), np_bits(k, O.BF16))
+    np.testing.assert_array_equal(np_bits(to_np(ungroup_keys(k_out)).transpose(0, 2, 1, 3), O.BF16), np_bits(k, O.BF16))
     np.testing.assert_array_equal(np_bits(to_np(ungroup_values(vt_out)).transpose(0, 2, 1, 3), O.BF16),
                                   np_bits(v, O.BF16))
 
@@ -129,7 +129,7 @@ def test_config4_prefill_attention_full_size(config4, device, window):
 
     c = config4
     B, S, H, R, D = c["B"], c["S"], c["H"], c["R"], c["D"]
-    kd = c["k"].permute(0, 2, 1, 3).contiguous()  # [B, H, S, D] (S is a multiple of 64)
+    kd = group_keys(c["k"].permute(0, 2, 1, 3))  # operand-ordered keys (S is a multiple of 64)
     vtd = group_values(c["v"].permute(0, 2, 1, 3))  # [B, H, S / 8, D, 8]
     km = torch.from_numpy(c["key_mask"]).to(device)
     out = kernels.prefill_attention(c["q"], kd, vtd, km, window=window)

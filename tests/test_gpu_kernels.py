@@ -14,7 +14,7 @@ from gpu_util import TOL, bits, cache_to_ref, np_bits, ref_to_cache, to_dev, to_
 from oracle import g4_oracle as O
 
 from gemma4_posttrain_jax_amd import _lib, kernels
-from gemma4_posttrain_jax_amd.kvcache import group_values, new_layer_cache, ungroup_values
+from gemma4_posttrain_jax_amd.kvcache import group_keys, group_values, new_layer_cache, ungroup_keys, ungroup_values
 
 pytestmark = pytest.mark.gpu
 
@@ -95,7 +95,7 @@ def test_append_with_norms_and_q_matches_oracle(device, dtype):
     k = rows_d[:, :, H * R * D: (H * R + H) * D].view(B, S, H, D)
     v = rows_d[:, :, (H * R + H) * D:].view(B, S, H, D)
     q_out = torch.empty((B, S, H, R, D), dtype=q.dtype, device=device)
-    k_out = torch.empty((B, H, 64, D), dtype=q.dtype, device=device)
+    k_out = torch.empty((B, H, 2, D // 32, 2, 16, 32), dtype=q.dtype, device=device)
     vt_out = torch.empty((B, H, 8, D, 8), dtype=q.dtype, device=device)
     flags = (_lib.G4_APPEND_NORM_Q | _lib.G4_APPEND_ROPE_Q | _lib.G4_APPEND_NORM_K | _lib.G4_APPEND_ROPE_K
              | _lib.G4_APPEND_NORM_V)
@@ -111,7 +111,7 @@ def test_append_with_norms_and_q_matches_oracle(device, dtype):
     v_ref = O.rms_norm(None, vr, 1e-6, dtype)
     tol = TOL[dtype]
     np.testing.assert_allclose(to_np(q_out), q_ref, atol=tol, rtol=0)
-    np.testing.assert_allclose(to_np(k_out[:, :, :S]).transpose(0, 2, 1, 3), k_ref, atol=tol, rtol=0)
+    np.testing.assert_allclose(to_np(ungroup_keys(k_out)[:, :, :S]).transpose(0, 2, 1, 3), k_ref, atol=tol, rtol=0)
     np.testing.assert_allclose(to_np(ungroup_values(vt_out)[:, :, :S]).transpose(0, 2, 1, 3), v_ref, atol=tol, rtol=0)
     ref = O.update_layer_cache(O.LayerKV(np.zeros((B, cap, H, D), np.float32), np.zeros((B, cap, H, D), np.float32)),
                                k_ref, v_ref, 0, True, dtype)
@@ -338,7 +338,7 @@ def test_prefill_matches_oracle(device, dtype, D, window):
     kd[:, :, :S] = to_dev(k, dtype, device).permute(0, 2, 1, 3)
     vs[:, :, :S] = to_dev(v, dtype, device).permute(0, 2, 1, 3)
     vtd = group_values(vs)
-    out = kernels.prefill_attention(to_dev(q, dtype, device), kd, vtd, torch.from_numpy(key_mask).to(device),
+    out = kernels.prefill_attention(to_dev(q, dtype, device), group_keys(kd), vtd, torch.from_numpy(key_mask).to(device),
                                     window=window)
     masks = O.make_qk_masks(key_mask, window if window else 1 << 30, 0, S)
     q_ref = q.transpose(0, 1, 3, 2, 4)  # [B, S, R, H, D]
@@ -365,7 +365,7 @@ def test_prefill_group_sizes(device, R):
     kd[:, :, :S] = to_dev(k, O.BF16, device).permute(0, 2, 1, 3)
     vs[:, :, :S] = to_dev(v, O.BF16, device).permute(0, 2, 1, 3)
     vtd = group_values(vs)
-    out = kernels.prefill_attention(to_dev(q, O.BF16, device), kd, vtd, torch.from_numpy(key_mask).to(device),
+    out = kernels.prefill_attention(to_dev(q, O.BF16, device), group_keys(kd), vtd, torch.from_numpy(key_mask).to(device),
                                     window=window)
     masks = O.make_qk_masks(key_mask, window, 0, S)
     o_ref = O.attention_core(q.transpose(0, 1, 3, 2, 4), k, v, masks[O.SLIDING], O.BF16).transpose(0, 1, 3, 2, 4)
