@@ -104,10 +104,7 @@ __global__ __launch_bounds__(kTpWavesS * 64) void decode_bf16_tp_scores_kernel(G
       if (w == 0) {
         prep_math<true, D>(pkv, (pp.flags & G4_APPEND_NORM_K) != 0, pp.k_norm_weight != nullptr,
                            (pp.flags & G4_APPEND_ROPE_K) != 0, pp.eps);
-        st_bf16<PER>(nk_lds + lane * PER, pkv.x);
-        st_bf16<PER>(reinterpret_cast<uint16_t*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D +
-                         kt_index(kr.new_slot, lane * PER, D),
-                     pkv.x);
+        st_bf16<PER>(nk_lds + lane * PER, pkv.x);  // the writer wave stores it to the cache after its scores
       } else {
         prep_math<true, D>(pkv, (pp.flags & G4_APPEND_NORM_V) != 0, false, false, pp.eps);
         uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
@@ -137,9 +134,17 @@ __global__ __launch_bounds__(kTpWavesS * 64) void decode_bf16_tp_scores_kernel(G
     score_to_lds<D>(kv, qop, vbits, ws + (int64_t)pair * R * row_slots, row_slots, chunk << 5, R, col, grp,
                     kBf16Min);
   }
-  // the fused append's cache write (prepared rows given): the K row after this wave's K loads have
-  // been consumed (no other wave of the launch reads that chunk); the V^T column is read only by
-  // the values launch
+  // the fused append's K row store: by the writer wave, after its K loads of the chunk have been
+  // consumed (no other wave of the launch reads that chunk), so no load of this launch can see a
+  // partly written row. With PREP the row comes from LDS (prepared by wave 0 before the barrier);
+  // its V^T column was stored by wave 1 above (read only by the values launch).
+  if constexpr (PREP) {
+    if (writer && pp.k_raw) {
+      uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D;
+      if (lane < D / 8)
+        *reinterpret_cast<u32x4*>(ck + kt_index(kr.new_slot, 8 * lane, D)) = *reinterpret_cast<const u32x4*>(nk_lds + 8 * lane);
+    }
+  }
   if (!PREP && writer) {
     uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D;
     if (lane < D / 8) *reinterpret_cast<u32x4*>(ck + kt_index(kr.new_slot, 8 * lane, D)) = load16(nk + 8 * lane);
