@@ -81,6 +81,15 @@ class G4SampleArgs(ctypes.Structure):
     ]
 
 
+class G4LmHeadSampleArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_int32), ("vocab", c_int32), ("hidden", c_int32), ("x", c_void_p), ("embed", c_void_p),
+        ("softcap", c_float), ("temperature", c_float), ("split_key", c_int32), ("key", c_void_p),
+        ("token_out", c_void_p), ("logp_out", c_void_p), ("logits_out", c_void_p), ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t),
+    ]
+
+
 class G4LinearArgs(ctypes.Structure):
     _fields_ = [
         ("x", c_void_p), ("w", c_void_p), ("y", c_void_p), ("m", c_int32), ("n", c_int32), ("k", c_int32),
@@ -108,6 +117,8 @@ PROTOTYPES = {
     "g4_kv_source_layers": (c_int32, [c_int32, c_int32, POINTER(c_int32), POINTER(c_int32)]),
     "g4_ring_slot_positions": (c_int32, [c_int32, c_int32, POINTER(c_int32)]),
     "g4_sample_tokens": (c_int32, [POINTER(G4SampleArgs), c_void_p]),
+    "g4_lm_head_sample_workspace_size": (c_size_t, [POINTER(G4LmHeadSampleArgs)]),
+    "g4_lm_head_sample": (c_int32, [POINTER(G4LmHeadSampleArgs), c_void_p]),
     "g4_rms_norm": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_float, c_void_p, c_void_p]),
     "g4_residual_norm": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_float, c_void_p, c_void_p, c_void_p]),

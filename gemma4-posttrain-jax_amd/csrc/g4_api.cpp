@@ -42,6 +42,7 @@ int device_setup(int* device) {
   std::call_once(g_setup_once[dev], [dev] {
     int rc = setup_decode_kernels(dev);
     if (rc == G4_OK) rc = setup_prefill_kernels(dev);
+    if (rc == G4_OK) rc = setup_lm_head(dev);
     if (rc != G4_OK) snprintf(g_setup_error[dev], sizeof(g_setup_error[dev]), "%s", g_error);
     g_setup_status[dev] = rc;
   });

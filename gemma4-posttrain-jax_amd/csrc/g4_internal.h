@@ -25,6 +25,7 @@ int device_setup(int* device);
 // Per-source set-up steps run by device_setup for `device` (the current device).
 int setup_decode_kernels(int device);
 int setup_prefill_kernels(int device);
+int setup_lm_head(int device);
 
 // Head dims with an instantiated kernel: powers of two 8..512 (bf16 attention: 32..256).
 inline bool supported_head_dim(int d) { return d >= 8 && d <= 512 && (d & (d - 1)) == 0; }

@@ -401,6 +401,76 @@ def sample_tokens(logits: torch.Tensor, *, softcap: float | None, temperature: f
     return token_out, logp_out
 
 
+LM_HEAD_MAX_ROWS = 256
+
+
+def lm_head_supported(x: torch.Tensor, embed: torch.Tensor) -> bool:
+    """Whether g4_lm_head_sample takes ``x [B, M] . embed [V, M]^T``: bf16, B <= 256, V % 128 == 0,
+    M % 32 == 0 (contiguous operands)."""
+
+    return (x.dtype == torch.bfloat16 and embed.dtype == torch.bfloat16 and x.dim() == 2 and embed.dim() == 2
+            and 0 < x.shape[0] <= LM_HEAD_MAX_ROWS and x.shape[1] == embed.shape[1] and embed.shape[0] % 128 == 0
+            and x.shape[1] % 32 == 0 and embed.shape[0] * embed.shape[1] * 2 < 2 ** 32)
+
+
+def _lm_head_call(x: torch.Tensor, embed: torch.Tensor, *, softcap: float | None, temperature: float,
+                  key: torch.Tensor | None, split_key: bool, token_out: torch.Tensor | None,
+                  logp_out: torch.Tensor | None, logits_out: torch.Tensor | None) -> torch.Tensor | None:
+    if not lm_head_supported(x, embed):
+        raise ValueError(f"g4_lm_head_sample does not take x {tuple(x.shape)} {x.dtype} / embed "
+                         f"{tuple(embed.shape)} {embed.dtype} (bf16, rows <= 256, vocab % 128, hidden % 32)")
+    x, embed = x.contiguous(), embed.contiguous()
+    B, M = x.shape
+    V = embed.shape[0]
+    dev = x.device
+    if key is not None and (key.dtype != torch.int32 or key.numel() != 2 or not key.is_contiguous()
+                            or key.device != dev):
+        raise ValueError("key must be a contiguous 2-element int32 tensor on x's device")
+    if logits_out is not None and (logits_out.dtype != torch.bfloat16 or tuple(logits_out.shape) != (B, V)
+                                   or not logits_out.is_contiguous()):
+        raise ValueError(f"logits_out must be a contiguous bf16 [{B}, {V}] tensor")
+    a = _lib.G4LmHeadSampleArgs(
+        batch=B, vocab=V, hidden=M, x=_ptr(x), embed=_ptr(embed), softcap=float(softcap or 0.0),
+        temperature=float(temperature), split_key=int(bool(split_key)), key=_ptr(key),
+        token_out=_ptr(token_out), logp_out=_ptr(logp_out), logits_out=_ptr(logits_out), workspace=None,
+        workspace_bytes=0)
+    need = _lib.lib().g4_lm_head_sample_workspace_size(ctypes.byref(a))
+    ws = None
+    if need:
+        ws = torch.empty(need // 4, dtype=torch.float32, device=dev)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), need
+    _lib.check(_lib.lib().g4_lm_head_sample(ctypes.byref(a), _stream()), "g4_lm_head_sample")
+    return ws
+
+
+def lm_head(x: torch.Tensor, embed: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """g4_lm_head_sample without sampling: ``bf16(x [B, M] . embed [V, M]^T)`` with f32 accumulation
+    (the logits before the soft-cap)."""
+
+    if out is None:
+        out = torch.empty((x.shape[0], embed.shape[0]), dtype=torch.bfloat16, device=x.device)
+    _lm_head_call(x, embed, softcap=None, temperature=0.0, key=None, split_key=False, token_out=None,
+                  logp_out=None, logits_out=out)
+    return out
+
+
+def lm_head_sample(x: torch.Tensor, embed: torch.Tensor, *, softcap: float | None, temperature: float,
+                   key: torch.Tensor | None, split_key: bool = True, token_out: torch.Tensor | None = None,
+                   logp_out: torch.Tensor | None = None,
+                   logits_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """g4_lm_head_sample: the LM head ``x [B, M] . embed [V, M]^T`` with sample_tokens' draw (no
+    proposal) on its bf16 logits in the epilogue, the logits never stored unless ``logits_out`` is
+    given. Same key / temperature / soft-cap semantics as sample_tokens; returns ``(token int32 [B],
+    logp f32 [B])``."""
+
+    B = x.shape[0]
+    token_out = torch.empty(B, dtype=torch.int32, device=x.device) if token_out is None else token_out
+    logp_out = torch.empty(B, dtype=torch.float32, device=x.device) if logp_out is None else logp_out
+    _lm_head_call(x, embed, softcap=softcap, temperature=temperature, key=key, split_key=split_key,
+                  token_out=token_out, logp_out=logp_out, logits_out=logits_out)
+    return token_out, logp_out
+
+
 def decode_prologue(embed: torch.Tensor, tokens: torch.Tensor, positions: torch.Tensor, active: torch.Tensor,
                     slot: torch.Tensor, key_mask: torch.Tensor, *, embed_scale: float,
                     inv_freq: list[torch.Tensor]) -> tuple[torch.Tensor, list[tuple[torch.Tensor, torch.Tensor]]]:

@@ -471,7 +471,13 @@ def forward_lm_head(embed_tokens: torch.Tensor, hidden: torch.Tensor, softcap: f
     """model.py:676-680: tied-embedding logits, ``tanh(x / cap) * cap``."""
 
     B, S, M = hidden.shape
-    logits = _proj(hidden.reshape(B * S, M), embed_tokens).reshape(B, S, -1)
+    x = hidden.reshape(B * S, M)
+    if x.is_cuda and kernels.lm_head_supported(x, embed_tokens):
+        # the decode batch (<= 256 rows): the native LM head, the GEMM g4_lm_head_sample runs when it
+        # samples in its epilogue, so a step's logits and its fused draw see the same bf16 values
+        logits = kernels.lm_head(x.contiguous(), embed_tokens).reshape(B, S, -1)
+    else:
+        logits = _proj(x, embed_tokens).reshape(B, S, -1)
     if softcap is not None:
         logits = (torch.tanh(logits.float() / softcap) * softcap).to(logits.dtype)
     return logits

@@ -124,9 +124,11 @@ class GraphedDecodeStep:
     whole step (every layer's GEMMs, norms, cache append and decode attention, the LM head) with
     one call and no host work per layer. The cache is updated in place.
 
-    With ``temperature`` given, the graph ends in the fused sampler (``g4_sample_tokens``: the LM
-    head's soft-capping, the full-vocab log-softmax, the split of ``key`` (a 2-word int32 device
-    tensor, advanced in place by every replay) and a greedy / categorical draw) and
+    With ``temperature`` given, the graph ends in the LM head with the sampler in its epilogue
+    (``g4_lm_head_sample``; ``g4_sample_tokens`` after a separate LM head where the shapes are
+    outside its limits): the LM head's soft-capping, the full-vocab log-softmax, the split of
+    ``key`` (a 2-word int32 device tensor, advanced in place by every replay) and a greedy /
+    categorical draw, and
     ``step_sample`` returns the next token and its log-probability; otherwise ``step`` returns the
     logits.
 
@@ -172,9 +174,16 @@ class GraphedDecodeStep:
         hidden, _ = forward_gemma4_text(self.params, self.tok[:, None], self.pos[:, None], config=self.config,
                                         attention_mask=self.active[:, None], kv_cache=self.cache,
                                         cache_mode="append", write_pos=self.slot)
-        raw = _proj(hidden[:, -1], self.params.embed_tokens)  # [B, V] before the soft-cap
-        kernels.sample_tokens(raw, softcap=self.config.final_logit_softcapping, temperature=self.temperature,
-                              key=self.key, split_key=True, token_out=self.token_out, logp_out=self.logp_out)
+        head_in = hidden[:, -1]
+        cap = self.config.final_logit_softcapping
+        if kernels.lm_head_supported(head_in, self.params.embed_tokens):
+            # the LM head with the draw in its epilogue: the [B, V] logits never reach HBM
+            kernels.lm_head_sample(head_in, self.params.embed_tokens, softcap=cap, temperature=self.temperature,
+                                   key=self.key, split_key=True, token_out=self.token_out, logp_out=self.logp_out)
+            return None
+        raw = _proj(head_in, self.params.embed_tokens)  # [B, V] before the soft-cap
+        kernels.sample_tokens(raw, softcap=cap, temperature=self.temperature, key=self.key, split_key=True,
+                              token_out=self.token_out, logp_out=self.logp_out)
         return None
 
     def _replay(self, token_ids: torch.Tensor, position_ids: torch.Tensor, active: torch.Tensor) -> None:

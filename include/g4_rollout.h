@@ -293,6 +293,38 @@ typedef struct G4SampleArgs {
 int g4_sample_tokens(const G4SampleArgs* args, void* stream);
 
 /*
+ * The decode step's LM head with the sampler in its epilogue: l = cast_bf16(x . embed^T) (bf16
+ * operands, f32 accumulation; forward_lm_head with the tied embedding, model.py:676-680), then,
+ * with token_out given, g4_sample_tokens' draw on l (no proposal) without l leaving the chip:
+ * soft-cap, full-vocab log-softmax, the key split (split_key as there) and the greedy /
+ * categorical draw of _sample_token (sampler.py:145-183, 265-270). With token_out NULL it is the
+ * plain LM head and writes l (before the soft-cap) to logits_out; with both it writes l and draws.
+ * Limits: batch 1..256, vocab a multiple of 128, hidden a multiple of 32, vocab * hidden * 2 < 4 GiB;
+ * x [batch, hidden] and embed [vocab, hidden] row-major bf16, 16-byte aligned. Sampling needs
+ * g4_lm_head_sample_workspace_size() bytes of device workspace (4-byte aligned; one launch at a
+ * time per buffer). Two launches on `stream` (the GEMM + epilogue, then the per-row merge).
+ */
+typedef struct G4LmHeadSampleArgs {
+  int32_t batch;
+  int32_t vocab;
+  int32_t hidden;
+  const void* x;          /* [batch, hidden] bf16 */
+  const void* embed;      /* [vocab, hidden] bf16 */
+  float softcap;          /* 0 = none */
+  float temperature;      /* <= 0 = greedy */
+  int32_t split_key;      /* as G4SampleArgs.split_key */
+  uint32_t* key;          /* device [2]; may be NULL only when greedy */
+  int32_t* token_out;     /* device [batch], or NULL: logits only */
+  float* logp_out;        /* device [batch] (with token_out) */
+  void* logits_out;       /* device [batch, vocab] bf16 before the soft-cap, or NULL (8-byte aligned) */
+  void* workspace;        /* device, g4_lm_head_sample_workspace_size() bytes when sampling */
+  size_t workspace_bytes;
+} G4LmHeadSampleArgs;
+
+size_t g4_lm_head_sample_workspace_size(const G4LmHeadSampleArgs* args);
+int g4_lm_head_sample(const G4LmHeadSampleArgs* args, void* stream);
+
+/*
  * Fused elementwise glue of the decoder layer (row-major [rows, cols] arrays, cols <= 4096 for
  * the norms; one pass each, the reference's rounding points kept). dtype = G4_DTYPE_*.
  *

@@ -76,6 +76,13 @@ class KernelTrace:
                 return y
             return f
 
+        def lm_head(orig):
+            def f(x, embed, *, out=None):
+                y = orig(x, embed, out=out)
+                rec(("proj", dict(x=sel(x), y=sel(y), w=embed)))
+                return y
+            return f
+
         def rms(orig):
             def f(x, weight, eps, out=None):
                 y = orig(x, weight, eps, out)
@@ -177,7 +184,7 @@ class KernelTrace:
                            ("linear_gelu", linear_gelu), ("linear_partials", partials),
                            ("residual_norm_splitk", resnorm_splitk), ("kv_append", append), ("prepare_q", prep_q),
                            ("prefill_attention", prefill_attn), ("decode_attention_fused", fused),
-                           ("decode_prologue", prologue)):
+                           ("decode_prologue", prologue), ("lm_head", lm_head)):
             self._patch(kernels, name, make)
         return self
 

@@ -44,7 +44,8 @@ def test_ctypes_structs_match_the_compiled_header(tmp_path):
     if cc is None:
         pytest.skip("no C compiler")
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
-    for st in (_lib.G4AppendArgs, _lib.G4DecodeArgs, _lib.G4PrefillArgs, _lib.G4SampleArgs):
+    for st in (_lib.G4AppendArgs, _lib.G4DecodeArgs, _lib.G4PrefillArgs, _lib.G4SampleArgs,
+               _lib.G4LmHeadSampleArgs, _lib.G4LinearArgs, _lib.G4PrologueArgs):
         lines.append(f'printf("{st.__name__} size %zu\\n", sizeof({st.__name__}));')
         for f, _ in st._fields_:
             lines.append(f'printf("{st.__name__} {f} %zu\\n", offsetof({st.__name__}, {f}));')
@@ -314,6 +315,35 @@ def test_sample_rejects_invalid_arguments(override, match):
     a = _sample_args(**override)
     rc = _lib.lib().g4_sample_tokens(ctypes.byref(a), None)
     assert rc == _lib.G4_ERR_INVALID
+    assert re.search(match, _lib.lib().g4_last_error().decode())
+
+
+def _lm_head_args(**kw):
+    base = dict(batch=256, vocab=262144, hidden=1536, x=16, embed=16, softcap=30.0, temperature=1.0, split_key=1,
+                key=16, token_out=16, logp_out=16, logits_out=None, workspace=None, workspace_bytes=0)
+    base.update(kw)
+    return _lib.G4LmHeadSampleArgs(**base)
+
+
+@pytest.mark.parametrize("override,match", [
+    (dict(batch=0), "batch 0"),
+    (dict(batch=257), "batch 257"),
+    (dict(vocab=1000), "vocab 1000"),
+    (dict(hidden=1540), "hidden 1540"),
+    (dict(vocab=262144 * 8, hidden=1536), "4 GiB"),
+    (dict(x=None), "NULL"),
+    (dict(embed=8), "alignment"),
+    (dict(logits_out=4), "alignment"),
+    (dict(token_out=None), "neither"),
+    (dict(logp_out=None), "logp_out"),
+    (dict(softcap=-1.0), "softcap"),
+    (dict(key=None), "key"),
+    (dict(split_key=2), "split_key"),
+])
+def test_lm_head_sample_rejects_invalid_arguments(override, match):
+    a = _lm_head_args(**override)
+    rc = _lib.lib().g4_lm_head_sample(ctypes.byref(a), None)
+    assert rc in (_lib.G4_ERR_INVALID, _lib.G4_ERR_UNSUPPORTED)
     assert re.search(match, _lib.lib().g4_last_error().decode())
 
 
