@@ -117,6 +117,7 @@ PROTOTYPES = {
     "g4_kv_source_layers": (c_int32, [c_int32, c_int32, POINTER(c_int32), POINTER(c_int32)]),
     "g4_ring_slot_positions": (c_int32, [c_int32, c_int32, POINTER(c_int32)]),
     "g4_sample_tokens": (c_int32, [POINTER(G4SampleArgs), c_void_p]),
+    "g4_softcap_bf16": (c_int32, [c_int64, c_void_p, c_float, c_void_p, c_void_p]),
     "g4_lm_head_sample_workspace_size": (c_size_t, [POINTER(G4LmHeadSampleArgs)]),
     "g4_lm_head_sample": (c_int32, [POINTER(G4LmHeadSampleArgs), c_void_p]),
     "g4_rms_norm": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_float, c_void_p, c_void_p]),

@@ -137,26 +137,32 @@ __device__ __forceinline__ void lh_compute(uint32_t slot, floatx4 (&acc)[4][8], 
 // optional logits store, the soft-cap, the running max / sum and the running argmax of the scores.
 template <bool SAMPLE, bool GREEDY>
 __device__ __forceinline__ void lh_epilogue(floatx4 v, LhState& sr, int row, int n, const G4LmHeadSampleArgs& a,
-                                            uint32_t k0, uint32_t k1) {
+                                            const CapTable& ct, uint32_t k0, uint32_t k1) {
+  uint32_t bits[4];
   float x[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) x[j] = round_bf16(v[j]);
+  for (int j = 0; j < 4; ++j) {
+    bits[j] = f32_to_bf16_bits(v[j]);
+    x[j] = bf16_bits_to_f32(bits[j]);
+  }
   if (a.logits_out) {
     uint16_t* dst = reinterpret_cast<uint16_t*>(a.logits_out) + (int64_t)row * a.vocab + n;
-    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]));
+    *reinterpret_cast<uint2*>(dst) = make_uint2(bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16));
   }
   if constexpr (SAMPLE) {
     if (a.softcap > 0.f) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = round_bf16(tanhf(x[j] / a.softcap) * a.softcap);  // the reference divides
+      for (int j = 0; j < 4; ++j) x[j] = capped(bits[j], ct);
     }
     const float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    const float mn = fmaxf(sr.m, mx);
+    if (mx > sr.m) {  // a new running max: rescale the sum (else the factor would be exactly 1)
+      sr.s *= expf(sr.m - mx);
+      sr.m = mx;
+    }
     float sum = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) sum += expf(x[j] - mn);
-    sr.s = sr.s * expf(sr.m - mn) + sum;
-    sr.m = mn;
+    for (int j = 0; j < 4; ++j) sum += expf(x[j] - sr.m);
+    sr.s += sum;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float score = x[j];
@@ -177,6 +183,7 @@ __device__ __forceinline__ void lh_epilogue(floatx4 v, LhState& sr, int row, int
 template <bool SAMPLE, bool GREEDY>
 __global__ __launch_bounds__(kLhThreads, kLhWgPerCu) void lm_head_kernel(G4LmHeadSampleArgs a) {
   __shared__ __attribute__((aligned(1024))) unsigned char ring[kLhSlots][kLhSlotBytes];
+  __shared__ uint16_t cap_tab[SAMPLE ? kCapTableEntries : 1];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, grp = lane >> 4;
@@ -201,6 +208,11 @@ __global__ __launch_bounds__(kLhThreads, kLhWgPerCu) void lm_head_kernel(G4LmHea
   LhState st[4];
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb) st[rb] = LhState{kF32Min, 0.f, -INFINITY, 0.f, 0x7fffffff};
+  const CapTable ct = cap_table(cap_tab, a.softcap);
+  if (SAMPLE && a.softcap > 0.f) {  // the soft-cap table, complete before any DMA is issued
+    cap_table_fill(cap_tab, a.softcap, threadIdx.x, kLhThreads);
+    __syncthreads();
+  }
 
   // the ring's stage sequence runs over every (tile, k stage) of this workgroup; stage q of the
   // sequence sits in slot q % 3. Stages past the last tile re-read stage 0 of the last tile (an L2
@@ -245,7 +257,7 @@ __global__ __launch_bounds__(kLhThreads, kLhWgPerCu) void lm_head_kernel(G4LmHea
 #pragma unroll
           for (int i = 0; i < 7; ++i) acc[rb][i] = acc[rb][i + 1];
           acc[rb][7] = v;
-          lh_epilogue<SAMPLE, GREEDY>(v, st[rb], row, n0 + 16 * cb + 4 * grp, a, k0, k1);
+          lh_epilogue<SAMPLE, GREEDY>(v, st[rb], row, n0 + 16 * cb + 4 * grp, a, ct, k0, k1);
         }
       }
     }

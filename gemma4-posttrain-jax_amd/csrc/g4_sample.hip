@@ -16,19 +16,26 @@ namespace {
 constexpr int kSampleThreads = 1024;
 #include "g4_sample_common.h"  // threefry2x32, Gumbel noise, the per-row running state
 
+// The soft-capped logit of column col (cap 0: the logit itself); bf16 logits go through the table.
 template <bool BF16>
-__device__ __forceinline__ float capped(const typename Elem<BF16>::T* row, int col, float cap) {
+__device__ __forceinline__ float capped_at(const typename Elem<BF16>::T* row, int col, const CapTable& t) {
   using E = Elem<BF16>;
-  float x = E::load(row, col);
-  if (cap > 0.f) x = E::round(tanhf(x / cap) * cap);  // the reference divides by the cap
-  return x;
+  if (!(t.cap > 0.f)) return E::load(row, col);
+  if constexpr (BF16) return capped(reinterpret_cast<const uint16_t*>(row)[col], t);
+  else return E::round(tanhf(E::load(row, col) / t.cap) * t.cap);  // the reference divides by the cap
 }
 
 template <bool BF16, bool VEC>
 __global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) {
   using T = typename Elem<BF16>::T;
   __shared__ RowState red[kSampleThreads / 64];
+  __shared__ uint16_t cap_tab[BF16 ? kCapTableEntries : 1];
   const int row = blockIdx.x;
+  const CapTable ct = cap_table(cap_tab, a.softcap);
+  if (BF16 && a.softcap > 0.f) {
+    cap_table_fill(cap_tab, a.softcap, threadIdx.x, kSampleThreads);
+    __syncthreads();
+  }
   const T* lrow = reinterpret_cast<const T*>(a.logits) + (int64_t)row * a.row_stride;
   const bool greedy = !(a.temperature > 0.f);
   const bool proposal = !greedy && a.proposal != nullptr;
@@ -52,12 +59,14 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) 
     float mx = -INFINITY;
 #pragma unroll
     for (int u = 0; u < N; ++u) mx = fmaxf(mx, x[u]);
-    const float mn = fmaxf(st.m, mx);
+    if (mx > st.m) {  // a new running max: rescale the sum (else the factor would be exactly 1)
+      st.s *= expf(st.m - mx);
+      st.m = mx;
+    }
     float sum = 0.f;
 #pragma unroll
-    for (int u = 0; u < N; ++u) sum += expf(x[u] - mn);
-    st.s = st.s * expf(st.m - mn) + sum;
-    st.m = mn;
+    for (int u = 0; u < N; ++u) sum += expf(x[u] - st.m);
+    st.s += sum;
     if (proposal) return;
     float score[N];
 #pragma unroll
@@ -98,8 +107,13 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) 
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t word = cur[BF16 ? 0 : e / 4][BF16 ? e / 2 : e % 4];
-        x[e] = BF16 ? (e & 1 ? __uint_as_float(word & 0xffff0000u) : __uint_as_float(word << 16)) : __uint_as_float(word);
-        if (a.softcap > 0.f) x[e] = E::round(tanhf(x[e] / a.softcap) * a.softcap);  // the reference divides by the cap
+        if constexpr (BF16) {
+          const uint32_t bits = e & 1 ? word >> 16 : word & 0xffffu;
+          x[e] = a.softcap > 0.f ? capped(bits, ct) : bf16_bits_to_f32(bits);
+        } else {
+          x[e] = __uint_as_float(word);
+          if (a.softcap > 0.f) x[e] = E::round(tanhf(x[e] / a.softcap) * a.softcap);  // the reference divides by the cap
+        }
       }
       step(x, 8 * j, 1);
     }
@@ -111,7 +125,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) 
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int c = c0 + u * kSampleThreads;
-        x[u] = c < a.vocab ? capped<BF16>(lrow, c, a.softcap) : -INFINITY;
+        x[u] = c < a.vocab ? capped_at<BF16>(lrow, c, ct) : -INFINITY;
       }
       step(x, c0, kSampleThreads);
     }
@@ -139,10 +153,33 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) 
     int token = t.idx < 0 ? 0 : (t.idx >= width ? width - 1 : t.idx);
     if (proposal && a.proposal_index) token = a.proposal_index[(int64_t)row * a.proposal_width + token];
     token = token < 0 ? 0 : (token >= a.vocab ? a.vocab - 1 : token);
-    const float x = capped<BF16>(lrow, token, a.softcap);
+    const float x = capped_at<BF16>(lrow, token, ct);
     a.token_out[row] = token;
     a.logp_out[row] = (x - t.m) - logf(t.s);
   }
+}
+
+// out = bf16(tanh(x / cap) * cap) elementwise over bf16 x, through the soft-cap table (each
+// workgroup fills its own); 8 elements per thread and step with 16-byte accesses, then the tail.
+constexpr int kCapThreads = 256;
+
+__global__ __launch_bounds__(kCapThreads) void softcap_kernel(const uint16_t* x, uint16_t* out, int64_t n, float cap) {
+  __shared__ uint16_t tab[kCapTableEntries];
+  cap_table_fill(tab, cap, threadIdx.x, kCapThreads);
+  __syncthreads();
+  const CapTable ct = cap_table(tab, cap);
+  const int64_t n8 = n / 8;
+  const int64_t stride = (int64_t)gridDim.x * kCapThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kCapThreads + threadIdx.x; i < n8; i += stride) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(x + 8 * i);
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      o[q] = f32_to_bf16_bits(capped(w[q] & 0xffffu, ct)) | (f32_to_bf16_bits(capped(w[q] >> 16, ct)) << 16);
+    *reinterpret_cast<u32x4*>(out + 8 * i) = o;
+  }
+  for (int64_t i = 8 * n8 + (int64_t)blockIdx.x * kCapThreads + threadIdx.x; i < n; i += stride)
+    out[i] = (uint16_t)f32_to_bf16_bits(capped(x[i], ct));
 }
 
 // key <- split(key)[0] = threefry2x32(key, (0, 0)), after every row has read the old key
@@ -200,4 +237,19 @@ extern "C" int g4_sample_tokens(const G4SampleArgs* args, void* stream) {
     return check_launch("g4_sample_tokens (key split)");
   }
   return G4_OK;
+}
+
+extern "C" int g4_softcap_bf16(int64_t n, const void* x, float cap, void* out, void* stream) {
+  using namespace g4;
+  if (n < 0) return fail(G4_ERR_INVALID, "g4_softcap_bf16: n %lld", (long long)n);
+  if (!(cap > 0.f) || !(cap < INFINITY)) return fail(G4_ERR_INVALID, "g4_softcap_bf16: cap must be finite and > 0");
+  if (n == 0) return G4_OK;
+  if (!x || !out) return fail(G4_ERR_INVALID, "g4_softcap_bf16: NULL pointer");
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(out) & 15))
+    return fail(G4_ERR_INVALID, "g4_softcap_bf16: x and out need 16-byte alignment");
+  const int64_t want = (n / 8 + kCapThreads - 1) / kCapThreads;
+  const unsigned grid = (unsigned)(want < 1 ? 1 : (want > 1024 ? 1024 : want));
+  hipLaunchKernelGGL(softcap_kernel, dim3(grid), dim3(kCapThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(x), static_cast<uint16_t*>(out), n, cap);
+  return check_launch("g4_softcap_bf16");
 }

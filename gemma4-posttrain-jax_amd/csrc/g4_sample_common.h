@@ -70,3 +70,56 @@ __device__ __forceinline__ RowState shfl_state(const RowState& x, int mask) {
   return y;
 }
 
+
+// The soft-cap of a bf16 value x, bf16(tanh(x / cap) * cap) with the division, tanhf and the
+// multiply in f32, through a table of the 16 binades where it is neither x nor saturated. With
+// e_c = floor(log2(cap)):
+// - 2^(e_c - 125) <= |x| < 2^(e_c - 12): y = x / cap is a normal float below 2^-12, so
+//   tanh(y) = y (1 - y^2 / 3 + ...) moves x by less than 2^-21 relative after the f32 roundings, far
+//   below half a bf16 ulp (2^-9): the result is x (smaller x would make y subnormal or zero);
+// - 2^(e_c - 12) <= |x| < 2^(e_c + 4): the table, 2 signs x 16 binades x 128 mantissas, filled with
+//   the formula itself;
+// - |x| >= 2^(e_c + 4) (y > 8), inf, NaN and |x| < 2^(e_c - 125): the formula itself (rare: a
+//   lane-divergent branch).
+constexpr int kCapTableEntries = 4096;
+
+typedef __attribute__((address_space(3))) const uint16_t LdsU16;
+
+struct CapTable {
+  const LdsU16* tab;  // LDS: entry (sign << 11) | (binade << 7) | mantissa
+  int e0;             // biased exponent of binade 0 (>= 1)
+  int e_id;           // smallest biased exponent of the identity range
+  float cap;
+};
+
+__device__ __forceinline__ float softcap_formula(float x, float cap) {
+  return round_bf16(tanhf(x / cap) * cap);  // the reference divides by the cap
+}
+
+__device__ __forceinline__ CapTable cap_table(const void* lds_tab, float cap) {
+  const int ec = (int)((__float_as_uint(cap) >> 23) & 0xff);
+  CapTable t;
+  t.tab = (const LdsU16*)lds_tab;
+  t.e0 = ec - 12 < 1 ? 1 : ec - 12;
+  t.e_id = ec - 125 < 1 ? 1 : ec - 125;
+  t.cap = cap;
+  return t;
+}
+
+// Fills the table with threads tid, tid + nthreads, ... (the caller synchronizes before use).
+__device__ __forceinline__ void cap_table_fill(uint16_t* tab, float cap, int tid, int nthreads) {
+  const int e0 = cap_table(tab, cap).e0;
+  for (int i = tid; i < kCapTableEntries; i += nthreads) {
+    const int e = e0 + ((i >> 7) & 15);
+    const uint32_t bits = ((uint32_t)(i >> 11) << 15) | ((uint32_t)(e < 255 ? e : 255) << 7) | (uint32_t)(i & 127);
+    tab[i] = (uint16_t)f32_to_bf16_bits(softcap_formula(bf16_bits_to_f32(bits), cap));
+  }
+}
+
+__device__ __forceinline__ float capped(uint32_t bits, const CapTable& t) {
+  const uint32_t mag = bits & 0x7fffu;
+  const int e = (int)(mag >> 7), rel = e - t.e0;
+  if (rel < 0 && e >= t.e_id) return bf16_bits_to_f32(bits);
+  if (rel >= 0 && rel < 16) return bf16_bits_to_f32(t.tab[((bits >> 15) << 11) | ((uint32_t)rel << 7) | (mag & 127u)]);
+  return softcap_formula(bf16_bits_to_f32(bits), t.cap);
+}

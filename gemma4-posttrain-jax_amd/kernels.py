@@ -401,6 +401,19 @@ def sample_tokens(logits: torch.Tensor, *, softcap: float | None, temperature: f
     return token_out, logp_out
 
 
+def softcap(x: torch.Tensor, cap: float, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """g4_softcap_bf16: ``bf16(tanh(x / cap) * cap)`` elementwise over a contiguous bf16 tensor (the
+    f32 division, tanh and multiply of forward_lm_head's soft-cap); ``out`` may be ``x``."""
+
+    if x.dtype != torch.bfloat16 or not x.is_contiguous():
+        raise ValueError("softcap takes a contiguous bf16 tensor")
+    out = torch.empty_like(x) if out is None else out
+    if out.dtype != x.dtype or out.shape != x.shape or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bf16 tensor of x's shape")
+    _lib.check(_lib.lib().g4_softcap_bf16(x.numel(), _ptr(x), float(cap), _ptr(out), _stream()), "g4_softcap_bf16")
+    return out
+
+
 LM_HEAD_MAX_ROWS = 256
 
 

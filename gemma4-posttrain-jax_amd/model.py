@@ -479,7 +479,10 @@ def forward_lm_head(embed_tokens: torch.Tensor, hidden: torch.Tensor, softcap: f
     else:
         logits = _proj(x, embed_tokens).reshape(B, S, -1)
     if softcap is not None:
-        logits = (torch.tanh(logits.float() / softcap) * softcap).to(logits.dtype)
+        if logits.dtype == torch.bfloat16 and logits.is_cuda and logits.is_contiguous():
+            logits = kernels.softcap(logits, softcap, out=logits)  # one native pass, the same bits
+        else:
+            logits = (torch.tanh(logits.float() / softcap) * softcap).to(logits.dtype)
     return logits
 
 

@@ -293,6 +293,13 @@ typedef struct G4SampleArgs {
 int g4_sample_tokens(const G4SampleArgs* args, void* stream);
 
 /*
+ * g4_softcap_bf16: out[i] = cast_bf16(tanh(x[i] / cap) * cap) over n bf16 values, the division,
+ * tanh and multiply in f32 -- the soft-cap of forward_lm_head (model.py:676-680) as the samplers
+ * apply it. cap finite and > 0; x and out 16-byte aligned (out may alias x).
+ */
+int g4_softcap_bf16(int64_t n, const void* x, float cap, void* out, void* stream);
+
+/*
  * The decode step's LM head with the sampler in its epilogue: l = cast_bf16(x . embed^T) (bf16
  * operands, f32 accumulation; forward_lm_head with the tied embedding, model.py:676-680), then,
  * with token_out given, g4_sample_tokens' draw on l (no proposal) without l leaving the chip:

@@ -347,6 +347,15 @@ def test_lm_head_sample_rejects_invalid_arguments(override, match):
     assert re.search(match, _lib.lib().g4_last_error().decode())
 
 
+def test_softcap_rejects_invalid_arguments():
+    L = _lib.lib()
+    for args, match in [((-1, 16, 30.0, 16), "n -1"), ((8, 16, 0.0, 16), "cap"), ((8, 16, float("inf"), 16), "cap"),
+                        ((8, None, 30.0, 16), "NULL"), ((8, 18, 30.0, 16), "alignment")]:
+        assert L.g4_softcap_bf16(*args, None) == _lib.G4_ERR_INVALID
+        assert re.search(match, L.g4_last_error().decode())
+    assert L.g4_softcap_bf16(0, None, 30.0, None, None) == 0
+
+
 def test_convert_rejects_invalid_arguments():
     L = _lib.lib()
     assert L.g4_convert_f32_to_bf16(1, 1, -1, None, None) == _lib.G4_ERR_INVALID

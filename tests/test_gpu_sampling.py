@@ -127,6 +127,27 @@ def test_softcap_applied_in_the_logits_dtype(device):
     np.testing.assert_allclose(logp.cpu().numpy(), want_logp, rtol=0, atol=LOGP_ATOL)
 
 
+@pytest.mark.parametrize("cap", [30.0, 50.0, 1.5, 0.37, 1000.0, 3.0e5])
+def test_softcap_table_on_every_bf16_value(device, cap):
+    """g4_softcap_bf16 -- the samplers' soft-cap: x itself below 2^(e_cap - 12), the formula from
+    2^(e_cap + 4) on, a table filled with the formula between -- equals bf16(tanh(x / cap) * cap)
+    computed in f32 by torch on the GPU for all 65,536 bf16 encodings (NaN stays NaN)."""
+
+    x = torch.from_numpy(np.arange(65536, dtype=np.uint16).view(np.int16)).view(torch.bfloat16).to(device)
+    got = kernels.softcap(x, cap)
+    want = (torch.tanh(x.float() / cap) * cap).to(torch.bfloat16)
+    nan = torch.isnan(want.float()).cpu().numpy()
+    assert torch.isnan(got.float()).cpu().numpy()[nan].all()
+    g = got.view(torch.int16).cpu().numpy()[~nan]
+    w = want.view(torch.int16).cpu().numpy()[~nan]
+    bad = np.nonzero(g != w)[0]
+    assert bad.size == 0, f"{bad.size} encodings differ, e.g. {[hex(int(v) & 0xffff) for v in np.arange(65536)[~nan][bad[:4]]]}"
+    # in place, and a length that leaves a tail after the 8-element steps
+    y = x[:1003].clone()
+    kernels.softcap(y, cap, out=y)
+    assert torch.equal(y.view(torch.int16), got[:1003].view(torch.int16))
+
+
 @pytest.mark.parametrize("temperature,top_k,top_p", [(1.0, 0, 1.0), (0.8, 7, 1.0), (0.8, 0, 0.9)])
 def test_generate_matches_oracle_rollout(device, temperature, top_k, top_p):
     """A whole rollout at T > 0 (TINY_A, f32, left-padded row): the same completion tokens as the
