@@ -3,18 +3,27 @@
 //
 // A workgroup of NW waves owns NW * NB * 16/R consecutive query positions of one (b, kv head);
 // each wave owns NB column blocks of 16 query rows (16/R positions x R heads each), so every K and
-// V^T operand tile it reads from LDS feeds NB MFMAs. The key range is
-// walked in 32-key chunks: every chunk's K and V^T are DMA'd into LDS once per workgroup
-// (buffer_load ... lds through a ring of 4 buffers, three chunks in flight ahead of the one being
-// computed, each wave issuing an equal share) as lane-ordered
-// MFMA operand tiles, and all 8 waves read them from there — against 1 KiB of global loads per
-// MFMA when each wave loads its own operands. The key-mask bytes of the row are staged in LDS
-// once, so a chunk's validity bits are one LDS byte per lane and a ballot.
+// V^T operand tile it reads from LDS feeds NB MFMAs. The key range is walked in 32-key chunks:
+// every chunk's K and V^T are DMA'd into LDS once per workgroup (buffer_load ... lds, each wave
+// issuing an equal share, into rings of 4 slots) as lane-ordered MFMA operand tiles, and all waves
+// read them from there. The key-mask bytes of the row are staged in LDS once, so a chunk's validity
+// is one LDS byte per lane and a ballot.
 //
 // Same two passes as prefill_bf16_kernel (the reference rounds probabilities after the full-row
 // softmax): pass 1 streams K for each row's max and sum, pass 2 streams K and V and forms exact
 // bf16 probabilities exp(s - m) * (1/l) for the value product. Workgroups are launched heaviest
 // (latest positions, longest causal key range) first.
+//
+// What bounds it is the issue rate of each SIMD's two waves, VALU work included, more than the
+// MFMAs, so the schedule is built around three things:
+//  - a wave-uniform fast path: a chunk whose 32 keys every row of the wave may see (key mask,
+//    causal limit, window) skips the per-key selects, and its scores are rounded two per
+//    conversion instruction;
+//  - operand tiles read from LDS through a rolling window: tile t + W is requested right after the
+//    MFMAs of tile t, so the LDS latency hides behind the MFMAs in flight;
+//  - in pass 2 the two waves sharing a SIMD (w, w + NW/2) are half a step apart. One runs the
+//    MFMA phase (the values of chunk c-1, then the QK of chunk c) while the other runs the VALU
+//    phase (the probabilities of a chunk), at raised priority while in the MFMA phase.
 
 constexpr int kPfMaxSeq = 32768;  // key-mask bytes staged in LDS
 
@@ -32,11 +41,67 @@ __device__ __forceinline__ void wait_vmcnt() {
   __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// The 8 scores of one column block (both 16-key halves), each rounded to bf16, two values per
+// conversion instruction; element e is key 8 * grp + e of the chunk.
+__device__ __forceinline__ void pf_round8(const floatx4 (&acc)[2], float (&sc)[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w = pack_bf16x2(acc[j >> 1][2 * (j & 1)], acc[j >> 1][2 * (j & 1) + 1]);
+    sc[2 * j] = __uint_as_float(w << 16);
+    sc[2 * j + 1] = __uint_as_float(w & 0xffff0000u);
+  }
+}
+
+// S^T of one chunk for the wave's NB column blocks: K operand tiles (KT = 2 halves x KS d-slices,
+// 1 KiB each from LDS address kbase) against the q operands in registers, a rolling window of WIN
+// tiles in flight (each read waited for right before its MFMAs; the chunk's DMA is covered by the
+// caller's vmcnt wait + barrier).
+template <int KT, int KS, int NB, int WIN>
+__device__ __forceinline__ void pf_qk(uint32_t kbase, const bf16x8 (&qop)[NB][KS], floatx4 (&acc)[NB][2], int lane) {
+  static_assert(WIN >= 1 && WIN <= 8 && WIN <= KT, "window of LDS reads (lgkm_wait counts up to 7)");
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int cb = 0; cb < NB; ++cb) acc[cb][0] = acc[cb][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+  u32x4 kv[WIN];
+#pragma unroll
+  for (int j = 0; j < WIN; ++j) kv[j] = lds_read16(kbase + 1024u * j + 16u * lane);
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    const int bb = t / KS, s = t - bb * KS;
+    const int later = KT - 1 - t < WIN - 1 ? KT - 1 - t : WIN - 1;  // reads issued after tile t's
+    lgkm_wait(later, kv[t % WIN]);
+#pragma unroll
+    for (int cb = 0; cb < NB; ++cb) acc[cb][bb] = mfma16x16x32(as_bf16x8(kv[t % WIN]), qop[cb][s], acc[cb][bb]);
+    if (t + WIN < KT) kv[t % WIN] = lds_read16(kbase + 1024u * (t + WIN) + 16u * lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// O^T += V^T P^T over one chunk: VT value operand tiles (one per 16-dim block, 1 KiB each from LDS
+// address vbase) against the wave's probabilities, a rolling window of WIN tiles in flight.
+template <int VT, int NB, int WIN>
+__device__ __forceinline__ void pf_pv(uint32_t vbase, const bf16x8 (&pop)[NB], floatx4 (&oacc)[NB][VT], int lane) {
+  static_assert(WIN >= 1 && WIN <= 8 && WIN <= VT, "window of LDS reads (lgkm_wait counts up to 7)");
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 vv[WIN];
+#pragma unroll
+  for (int i = 0; i < WIN; ++i) vv[i] = lds_read16(vbase + 1024u * i + 16u * lane);
+#pragma unroll
+  for (int i = 0; i < VT; ++i) {
+    const int later = VT - 1 - i < WIN - 1 ? VT - 1 - i : WIN - 1;
+    lgkm_wait(later, vv[i % WIN]);
+#pragma unroll
+    for (int cb = 0; cb < NB; ++cb) oacc[cb][i] = mfma16x16x32(as_bf16x8(vv[i % WIN]), pop[cb], oacc[cb][i]);
+    if (i + WIN < VT) vv[i % WIN] = lds_read16(vbase + 1024u * (i + WIN) + 16u * lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 template <int D, int NB, int NW>
 __global__ __launch_bounds__(NW * 64) void prefill_bf16_lds_kernel(G4PrefillArgs a) {
   using S_ = PfShape<D, NW>;
   constexpr int KS = D / 32;
-  // four buffers as separate arrays, so the compiler's wait before reading one does not include
+  // the ring slots as separate arrays, so the compiler's wait before reading one does not include
   // the DMA still in flight into the others
   __shared__ __attribute__((aligned(1024))) unsigned char kb0[S_::KT][1024];
   __shared__ __attribute__((aligned(1024))) unsigned char vb0[S_::VT][1024];
@@ -95,34 +160,45 @@ __global__ __launch_bounds__(NW * 64) void prefill_bf16_lds_kernel(G4PrefillArgs
   const int kmin = a.window > 0 ? max(0, p0 - a.window + 1) : 0;
   const int c_begin = kmin >> 5, c_end = pos_last >> 5;
 
-  // this wave's share of a chunk's operand tiles into LDS
-  auto issue = [&](int c, unsigned char (&kt)[S_::KT][1024], unsigned char (&vt)[S_::VT][1024], bool with_v) {
-    const int c0 = c << 5;
+  // This wave's share of a chunk's K / V^T operand tiles into LDS. Both layouts put chunk c at byte
+  // 64 * D * c, so a tile's lane offset does not depend on the chunk, which rides in soffset (every
+  // chunk issued lies inside the cache rows: c <= (S - 1) / 32 and S <= k_stride).
+  auto issue_k = [&](int c, unsigned char (&kt)[S_::KT][1024]) {
+    const uint32_t cofs = (uint32_t)c * (uint32_t)(64 * D);
 #pragma unroll
     for (int i = 0; i < S_::KT_W; ++i) {
       const int t = w * S_::KT_W + i, bb = t / KS, s = t - bb * KS;
-      const int key = c0 + 8 * (col >> 2) + 4 * bb + (col & 3);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)&kt[t][0], 16,
-                                               (uint32_t)kt_index(key, 32 * s + 8 * grp, D) * 2u, 0, 0, 0);
+      const uint32_t ko = (uint32_t)kt_index(8 * (col >> 2) + 4 * bb + (col & 3), 32 * s + 8 * grp, D) * 2u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)&kt[t][0], 16, ko, cofs, 0, 0);
     }
-    if (with_v) {
+  };
+  auto issue_v = [&](int c, unsigned char (&vt)[S_::VT][1024]) {
+    const uint32_t cofs = (uint32_t)c * (uint32_t)(64 * D);
 #pragma unroll
-      for (int i = 0; i < S_::VT_W; ++i) {
-        const int t = w * S_::VT_W + i;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rv, (__attribute__((address_space(3))) void*)&vt[t][0], 16,
-            vt_operand_bytes(4 * c + grp, 16 * t + col, D), 0, 0, 0);
-      }
+    for (int i = 0; i < S_::VT_W; ++i) {
+      const int t = w * S_::VT_W + i;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&vt[t][0], 16,
+                                               vt_operand_bytes(grp, 16 * t + col, D), cofs, 0, 0);
     }
   };
-  // key-mask bits of the chunk's 32 keys (bit e <-> key c0 + 8*grp + e), shared by the blocks
-  auto mask_bits = [&](int c) -> uint32_t {
+  // key-mask ballot of the chunk's 32 keys (lanes l and l + 32 both hold key 32 c + l % 32)
+  auto chunk_ballot = [&](int c) -> uint64_t {
     const int key = (c << 5) + (lane & 31);
-    const uint64_t mb = __ballot(key < S && km_lds[key < S ? key : 0] != 0);
-    return (uint32_t)(mb >> (8 * grp)) & 0xffu;
+    return __ballot(key < S && km_lds[key < S ? key : 0] != 0);
   };
-  // ... restricted to the keys block cb's row may see: causal, and the window
-  auto valid_bits = [&](int c, uint32_t bits, int cb) -> uint32_t {
+  // Wave-uniform: every row of this wave sees all 32 keys of chunk c (key mask, causal limit,
+  // window, rows inside the sequence).
+  const int wpos_min = p0 + w * ppw;
+  const int wpos_max = wpos_min + (NB - 1) * ppc + 15 / R;
+  auto chunk_full = [&](int c, uint64_t mb) -> bool {
+    const int k0 = c << 5;
+    return (uint32_t)mb == 0xffffffffu && k0 + 31 <= wpos_min && wpos_max < S &&
+           (a.window <= 0 || k0 >= wpos_max - a.window + 1);
+  };
+  // this lane's key bits of the chunk (bit e <-> key 32 c + 8 grp + e) for block cb's row: the key
+  // mask, causal, and the window
+  auto valid_bits = [&](int c, uint64_t mb, int cb) -> uint32_t {
+    uint32_t bits = (uint32_t)(mb >> (8 * grp)) & 0xffu;
     const int lo = (c << 5) + 8 * grp;
     const int hi_ok = my_pos[cb] - lo;  // keys lo + e valid for e <= hi_ok
     bits &= hi_ok >= 7 ? 0xffu : (hi_ok < 0 ? 0u : (0xffu >> (7 - hi_ok)));
@@ -132,35 +208,6 @@ __global__ __launch_bounds__(NW * 64) void prefill_bf16_lds_kernel(G4PrefillArgs
     }
     return row_ok[cb] ? bits : 0u;
   };
-  // scores of both 16-key halves (bb) for every block: each K tile is read once for NB MFMAs
-  // (the scheduling barriers bound how many operand tiles are read ahead into registers)
-  auto qk = [&](unsigned char (&kt)[S_::KT][1024], floatx4 (&acc)[NB][2]) {
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
-      floatx4 x[NB];
-#pragma unroll
-      for (int cb = 0; cb < NB; ++cb) x[cb] = floatx4{0.f, 0.f, 0.f, 0.f};
-      // the K tiles are read by inline-assembly LDS reads, each waited for right before its MFMAs
-      // (the DMA of this chunk is covered by wait_chunk's vmcnt + barrier)
-      constexpr int KG = KS < 4 ? KS : 4;  // tiles read ahead (bounds the registers they hold)
-#pragma unroll
-      for (int s0 = 0; s0 < KS; s0 += KG) {
-        u32x4 kv[KG];
-#pragma unroll
-        for (int j = 0; j < KG; ++j) kv[j] = lds_read16(lds_addr(&kt[bb * KS + s0 + j][16 * lane]));
-#pragma unroll
-        for (int j = 0; j < KG; ++j) {
-          lgkm_wait(KG - 1 - j, kv[j]);
-#pragma unroll
-          for (int cb = 0; cb < NB; ++cb) x[cb] = mfma16x16x32(as_bf16x8(kv[j]), qop[cb][s0 + j], x[cb]);
-        }
-      }
-#pragma unroll
-      for (int cb = 0; cb < NB; ++cb) acc[cb][bb] = x[cb];
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
 
   // ---- pass 1: row max and sum --------------------------------------------------------------------
   float m[NB], l[NB];
@@ -169,15 +216,31 @@ __global__ __launch_bounds__(NW * 64) void prefill_bf16_lds_kernel(G4PrefillArgs
     m[cb] = kBf16Min;
     l[cb] = 0.f;
   }
+  // one rescale per chunk: l <- l * exp(m - m') + sum exp(s - m') with m' = max(m, chunk max)
+  // (masked keys score the fill value, whose exp vanishes against any real maximum)
   auto stats = [&](int c, unsigned char (&kt)[S_::KT][1024]) {
     floatx4 acc[NB][2];
-    qk(kt, acc);
-    const uint32_t mbits = mask_bits(c);
+    pf_qk<S_::KT, KS, NB, 8>(lds_addr(&kt[0][0]), qop, acc, lane);  // pass 1 holds no value accumulators
+    const uint64_t mb = chunk_ballot(c);
+    if (chunk_full(c, mb)) {
+#pragma unroll
+      for (int cb = 0; cb < NB; ++cb) {
+        float sc[8], mx = kBf16Min;
+        pf_round8(acc[cb], sc);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, sc[e]);
+        const float mn = fmaxf(m[cb], mx);
+        float sum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += __expf(sc[e] - mn);
+        l[cb] = l[cb] * __expf(m[cb] - mn) + sum;
+        m[cb] = mn;
+      }
+      return;
+    }
 #pragma unroll
     for (int cb = 0; cb < NB; ++cb) {
-      // one rescale per chunk: l <- l * exp(m - m') + sum exp(s - m') with m' = max(m, chunk max)
-      // (masked keys score the fill value, whose exp vanishes against any real maximum)
-      const uint32_t bits = valid_bits(c, mbits, cb);
+      const uint32_t bits = valid_bits(c, mb, cb);
       float sc[8], mx = kBf16Min;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -194,44 +257,37 @@ __global__ __launch_bounds__(NW * 64) void prefill_bf16_lds_kernel(G4PrefillArgs
   };
   // One pipeline step: wait for this wave's DMA of chunk c (chunks c+1, c+2 may stay in flight),
   // barrier (every wave's share of chunk c has landed, and every wave is done with chunk c-1, whose
-  // buffer the DMA of chunk c+3 reuses), queue chunk c+3, compute chunk c.
-  auto wait_chunk = [&](int c, int c_last, bool with_v) {
+  // slot the DMA of chunk c+3 reuses), queue chunk c+3, compute chunk c.
+  auto wait_chunk = [&](int c, int c_last) {
+    constexpr int n = S_::KT_W;
     const int ahead = min(c_last - c, 2);  // chunks queued after c
-    if (with_v) {
-      constexpr int n = S_::KT_W + S_::VT_W;
-      if (ahead >= 2) wait_vmcnt<2 * n>();
-      else if (ahead == 1) wait_vmcnt<n>();
-      else wait_vmcnt<0>();
-    } else {
-      constexpr int n = S_::KT_W;
-      if (ahead >= 2) wait_vmcnt<2 * n>();
-      else if (ahead == 1) wait_vmcnt<n>();
-      else wait_vmcnt<0>();
-    }
+    if (ahead >= 2) wait_vmcnt<2 * n>();
+    else if (ahead == 1) wait_vmcnt<n>();
+    else wait_vmcnt<0>();
     wg_barrier();
   };
   __syncthreads();  // key-mask bytes in LDS (no DMA in flight yet)
-  issue(c_begin, kb0, vb0, false);
-  if (c_begin + 1 <= c_end) issue(c_begin + 1, kb1, vb1, false);
-  if (c_begin + 2 <= c_end) issue(c_begin + 2, kb2, vb2, false);
+  issue_k(c_begin, kb0);
+  if (c_begin + 1 <= c_end) issue_k(c_begin + 1, kb1);
+  if (c_begin + 2 <= c_end) issue_k(c_begin + 2, kb2);
   // (guarded steps rather than early exits: the accumulators then merge at one point per step)
   for (int c = c_begin; c <= c_end; c += 4) {
-    wait_chunk(c, c_end, false);
-    if (c + 3 <= c_end) issue(c + 3, kb3, vb3, false);
+    wait_chunk(c, c_end);
+    if (c + 3 <= c_end) issue_k(c + 3, kb3);
     stats(c, kb0);
     if (c + 1 <= c_end) {
-      wait_chunk(c + 1, c_end, false);
-      if (c + 4 <= c_end) issue(c + 4, kb0, vb0, false);
+      wait_chunk(c + 1, c_end);
+      if (c + 4 <= c_end) issue_k(c + 4, kb0);
       stats(c + 1, kb1);
     }
     if (c + 2 <= c_end) {
-      wait_chunk(c + 2, c_end, false);
-      if (c + 5 <= c_end) issue(c + 5, kb1, vb1, false);
+      wait_chunk(c + 2, c_end);
+      if (c + 5 <= c_end) issue_k(c + 5, kb1);
       stats(c + 2, kb2);
     }
     if (c + 3 <= c_end) {
-      wait_chunk(c + 3, c_end, false);
-      if (c + 6 <= c_end) issue(c + 6, kb2, vb2, false);
+      wait_chunk(c + 3, c_end);
+      if (c + 6 <= c_end) issue_k(c + 6, kb2);
       stats(c + 3, kb3);
     }
   }
@@ -263,15 +319,25 @@ __global__ __launch_bounds__(NW * 64) void prefill_bf16_lds_kernel(G4PrefillArgs
   for (int cb = 0; cb < NB; ++cb)
 #pragma unroll
     for (int i = 0; i < S_::VT; ++i) oacc[cb][i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  auto values = [&](int c, unsigned char (&kt)[S_::KT][1024], unsigned char (&vt)[S_::VT][1024]) {
-    floatx4 acc[NB][2];
-    qk(kt, acc);
-    const uint32_t mbits = mask_bits(c);
+  // exact bf16 probabilities of chunk c from its score accumulators (the B operand of O^T += V^T P^T)
+  auto probs = [&](int c, const floatx4 (&acc)[NB][2], bf16x8 (&pop)[NB]) {
+    const uint64_t mb = chunk_ballot(c);
+    if (!any_masked && chunk_full(c, mb)) {
+#pragma unroll
+      for (int cb = 0; cb < NB; ++cb) {
+        float sc[8], p[8];
+        pf_round8(acc[cb], sc);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p[e] = __expf(sc[e] - m[cb]) * rl[cb];
+        pop[cb] = as_bf16x8(u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                                  pack_bf16x2(p[6], p[7])});
+      }
+      return;
+    }
     const int kb = (c << 5) + 8 * grp;
-    bf16x8 pop[NB];
 #pragma unroll
     for (int cb = 0; cb < NB; ++cb) {
-      const uint32_t bits = valid_bits(c, mbits, cb);
+      const uint32_t bits = valid_bits(c, mb, cb);
       float p[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -281,44 +347,61 @@ __global__ __launch_bounds__(NW * 64) void prefill_bf16_lds_kernel(G4PrefillArgs
       pop[cb] = as_bf16x8(u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
                                 pack_bf16x2(p[6], p[7])});
     }
-    constexpr int GRP = 8 / NB;  // V tiles read ahead per scheduling group
-#pragma unroll
-    for (int i0 = 0; i0 < S_::VT; i0 += GRP) {
-      __builtin_amdgcn_sched_barrier(0);
-      u32x4 vv[GRP];
-#pragma unroll
-      for (int i = i0; i < i0 + GRP && i < S_::VT; ++i) vv[i - i0] = lds_read16(lds_addr(&vt[i][16 * lane]));
-#pragma unroll
-      for (int i = i0; i < i0 + GRP && i < S_::VT; ++i) {
-        lgkm_wait((i0 + GRP < S_::VT ? i0 + GRP : S_::VT) - 1 - i, vv[i - i0]);
-#pragma unroll
-        for (int cb = 0; cb < NB; ++cb) oacc[cb][i] = mfma16x16x32(as_bf16x8(vv[i - i0]), pop[cb], oacc[cb][i]);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
   };
-  issue(c2_begin, kb0, vb0, true);
-  if (c2_begin + 1 <= c2_end) issue(c2_begin + 1, kb1, vb1, true);
-  if (c2_begin + 2 <= c2_end) issue(c2_begin + 2, kb2, vb2, true);
-  for (int c = c2_begin; c <= c2_end; c += 4) {
-    wait_chunk(c, c2_end, true);
-    if (c + 3 <= c2_end) issue(c + 3, kb3, vb3, true);
-    values(c, kb0, vb0);
-    if (c + 1 <= c2_end) {
-      wait_chunk(c + 1, c2_end, true);
-      if (c + 4 <= c2_end) issue(c + 4, kb0, vb0, true);
-      values(c + 1, kb1, vb1);
-    }
-    if (c + 2 <= c2_end) {
-      wait_chunk(c + 2, c2_end, true);
-      if (c + 5 <= c2_end) issue(c + 5, kb1, vb1, true);
-      values(c + 2, kb2, vb2);
-    }
-    if (c + 3 <= c2_end) {
-      wait_chunk(c + 3, c2_end, true);
-      if (c + 6 <= c2_end) issue(c + 6, kb2, vb2, true);
-      values(c + 3, kb3, vb3);
-    }
+  // One barrier per chunk step. After the barrier of chunk c every wave runs two phases:
+  // M(c) = the values of chunk c-1 (its V^T tiles x the probabilities formed earlier) and the QK of
+  // chunk c (MFMA work), and P(c) = the probabilities of chunk c (VALU work). Waves 0..NW/2-1 run
+  // M(c) then P(c); waves NW/2.. run P(c-1) then M(c). Chunk j sits in slot (j - c2_begin) % 4 of
+  // both rings; K(c) and V(c-1) are read only in step c, and the barrier of chunk c queues K(c+3)
+  // and V(c+2) into the slots of K(c-1) and V(c-2), which step c-1 finished reading.
+  const bool lead = w < NW / 2;
+  // this wave's DMAs of K(c) and V(c-1) have landed: queued after them are V(c) and, where they
+  // exist, K(c+1), K(c+2) and V(c+1)
+  auto wait_step = [&](int c, int c_last) {
+    constexpr int nk = S_::KT_W, nv = S_::VT_W;
+    if (c + 2 <= c_last) wait_vmcnt<2 * nk + 2 * nv>();
+    else if (c + 1 <= c_last) wait_vmcnt<nk + 2 * nv>();
+    else wait_vmcnt<nv>();
+    wg_barrier();
+  };
+  floatx4 acc[NB][2];
+  bf16x8 pop[NB];
+  auto p2_step = [&](int c, unsigned char (&kcur)[S_::KT][1024], unsigned char (&vprev)[S_::VT][1024],
+                     unsigned char (&knext)[S_::KT][1024], unsigned char (&vnext)[S_::VT][1024]) {
+    wait_step(c, c2_end);
+    if (c + 3 <= c2_end) issue_k(c + 3, knext);
+    if (c + 2 <= c2_end) issue_v(c + 2, vnext);
+    if (!lead && c > c2_begin) probs(c - 1, acc, pop);
+    __builtin_amdgcn_s_setprio(1);
+    if (c > c2_begin) pf_pv<S_::VT, NB, 4>(lds_addr(&vprev[0][0]), pop, oacc, lane);
+    pf_qk<S_::KT, KS, NB, 4>(lds_addr(&kcur[0][0]), qop, acc, lane);
+    __builtin_amdgcn_s_setprio(0);
+    if (lead) probs(c, acc, pop);
+  };
+  // prologue, in the steady state's order: K(b), K(b+1), V(b), K(b+2), V(b+1) (b = c2_begin <= c2_end:
+  // a row's own position is one of its keys)
+  issue_k(c2_begin, kb0);
+  if (c2_begin + 1 <= c2_end) issue_k(c2_begin + 1, kb1);
+  issue_v(c2_begin, vb0);
+  if (c2_begin + 2 <= c2_end) issue_k(c2_begin + 2, kb2);
+  if (c2_begin + 1 <= c2_end) issue_v(c2_begin + 1, vb1);
+  for (int c = c2_begin; c <= c2_end; c += 4) {  // guarded steps: the accumulators merge once per step
+    p2_step(c, kb0, vb3, kb3, vb2);
+    if (c + 1 <= c2_end) p2_step(c + 1, kb1, vb0, kb0, vb3);
+    if (c + 2 <= c2_end) p2_step(c + 2, kb2, vb1, kb1, vb0);
+    if (c + 3 <= c2_end) p2_step(c + 3, kb3, vb2, kb2, vb1);
+  }
+  // the last chunk's values: every wave's share of its V^T tiles has landed after this barrier
+  wait_vmcnt<0>();
+  wg_barrier();
+  if (!lead) probs(c2_end, acc, pop);
+  {
+    const int slot = (c2_end - c2_begin) & 3;
+    const uint32_t vlast = slot == 0   ? lds_addr(&vb0[0][0])
+                           : slot == 1 ? lds_addr(&vb1[0][0])
+                           : slot == 2 ? lds_addr(&vb2[0][0])
+                                       : lds_addr(&vb3[0][0]);
+    pf_pv<S_::VT, NB, 4>(vlast, pop, oacc, lane);
   }
 
 #pragma unroll
