@@ -229,7 +229,7 @@ int raise_prefill_lds_limit(int device) {
 template <int D>
 void launch_prefill_lds(const G4PrefillArgs& a, hipStream_t st) {
   const int ppb = kPfWaves * kPfBlocks * (16 / a.group);
-  const dim3 grid((unsigned)((a.seq + ppb - 1) / ppb), a.kv_heads, a.batch);
+  const dim3 grid((unsigned)((a.seq + ppb - 1) / ppb) * (unsigned)a.kv_heads * (unsigned)a.batch);
   const size_t lds = ((size_t)a.seq + 15) / 16 * 16;
   hipLaunchKernelGGL((prefill_bf16_lds_kernel<D, kPfBlocks, kPfWaves>), grid, dim3(kPfWaves * 64), lds, st, a);
 }
