@@ -177,6 +177,17 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voffset, (int)soffset, 0));
 }
 
+// Cache-policy bits of a non-temporal access (the nt bit), for streams of which each byte is read
+// by one workgroup once: the value cache, and the key cache where no other workgroup reads the same
+// rows. On the decode streams nt loads measured 5-7 % faster than plain ones (config 2: 16.3 -> 15.4
+// us with nt on V only; the E2B two-launch layer: 60.6 -> 56.4 us with nt on K and V). Where the two
+// workgroups of a pair read the same K rows (the second from L2), plain loads stay faster.
+constexpr int kNonTemporal = 2;
+
+__device__ __forceinline__ u32x4 buffer_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voffset, uint32_t soffset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voffset, (int)soffset, kNonTemporal));
+}
+
 __device__ __forceinline__ floatx4 mfma16x16x32(bf16x8 a, bf16x8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

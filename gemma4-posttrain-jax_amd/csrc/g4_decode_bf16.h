@@ -81,7 +81,8 @@ __device__ __forceinline__ bf16x8 q_operand(const uint16_t* qs, int R, int col, 
   return as_bf16x8(v);
 }
 
-template <int D>
+// NT: non-temporal loads (no other workgroup reads these key rows).
+template <int D, bool NT = false>
 __device__ __forceinline__ void load_k_chunk(u32x4 (&kv)[2][D / 32], __amdgpu_buffer_rsrc_t rk, int c0, int col,
                                              int grp) {
 #pragma unroll
@@ -89,7 +90,7 @@ __device__ __forceinline__ void load_k_chunk(u32x4 (&kv)[2][D / 32], __amdgpu_bu
     // block (chunk, s, bb) of the key layout: lane (grp, col) reads 16 bytes at col * 64 + grp * 16
     const uint32_t voff = (uint32_t)((((c0 >> 5) * (D >> 5)) * 2 + bb) * 1024 + col * 64 + grp * 16);
 #pragma unroll
-    for (int s = 0; s < D / 32; ++s) kv[bb][s] = buffer_load16(rk, voff + 2048u * s, 0u);
+    for (int s = 0; s < D / 32; ++s) kv[bb][s] = NT ? buffer_load16_nt(rk, voff + 2048u * s, 0u) : buffer_load16(rk, voff + 2048u * s, 0u);
   }
 }
 

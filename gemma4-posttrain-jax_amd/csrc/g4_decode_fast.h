@@ -112,12 +112,12 @@ __device__ __forceinline__ void fast_load_v(u32x4 (&vg)[8][DPW], __amdgpu_buffer
     if (c < n_chunks) {
       const uint32_t voff = vt_operand_bytes(4 * c + grp, col, D);
 #pragma unroll
-      for (int ii = 0; ii < DPW; ++ii) vg[i][ii] = buffer_load16(rv, voff, 256u * (dblock0 + ii));
+      for (int ii = 0; ii < DPW; ++ii) vg[i][ii] = buffer_load16_nt(rv, voff, 256u * (dblock0 + ii));
     }
   }
 }
 
-// fast_load_v with every load issued (a chunk past the row re-reads the last one: an L2 hit), so the
+// fast_load_v with every load issued (a chunk past the row re-reads the last one), so the
 // number of loads behind it is fixed and later waits need not include them
 template <int DPW>
 __device__ __forceinline__ void fast_load_v_fixed(u32x4 (&vg)[8][DPW], __amdgpu_buffer_rsrc_t rv, int D, int g,
@@ -128,7 +128,7 @@ __device__ __forceinline__ void fast_load_v_fixed(u32x4 (&vg)[8][DPW], __amdgpu_
     const int c = g * 8 + i < n_chunks ? g * 8 + i : c_last;
     const uint32_t voff = vt_operand_bytes(4 * c + grp, col, D);
 #pragma unroll
-    for (int ii = 0; ii < DPW; ++ii) vg[i][ii] = buffer_load16(rv, voff, 256u * (dblock0 + ii));
+    for (int ii = 0; ii < DPW; ++ii) vg[i][ii] = buffer_load16_nt(rv, voff, 256u * (dblock0 + ii));
   }
 }
 

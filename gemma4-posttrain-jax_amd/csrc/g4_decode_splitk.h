@@ -77,8 +77,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_scores_k
   const bool ok1 = slot_valid_flat(a, b, kr, c1 + (lane & 31), mb1);
   __builtin_amdgcn_sched_barrier(0);
   u32x4 k0[2][D / 32], k1[2][D / 32];
-  load_k_chunk<D>(k0, rk, c0, col, grp);
-  load_k_chunk<D>(k1, rk, c1, col, grp);
+  load_k_chunk<D, true>(k0, rk, c0, col, grp);
+  load_k_chunk<D, true>(k1, rk, c1, col, grp);
   __builtin_amdgcn_sched_barrier(0);
   if (owner && lane < D / 8) reinterpret_cast<u32x4*>(nk_lds)[lane] = nkv;  // read back by this wave only
   const uint64_t vb0 = __ballot(ok0 && mb0 != 0);
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_k
     if (i < n_here) {
       const uint32_t voff = vt_operand_bytes(4 * (cbase + i) + grp, col, D);
 #pragma unroll
-      for (int ii = 0; ii < DPW; ++ii) vv[i][ii] = buffer_load16(rv, voff, 256u * ((dh * NW + w) * DPW + ii));
+      for (int ii = 0; ii < DPW; ++ii) vv[i][ii] = buffer_load16_nt(rv, voff, 256u * ((dh * NW + w) * DPW + ii));
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_k
     const bf16x8 pop = prob_operand(sp, kStageStride, (i << 5) + 8 * grp, R, col);
 #pragma unroll
     for (int ii = 0; ii < DPW; ++ii)
-      oacc[ii] = mfma16x16x32(as_bf16x8(buffer_load16(rv, voff, 256u * ((dh * NW + w) * DPW + ii))), pop, oacc[ii]);
+      oacc[ii] = mfma16x16x32(as_bf16x8(buffer_load16_nt(rv, voff, 256u * ((dh * NW + w) * DPW + ii))), pop, oacc[ii]);
   }
   // lane (grp, col < R) holds O^T[d = 16*(w*DPW + ii) + 4*grp + j][head col]
   if (col < R) {

@@ -108,7 +108,7 @@ __device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles* __res
     const int cs = c < n_chunks ? c : c_last;
     const uint32_t voff = vt_operand_bytes(4 * cs + grp, col, D);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&tiles[w][c & (NW - 1)][0],
-                                             16, voff, soff, 0, 0);
+                                             16, voff, soff, 0, kNonTemporal);
   };
 #pragma unroll
   for (int c = 0; c < NW; ++c) dma_v(vt_lo, c);

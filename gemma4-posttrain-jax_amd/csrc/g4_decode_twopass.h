@@ -85,7 +85,7 @@ __global__ __launch_bounds__(kTpWavesS * 64) void decode_bf16_tp_scores_kernel(G
     const __amdgpu_buffer_rsrc_t rk =
         make_rsrc(reinterpret_cast<const uint16_t*>(a.cache_k) + (int64_t)pair * a.slot_stride * D,
                   (uint32_t)a.slot_stride * D * 2u);
-    load_k_chunk<D>(kv, rk, chunk << 5, col, grp);
+    load_k_chunk<D, true>(kv, rk, chunk << 5, col, grp);
   }
   if constexpr (PREP) {
     if (w < R) {
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(kTpWavesV * 64) void decode_bf16_tp_values_kernel(G
   u32x4 vv[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
-    vv[c] = buffer_load16(rv, c < n_chunks ? vt_operand_bytes(4 * c + grp, col, D) : pair_bytes, soff);
+    vv[c] = buffer_load16_nt(rv, c < n_chunks ? vt_operand_bytes(4 * c + grp, col, D) : pair_bytes, soff);
 
   // exact probabilities: head w first; heads w + 4, w + 8, ... (R > 4) from rows loaded afterwards
   const bool all_masked = tp_probabilities<NB>(sv, w, w < R, sp, kStride, NCH * 32, n_scanned, a.capacity, lane);
@@ -283,7 +283,7 @@ __global__ __launch_bounds__(kTpWavesV * 64) void decode_bf16_tp_values_kernel(G
   if (all_masked) {
     const int cap_chunks = (a.capacity + 31) >> 5;
     for (int c = n_chunks; c < cap_chunks; ++c) {
-      const u32x4 v = buffer_load16(rv, vt_operand_bytes(4 * c + grp, col, D), soff);
+      const u32x4 v = buffer_load16_nt(rv, vt_operand_bytes(4 * c + grp, col, D), soff);
       oacc = mfma16x16x32(as_bf16x8(v), prob_operand(sp, kStride, (c << 5) + 8 * grp, R, col), oacc);
     }
   }
