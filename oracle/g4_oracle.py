@@ -818,6 +818,10 @@ def generate(params, cfg, prompt_ids, prompt_mask, *, sampler_config: SamplerCon
         raise ValueError("prompt width does not match max_prompt_len")
     if sc.max_prompt_len <= 0 or sc.max_new_tokens <= 0:
         raise ValueError("max_prompt_len and max_new_tokens must both be positive")
+    if sc.top_k > cfg.vocab_size:  # sampler.py:219-220
+        raise ValueError(f"top_k={sc.top_k} exceeds vocab_size={cfg.vocab_size}")
+    if not math.isfinite(sc.temperature):  # sampler.py:221-222
+        raise ValueError("temperature must be finite")
     if not math.isfinite(sc.top_p) or not 0 < sc.top_p <= 1:
         raise ValueError("top_p must be finite and in (0, 1]")
     prompt_mask = prompt_mask.astype(bool)

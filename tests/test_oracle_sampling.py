@@ -102,3 +102,18 @@ def test_generate_key_schedule_is_split_per_step():
         key, sub = JR.split(key)
         tok, _ = O.sample_token(logits, temperature=1.0, key=sub)
         np.testing.assert_array_equal(rb.completion_ids[:, t], tok)
+
+
+@pytest.mark.parametrize("kw,msg", [(dict(top_k=10 ** 6), "exceeds vocab_size"),
+                                    (dict(temperature=float("inf")), "temperature must be finite"),
+                                    (dict(temperature=float("nan")), "temperature must be finite"),
+                                    (dict(top_p=0.0), "top_p")])
+def test_generate_rejects_the_references_invalid_configs(kw, msg):
+    """generate raises on the reference's invalid sampler configs (sampler.py:215-224): top_k above
+    the vocabulary, a non-finite temperature, top_p outside (0, 1]."""
+
+    cfg = O.config_from_hf(__import__("hf_util").TINY_A)
+    params = O.init_params(cfg, seed=0, dtype=O.F32)
+    ids = np.array([[5, 6, 7]], np.int32)
+    with pytest.raises(ValueError, match=msg):
+        O.generate(params, cfg, ids, np.ones_like(ids, bool), sampler_config=O.SamplerConfig(3, 2, **kw))
