@@ -242,8 +242,8 @@ bool use_two_pass(const G4DecodeArgs& a) {
 
 template <int D, int NCH>
 void launch_tp_values(const G4DecodeArgs& a, const uint16_t* ws, int row_slots, hipStream_t st) {
-  hipLaunchKernelGGL((decode_bf16_tp_values_kernel<D, NCH>), dim3((unsigned)((int64_t)a.batch * a.kv_heads * (D / 16 / kTpWavesV))),
-                     dim3(kTpWavesV * 64), (size_t)a.group * tp_lds_stride(NCH) * 2, st, a, ws, row_slots);
+  hipLaunchKernelGGL((decode_bf16_tp_values_kernel<D, NCH>), dim3((unsigned)((int64_t)a.batch * a.kv_heads * (D / 16 / tp_waves_v<NCH>()))),
+                     dim3(tp_waves_v<NCH>() * 64), (size_t)a.group * tp_lds_stride(NCH) * 2, st, a, ws, row_slots);
 }
 
 template <int D>

@@ -21,9 +21,13 @@
 // Workspace: scores bf16 [pairs][R][row_slots], row_slots = 512 (capacity <= 512) or 1024.
 
 constexpr int kTpWavesS = 4;  // waves per scores workgroup
-// waves per values workgroup: 8 (two workgroups per (b, kv head) at D = 256) halves the exact-probability
-// work every workgroup repeats for the pair's heads against 4 waves (E2B decode step 4.86 -> 4.73 ms)
-constexpr int kTpWavesV = 8;
+// Waves per values workgroup. Every workgroup forms the exact probabilities of the pair's heads for
+// itself, so fewer, larger workgroups repeat less of that work: 8 waves (two workgroups per (b, kv
+// head) at D = 256) for rows of up to 16 chunks, where the kernel holds 102 VGPRs (E2B decode step
+// 4.86 -> 4.73 ms against 4 waves); 4 waves for longer rows, whose 152+ VGPRs would leave one
+// 8-wave workgroup per CU.
+template <int NCH>
+constexpr int tp_waves_v() { return NCH <= 16 ? 8 : 4; }
 constexpr int kTpMaxSlots = 1024;
 
 __host__ __device__ inline int twopass_row_slots(int capacity) { return capacity <= 512 ? 512 : kTpMaxSlots; }
@@ -216,10 +220,11 @@ __device__ __forceinline__ bool tp_probabilities(const u32x4 (&sv)[NB], int hh, 
 // the R rows over the banks.
 __host__ __device__ constexpr int tp_lds_stride(int nch) { return nch * 32 + 32; }
 
-// grid: pairs x D / (16 kTpWavesV). NCH >= ceil(capacity / 32): V^T chunks held in registers.
+// grid: pairs x D / (16 tp_waves_v<NCH>()). NCH >= ceil(capacity / 32): V^T chunks held in registers.
 template <int D, int NCH>
-__global__ __launch_bounds__(kTpWavesV * 64) void decode_bf16_tp_values_kernel(G4DecodeArgs a, const uint16_t* ws,
+__global__ __launch_bounds__(tp_waves_v<NCH>() * 64) void decode_bf16_tp_values_kernel(G4DecodeArgs a, const uint16_t* ws,
                                                                               int row_slots) {
+  constexpr int kTpWavesV = tp_waves_v<NCH>();
   constexpr int kParts = D / 16 / kTpWavesV;  // workgroups per pair
   static_assert(kParts >= 1 && kParts * kTpWavesV * 16 == D, "one 16-row d-block of V^T per wave");
   constexpr int NB = (NCH + 15) / 16;  // 512-slot blocks of a score row
@@ -259,7 +264,7 @@ __global__ __launch_bounds__(kTpWavesV * 64) void decode_bf16_tp_values_kernel(G
   for (int c = 0; c < NCH; ++c)
     vv[c] = buffer_load16_nt(rv, c < n_chunks ? vt_operand_bytes(4 * c + grp, col, D) : pair_bytes, soff);
 
-  // exact probabilities: head w first; heads w + 8, w + 16, ... (R > 8) from rows loaded afterwards
+  // exact probabilities: head w first; heads w + kTpWavesV, ... (more heads than waves) from rows loaded afterwards
   const bool all_masked = tp_probabilities<NB>(sv, w, w < R, sp, kStride, NCH * 32, n_scanned, a.capacity, lane);
   for (int hh = w + kTpWavesV; hh < R; hh += kTpWavesV) {
     u32x4 sh[NB];
