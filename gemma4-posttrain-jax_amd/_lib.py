@@ -81,6 +81,16 @@ class G4SampleArgs(ctypes.Structure):
     ]
 
 
+class G4RolloutStepArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_int32), ("max_new", c_int32), ("step", c_int32), ("pad_id", c_int32), ("n_eos", c_int32),
+        ("id_bytes", c_int32), ("eos_ids", c_void_p), ("sampled", c_void_p), ("logp", c_void_p), ("active", c_void_p),
+        ("prompt_lengths", c_void_p), ("completion_ids", c_void_p), ("completion_mask", c_void_p),
+        ("rollout_logps", c_void_p), ("next_token", c_void_p), ("next_pos", c_void_p), ("next_mask", c_void_p),
+        ("any_active", c_void_p),
+    ]
+
+
 class G4LmHeadSampleArgs(ctypes.Structure):
     _fields_ = [
         ("batch", c_int32), ("vocab", c_int32), ("hidden", c_int32), ("x", c_void_p), ("embed", c_void_p),
@@ -127,6 +137,7 @@ PROTOTYPES = {
     "g4_residual_norm_splitk": (c_int32, [c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
                                           c_void_p, c_float, c_void_p, c_void_p, c_void_p]),
     "g4_decode_prologue": (c_int32, [POINTER(G4PrologueArgs), c_void_p]),
+    "g4_rollout_step": (c_int32, [POINTER(G4RolloutStepArgs), c_void_p]),
     "g4_linear_workspace_size": (c_size_t, [POINTER(G4LinearArgs)]),
     "g4_linear_bf16": (c_int32, [POINTER(G4LinearArgs), c_void_p]),
     "g4_convert_f32_to_bf16": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),

@@ -1,0 +1,57 @@
+// generate's per-step bookkeeping (g4_rollout_step, sampler.py:279-296): the masked token and
+// log-probability of the step's draw into the completion arrays, the EOS update of the active rows
+// and the next decode step's inputs, in one launch of one workgroup (one thread per row) instead
+// of a dozen framework kernels.
+#include "g4_common.h"
+#include "g4_internal.h"
+
+namespace g4 {
+namespace {
+
+constexpr int kRolloutThreads = 1024;
+
+// One workgroup; thread t takes rows t, t + 1024, ... (a rollout batch is a few hundred rows).
+__global__ __launch_bounds__(kRolloutThreads) void rollout_step_kernel(G4RolloutStepArgs a) {
+  bool stays_any = false;
+  for (int b = threadIdx.x; b < a.batch; b += blockDim.x) {
+    const bool act = a.active[b] != 0;                 // the step's mask
+    const int32_t tok = act ? a.sampled[b] : a.pad_id;  // finished rows emit pad
+    const int64_t at = (int64_t)b * a.max_new + a.step;
+    if (a.id_bytes == 8) reinterpret_cast<int64_t*>(a.completion_ids)[at] = tok;
+    else reinterpret_cast<int32_t*>(a.completion_ids)[at] = tok;
+    a.completion_mask[at] = act ? 1 : 0;
+    a.rollout_logps[at] = act ? a.logp[b] : 0.f;
+    bool eos = false;
+    for (int i = 0; i < a.n_eos; ++i) eos = eos || tok == a.eos_ids[i];
+    const bool stays = act && !eos;
+    stays_any = stays_any || stays;
+    if (a.next_token) a.next_token[b] = tok;
+    if (a.next_pos) a.next_pos[b] = a.prompt_lengths[b] + a.step;
+    if (a.next_mask) a.next_mask[b] = act ? 1 : 0;
+    a.active[b] = stays ? 1 : 0;
+  }
+  const int any = __syncthreads_or(stays_any ? 1 : 0);
+  if (threadIdx.x == 0 && a.any_active) *a.any_active = any ? 1 : 0;
+}
+
+}  // namespace
+}  // namespace g4
+
+extern "C" int g4_rollout_step(const G4RolloutStepArgs* args, void* stream) {
+  using namespace g4;
+  if (!args) return fail(G4_ERR_INVALID, "g4_rollout_step: args is NULL");
+  const G4RolloutStepArgs& a = *args;
+  if (a.batch <= 0) return fail(G4_ERR_INVALID, "g4_rollout_step: batch %d", a.batch);
+  if (a.max_new <= 0 || a.step < 0 || a.step >= a.max_new)
+    return fail(G4_ERR_INVALID, "g4_rollout_step: step %d outside [0, max_new = %d)", a.step, a.max_new);
+  if (a.id_bytes != 4 && a.id_bytes != 8) return fail(G4_ERR_INVALID, "g4_rollout_step: id_bytes %d", a.id_bytes);
+  if (a.n_eos < 0 || (a.n_eos > 0 && !a.eos_ids)) return fail(G4_ERR_INVALID, "g4_rollout_step: eos_ids / n_eos");
+  if (!a.sampled || !a.logp || !a.active || !a.completion_ids || !a.completion_mask || !a.rollout_logps ||
+      (a.next_pos && !a.prompt_lengths))
+    return fail(G4_ERR_INVALID, "g4_rollout_step: NULL pointer");
+  if (reinterpret_cast<uintptr_t>(a.completion_ids) % (uintptr_t)a.id_bytes)
+    return fail(G4_ERR_INVALID, "g4_rollout_step: completion_ids not %d-byte aligned", a.id_bytes);
+  const int threads = a.batch < kRolloutThreads ? (a.batch + 63) / 64 * 64 : kRolloutThreads;
+  hipLaunchKernelGGL(rollout_step_kernel, dim3(1), dim3(threads), 0, reinterpret_cast<hipStream_t>(stream), a);
+  return check_launch("g4_rollout_step");
+}

@@ -401,6 +401,59 @@ def sample_tokens(logits: torch.Tensor, *, softcap: float | None, temperature: f
     return token_out, logp_out
 
 
+def rollout_step(step: int, sampled: torch.Tensor, logp: torch.Tensor, active: torch.Tensor, *,
+                 completion_ids: torch.Tensor, completion_mask: torch.Tensor, rollout_logps: torch.Tensor,
+                 pad_id: int, eos_ids: torch.Tensor | None, prompt_lengths: torch.Tensor | None = None,
+                 next_token: torch.Tensor | None = None, next_pos: torch.Tensor | None = None,
+                 next_mask: torch.Tensor | None = None, any_active: torch.Tensor | None = None) -> None:
+    """g4_rollout_step: the bookkeeping of one generate step (sampler.py:279-296) in one launch.
+    Column ``step`` of ``completion_ids`` (int32/int64) / ``completion_mask`` (bool) /
+    ``rollout_logps`` (f32) receives the drawn token and logp of the rows in ``active`` (pad and 0
+    elsewhere); ``active`` (bool [B]) is cleared in place for rows whose token is in ``eos_ids``
+    (int32 [n]); ``next_token`` / ``next_pos`` / ``next_mask`` (int32 / int32 / bool [B], optional)
+    receive the next decode step's inputs (the token, ``prompt_lengths + step``, the mask before the
+    update) and ``any_active`` (bool [1], optional) whether a row stays active."""
+
+    B = sampled.shape[0]
+    dev = sampled.device
+    if B <= 0:
+        raise ValueError("rollout_step needs at least one row")
+    N = completion_ids.shape[1] if completion_ids.dim() == 2 else -1
+    if not 0 <= step < N:
+        raise ValueError(f"step {step} outside the completion width {N}")
+
+    def want(t, name, dtype, shape):
+        if t is not None and (t.dtype != dtype or tuple(t.shape) != shape or not t.is_contiguous() or t.device != dev):
+            raise ValueError(f"{name} must be a contiguous {dtype} tensor of shape {shape} on {dev}")
+
+    want(sampled, "sampled", torch.int32, (B,))
+    want(logp, "logp", torch.float32, (B,))
+    want(active, "active", torch.bool, (B,))
+    if completion_ids.dtype not in (torch.int32, torch.int64):
+        raise ValueError("completion_ids must be int32 or int64")
+    want(completion_ids, "completion_ids", completion_ids.dtype, (B, N))
+    want(completion_mask, "completion_mask", torch.bool, (B, N))
+    want(rollout_logps, "rollout_logps", torch.float32, (B, N))
+    want(prompt_lengths, "prompt_lengths", torch.int32, (B,))
+    want(next_token, "next_token", torch.int32, (B,))
+    want(next_pos, "next_pos", torch.int32, (B,))
+    want(next_mask, "next_mask", torch.bool, (B,))
+    want(any_active, "any_active", torch.bool, (1,))
+    n_eos = 0 if eos_ids is None else eos_ids.numel()
+    if n_eos:
+        want(eos_ids, "eos_ids", torch.int32, (n_eos,))
+    if next_pos is not None and prompt_lengths is None:
+        raise ValueError("next_pos needs prompt_lengths")
+    a = _lib.G4RolloutStepArgs(
+        batch=B, max_new=N, step=int(step), pad_id=int(pad_id), n_eos=n_eos, id_bytes=completion_ids.element_size(),
+        eos_ids=_ptr(eos_ids) if n_eos else None, sampled=_ptr(sampled), logp=_ptr(logp), active=_ptr(active),
+        prompt_lengths=_ptr(prompt_lengths), completion_ids=_ptr(completion_ids),
+        completion_mask=_ptr(completion_mask), rollout_logps=_ptr(rollout_logps), next_token=_ptr(next_token),
+        next_pos=_ptr(next_pos), next_mask=_ptr(next_mask), any_active=_ptr(any_active),
+    )
+    _lib.check(_lib.lib().g4_rollout_step(ctypes.byref(a), _stream()), "g4_rollout_step")
+
+
 def softcap(x: torch.Tensor, cap: float, *, out: torch.Tensor | None = None) -> torch.Tensor:
     """g4_softcap_bf16: ``bf16(tanh(x / cap) * cap)`` elementwise over a contiguous bf16 tensor (the
     f32 division, tanh and multiply of forward_lm_head's soft-cap); ``out`` may be ``x``."""

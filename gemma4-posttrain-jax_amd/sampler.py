@@ -212,6 +212,25 @@ class GraphedDecodeStep:
         self._replay(token_ids, position_ids, active)
         return self.token_out, self.logp_out
 
+    def replay_sample(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """``step_sample`` on the inputs already in ``tok`` / ``pos`` / ``active`` (written there by
+        the caller's own kernels, e.g. ``g4_rollout_step``)."""
+
+        if self.temperature is None:
+            raise RuntimeError("this step was captured without sampling: use replay_logits")
+        self.graph.replay()
+        self.length += 1
+        return self.token_out, self.logp_out
+
+    def replay_logits(self) -> torch.Tensor:
+        """``step`` on the inputs already in ``tok`` / ``pos`` / ``active``."""
+
+        if self.temperature is not None:
+            raise RuntimeError("this step was captured with fused sampling: use replay_sample")
+        self.graph.replay()
+        self.length += 1
+        return self.logits
+
     @property
     def kv_cache(self) -> KVCache:
         return self.cache._replace(length=self.length)
@@ -320,10 +339,13 @@ def generate(
     key_state = key_tensor(key, dev, sc.seed)  # the loop's key, split once per step on the device
     prompt_lengths = prompt_mask.sum(dim=-1, dtype=torch.int32)
     active = torch.ones(B, dtype=torch.bool, device=dev)
-    completion_ids = torch.full((B, N), config.pad_token_id, dtype=prompt_ids.dtype, device=dev)
+    ids_dtype = prompt_ids.dtype if prompt_ids.dtype in (torch.int32, torch.int64) else torch.int64
+    completion_ids = torch.full((B, N), config.pad_token_id, dtype=ids_dtype, device=dev)
     completion_mask = torch.zeros((B, N), dtype=torch.bool, device=dev)
     rollout_logps = torch.zeros((B, N), dtype=torch.float32, device=dev)
-    eos = torch.tensor(list(sc.eos_ids), dtype=torch.int64, device=dev)
+    # token ids are int32, so an EOS id outside that range never matches
+    eos = torch.tensor([e for e in sc.eos_ids if -2**31 <= e < 2**31], dtype=torch.int32, device=dev)
+    any_dev = torch.ones(1, dtype=torch.bool, device=dev)
     logits = out.logits[:, -1].float()
     cache = out.kv_cache
     fused = _fused_sampling(sc, config.vocab_size)
@@ -340,28 +362,30 @@ def generate(
         else:
             sampled, logp = _draw(logits, key_state, temperature=sc.temperature, top_k=sc.top_k, top_p=sc.top_p,
                                   split_key=True)
-        token = torch.where(active, sampled, torch.full_like(sampled, config.pad_token_id)).to(prompt_ids.dtype)
-        logp = torch.where(active, logp, torch.zeros_like(logp))
-        completion_ids[:, step] = token
-        completion_mask[:, step] = active
-        rollout_logps[:, step] = logp
-        if len(sc.eos_ids):
-            next_active = active & ~torch.isin(token.long(), eos)
-            any_active = bool(next_active.any())  # the only host sync per step (while_loop's cond)
-        else:  # without EOS ids no row finishes: the loop runs all N steps and never waits on the device
-            next_active, any_active = active, True
-        if step + 1 < N and any_active:
-            pos = (prompt_lengths + step).to(torch.int32)
+        decode_next = step + 1 < N
+        # the masked token / logp into column `step`, the EOS update of `active` and the next decode
+        # step's inputs (the token, prompt_lengths + step, this step's mask) written straight into
+        # the graph's input buffers
+        kernels.rollout_step(step, sampled, logp, active, completion_ids=completion_ids,
+                             completion_mask=completion_mask, rollout_logps=rollout_logps,
+                             pad_id=config.pad_token_id, eos_ids=eos, prompt_lengths=prompt_lengths,
+                             next_token=graphed.tok if decode_next else None,
+                             next_pos=graphed.pos if decode_next else None,
+                             next_mask=graphed.active if decode_next else None,
+                             any_active=any_dev if eos.numel() else None)
+        # with EOS ids, whether a row is still active is the only host sync per step (while_loop's
+        # cond); without them no row finishes and the loop never waits on the device
+        any_active = bool(any_dev.item()) if eos.numel() else True
+        if decode_next and any_active:
             if fused:
-                nxt = graphed.step_sample(token.to(torch.int32), pos, active)
+                nxt = graphed.replay_sample()
             else:
-                logits = graphed.step(token.to(torch.int32), pos, active)
-        active = next_active
+                logits = graphed.replay_logits()
         step += 1
         if not any_active:
             break
     lengths = completion_mask.sum(dim=-1, dtype=torch.int32)
-    return RolloutBatch(prompt_ids, completion_ids, completion_mask, rollout_logps, lengths)
+    return RolloutBatch(prompt_ids, completion_ids.to(prompt_ids.dtype), completion_mask, rollout_logps, lengths)
 
 
 class NativeRollout:

@@ -429,6 +429,42 @@ size_t g4_linear_workspace_size(const G4LinearArgs* args);
 int g4_linear_bf16(const G4LinearArgs* args, void* stream);
 
 /*
+ * One iteration of generate's loop body after the draw (sampler.py:279-296), for the batch rows of
+ * a rollout at step `step` (0 <= step < max_new):
+ *   token = active ? sampled : pad_id;  logp = active ? logp_in : 0
+ *   completion_ids[:, step] = token; completion_mask[:, step] = active; rollout_logps[:, step] = logp
+ *   active <- active && token is none of eos_ids
+ * and the inputs of the decode step that follows it (sampler.py:287-296): next_token = token,
+ * next_pos = prompt_lengths + step, next_mask = active before the update (the step's mask).
+ * *any_active is set to 1 when a row stays active, else 0 (while_loop's condition, sampler.py:267-
+ * 268). completion_ids are int32 (id_bytes 4) or int64 (id_bytes 8), the prompt ids' dtype; masks
+ * are one byte per row (0 / 1). batch >= 1. The next_* and any_active pointers may be NULL. One
+ * launch of one workgroup on `stream`; it allocates nothing.
+ */
+typedef struct G4RolloutStepArgs {
+  int32_t batch;
+  int32_t max_new;
+  int32_t step;
+  int32_t pad_id;
+  int32_t n_eos;
+  int32_t id_bytes;               /* 4 or 8 */
+  const int32_t* eos_ids;         /* device [n_eos] (NULL when n_eos = 0) */
+  const int32_t* sampled;         /* device [batch] */
+  const float* logp;              /* device [batch] */
+  uint8_t* active;                /* device [batch], updated in place */
+  const int32_t* prompt_lengths;  /* device [batch] (needed with next_pos) */
+  void* completion_ids;           /* device [batch, max_new] */
+  uint8_t* completion_mask;       /* device [batch, max_new] */
+  float* rollout_logps;           /* device [batch, max_new] */
+  int32_t* next_token;            /* device [batch] or NULL */
+  int32_t* next_pos;              /* device [batch] or NULL */
+  uint8_t* next_mask;             /* device [batch] or NULL */
+  uint8_t* any_active;            /* device [1] or NULL */
+} G4RolloutStepArgs;
+
+int g4_rollout_step(const G4RolloutStepArgs* args, void* stream);
+
+/*
  * Rollout weight handoff. g4_convert_f32_to_bf16: out[i] = bf16 bits of in[i], round to nearest
  * even on the raw bits, (bits + 0x7FFF + ((bits >> 16) & 1)) >> 16 — the conversion of
  * inference_device.py:10-45 (device_converter), equal to the astype(bfloat16) of

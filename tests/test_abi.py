@@ -45,7 +45,7 @@ def test_ctypes_structs_match_the_compiled_header(tmp_path):
         pytest.skip("no C compiler")
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for st in (_lib.G4AppendArgs, _lib.G4DecodeArgs, _lib.G4PrefillArgs, _lib.G4SampleArgs,
-               _lib.G4LmHeadSampleArgs, _lib.G4LinearArgs, _lib.G4PrologueArgs):
+               _lib.G4LmHeadSampleArgs, _lib.G4LinearArgs, _lib.G4PrologueArgs, _lib.G4RolloutStepArgs):
         lines.append(f'printf("{st.__name__} size %zu\\n", sizeof({st.__name__}));')
         for f, _ in st._fields_:
             lines.append(f'printf("{st.__name__} {f} %zu\\n", offsetof({st.__name__}, {f}));')
@@ -364,3 +364,30 @@ def test_convert_rejects_invalid_arguments():
     assert re.search("16-byte aligned", L.g4_last_error().decode())
     assert L.g4_convert_f32_to_bf16(None, None, 0, None, None) == _lib.G4_OK  # nothing to do
     assert L.g4_convert_bf16_to_f32(None, 16, 8, None) == _lib.G4_ERR_INVALID
+
+
+def _rollout_step_args(**kw):
+    base = dict(batch=4, max_new=8, step=0, pad_id=0, n_eos=1, id_bytes=4, eos_ids=16, sampled=16, logp=16,
+                active=16, prompt_lengths=16, completion_ids=16, completion_mask=16, rollout_logps=16,
+                next_token=16, next_pos=16, next_mask=16, any_active=16)
+    base.update(kw)
+    return _lib.G4RolloutStepArgs(**base)
+
+
+@pytest.mark.parametrize("override,match", [
+    (dict(batch=0), "batch 0"),
+    (dict(step=8), "step 8"),
+    (dict(step=-1), "step -1"),
+    (dict(max_new=0), "max_new = 0"),
+    (dict(id_bytes=2), "id_bytes 2"),
+    (dict(eos_ids=None), "eos_ids"),
+    (dict(n_eos=-1), "eos_ids"),
+    (dict(sampled=None), "NULL"),
+    (dict(prompt_lengths=None), "NULL"),
+    (dict(id_bytes=8, completion_ids=20), "8-byte aligned"),
+])
+def test_rollout_step_rejects_invalid_arguments(override, match):
+    a = _rollout_step_args(**override)
+    rc = _lib.lib().g4_rollout_step(ctypes.byref(a), None)
+    assert rc == _lib.G4_ERR_INVALID
+    assert re.search(match, _lib.lib().g4_last_error().decode())

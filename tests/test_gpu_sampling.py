@@ -184,3 +184,48 @@ def test_draws_over_long_rows_follow_the_jax_stream(device, scale):
     want_tok, want_logp = O.sample_token(x, temperature=1.0, key=sub)
     np.testing.assert_array_equal(tok.cpu().numpy(), want_tok)
     np.testing.assert_allclose(logp.cpu().numpy(), want_logp, rtol=0, atol=LOGP_ATOL)
+
+
+@pytest.mark.parametrize("B,ids_dtype", [(5, torch.int32), (300, torch.int64), (1500, torch.int32)])
+def test_rollout_step_bookkeeping(device, B, ids_dtype):
+    """g4_rollout_step over two steps against the loop body of sampler.py:279-296 stated with numpy:
+    finished rows emit pad with logp 0 and mask 0, the EOS test clears `active`, the next decode
+    inputs are (token, prompt_length + step, the step's mask); rows beyond 1024 take the kernel's
+    strided loop. A last call whose rows all hit EOS reports no active row."""
+
+    rng = np.random.default_rng(B)
+    N, pad, eos = 6, 7, np.array([3, 11, 2**20], np.int32)
+    ids = torch.full((B, N), pad, dtype=ids_dtype, device=device)
+    mask = torch.zeros((B, N), dtype=torch.bool, device=device)
+    logps = torch.zeros((B, N), dtype=torch.float32, device=device)
+    plen = torch.from_numpy(rng.integers(1, 50, B).astype(np.int32)).to(device)
+    act_np = rng.random(B) < 0.8
+    active = torch.from_numpy(act_np).to(device)
+    eos_t = torch.from_numpy(eos).to(device)
+    nt, npos = torch.full((B,), -1, dtype=torch.int32, device=device), torch.full((B,), -1, dtype=torch.int32, device=device)
+    nmask, anyd = torch.zeros(B, dtype=torch.bool, device=device), torch.zeros(1, dtype=torch.bool, device=device)
+    want_ids, want_mask = np.full((B, N), pad, np.int64), np.zeros((B, N), bool)
+    want_lp = np.zeros((B, N), np.float32)
+    for step in (0, 1):
+        tok = rng.integers(0, 16, B).astype(np.int32)
+        lp = -rng.random(B).astype(np.float32)
+        kernels.rollout_step(step, torch.from_numpy(tok).to(device), torch.from_numpy(lp).to(device), active,
+                             completion_ids=ids, completion_mask=mask, rollout_logps=logps, pad_id=pad, eos_ids=eos_t,
+                             prompt_lengths=plen, next_token=nt, next_pos=npos, next_mask=nmask, any_active=anyd)
+        token = np.where(act_np, tok, pad)
+        want_ids[:, step], want_mask[:, step], want_lp[:, step] = token, act_np, np.where(act_np, lp, 0)
+        np.testing.assert_array_equal(nt.cpu().numpy(), token)
+        np.testing.assert_array_equal(npos.cpu().numpy(), plen.cpu().numpy() + step)
+        np.testing.assert_array_equal(nmask.cpu().numpy(), act_np)
+        act_np = act_np & ~np.isin(token, eos)
+        np.testing.assert_array_equal(active.cpu().numpy(), act_np)
+        assert bool(anyd.item()) == bool(act_np.any())
+    np.testing.assert_array_equal(ids.cpu().numpy(), want_ids)
+    np.testing.assert_array_equal(mask.cpu().numpy(), want_mask)
+    np.testing.assert_array_equal(logps.cpu().numpy(), want_lp)  # copied, not computed: exact
+    # every remaining row draws an EOS id: nothing stays active
+    kernels.rollout_step(2, torch.full((B,), 11, dtype=torch.int32, device=device), torch.zeros(B, device=device),
+                         active, completion_ids=ids, completion_mask=mask, rollout_logps=logps, pad_id=pad,
+                         eos_ids=eos_t, any_active=anyd)
+    assert not bool(anyd.item()) and not bool(active.any())
+    np.testing.assert_array_equal(mask[:, 2].cpu().numpy(), act_np)
