@@ -195,11 +195,12 @@ namespace {
 
 // Whether the call takes the split-K path (bf16, head dims 128/256, rows longer than one split).
 bool use_split_keys(const G4DecodeArgs& a) {
-  if (a.dtype != G4_DTYPE_BF16 || (a.head_dim != 128 && a.head_dim != 256)) return false;
+  if (a.dtype != G4_DTYPE_BF16 || (a.head_dim != 128 && a.head_dim != 256 && a.head_dim != 512)) return false;
   const int t_alloc = (a.capacity + 31) / 32 * 32;
   if (t_alloc <= kSplitSlots) return false;
   if (a.num_splits == G4_DECODE_SPLIT_KEYS) return true;
   if (a.num_splits != 0) return false;
+  if (a.head_dim == 512) return true;  // no one-launch kernel at this head dim (rows beyond the two-launch path's)
   const int64_t npairs = (int64_t)a.batch * a.kv_heads;
   return npairs < 256 || fast_lds_bytes(a.group, a.head_dim, t_alloc) > kMaxLdsFast;
 }
@@ -231,13 +232,16 @@ int launch_split_keys(const G4DecodeArgs& a, hipStream_t st) {
 constexpr int64_t kTwoPassMinPairs = 256;
 
 bool two_pass_applies(const G4DecodeArgs& a) {
-  return a.dtype == G4_DTYPE_BF16 && (a.head_dim == 128 || a.head_dim == 256) && a.capacity <= kTpMaxSlots;
+  return a.dtype == G4_DTYPE_BF16 && (a.head_dim == 128 || a.head_dim == 256 || a.head_dim == 512) &&
+         a.capacity <= kTpMaxSlots;
 }
 
+// Head dim 512 (the reference's default global head dim) has no one-launch kernel: its rows take
+// the two-launch path up to 1024 slots and the split-K path beyond, whatever the pair count.
 bool use_two_pass(const G4DecodeArgs& a) {
   if (!two_pass_applies(a)) return false;
   if (a.num_splits == G4_DECODE_TWO_PASS || a.prep) return true;  // only this path fuses the preparation
-  return a.num_splits == 0 && (int64_t)a.batch * a.kv_heads >= kTwoPassMinPairs;
+  return a.num_splits == 0 && (a.head_dim == 512 || (int64_t)a.batch * a.kv_heads >= kTwoPassMinPairs);
 }
 
 template <int D, int NCH>
@@ -305,8 +309,10 @@ int setup_decode_kernels(int device) {
       {(const void*)decode_bf16_fast_kernel<256, 1, false>, (int)kMaxLdsFast},
       {(const void*)decode_bf16_splitk_scores_kernel<128>, stage},
       {(const void*)decode_bf16_splitk_scores_kernel<256>, stage},
+      {(const void*)decode_bf16_splitk_scores_kernel<512>, stage},
       {(const void*)decode_bf16_splitk_values_kernel<128>, stage},
       {(const void*)decode_bf16_splitk_values_kernel<256>, stage},
+      {(const void*)decode_bf16_splitk_values_kernel<512>, stage},
   };
   for (const auto& k : kernels)
     if (hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize, k.bytes) != hipSuccess)
@@ -351,7 +357,7 @@ int validate_decode_args(const G4DecodeArgs& a) {
     const G4DecodePrep& p = *a.prep;
     if (!two_pass_applies(a) || a.num_splits == G4_DECODE_SPLIT_KEYS || a.num_splits > 0)
       return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: fused preparation needs the two-launch path (bf16, head_dim "
-                  "128/256, capacity <= %d, num_splits 0 or G4_DECODE_TWO_PASS)", kTpMaxSlots);
+                  "128/256/512, capacity <= %d, num_splits 0 or G4_DECODE_TWO_PASS)", kTpMaxSlots);
     if (a.new_k || a.new_v) return fail(G4_ERR_INVALID, "g4_decode_attention: prep replaces new_k / new_v");
     if (!p.q_raw || (p.k_raw == nullptr) != (p.v_raw == nullptr) || (p.k_raw && !a.cache_k_w))
       return fail(G4_ERR_INVALID, "g4_decode_attention: prep needs q_raw, k_raw with v_raw, and cache_k_w to append");
@@ -374,10 +380,13 @@ int validate_decode_args(const G4DecodeArgs& a) {
   if (a.num_splits < G4_DECODE_TWO_PASS || a.num_splits > 2)
     return fail(G4_ERR_INVALID, "g4_decode_attention: num_splits %d", a.num_splits);
   if (a.num_splits == G4_DECODE_TWO_PASS && !two_pass_applies(a))
-    return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: two-pass needs bf16, head_dim 128/256, capacity <= %d",
+    return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: two-pass needs bf16, head_dim 128/256/512, capacity <= %d",
                 kTpMaxSlots);
-  if (a.dtype == G4_DTYPE_BF16 && a.head_dim > 256)
-    return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: bf16 head_dim %d (bf16 decode covers 32..256)", a.head_dim);
+  if (a.dtype == G4_DTYPE_BF16 && a.head_dim == 512 && a.num_splits > 0)
+    return fail(G4_ERR_UNSUPPORTED,
+                "g4_decode_attention: bf16 head_dim 512 takes num_splits 0, G4_DECODE_TWO_PASS or G4_DECODE_SPLIT_KEYS");
+  if (a.dtype == G4_DTYPE_BF16 && a.head_dim < 32)
+    return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: bf16 head_dim %d (bf16 decode covers 32..512)", a.head_dim);
   return G4_OK;
 }
 
@@ -399,7 +408,9 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
     if (!a.workspace || a.workspace_bytes < need)
       return fail(G4_ERR_WORKSPACE, "g4_decode_attention: two-pass needs %zu B of workspace (have %zu)", need,
                   a.workspace ? a.workspace_bytes : (size_t)0);
-    const int rc = a.head_dim == 256 ? launch_two_pass<256>(a, st) : launch_two_pass<128>(a, st);
+    const int rc = a.head_dim == 512   ? launch_two_pass<512>(a, st)
+                   : a.head_dim == 256 ? launch_two_pass<256>(a, st)
+                                       : launch_two_pass<128>(a, st);
     if (rc != G4_OK) return rc;
     return check_launch("g4_decode_attention");
   }
@@ -408,12 +419,14 @@ extern "C" int g4_decode_attention(const G4DecodeArgs* args, void* stream) {
     if (!a.workspace || a.workspace_bytes < need)
       return fail(G4_ERR_WORKSPACE, "g4_decode_attention: split-K needs %zu B of workspace (have %zu)", need,
                   a.workspace ? a.workspace_bytes : (size_t)0);
-    const int rc = a.head_dim == 256 ? launch_split_keys<256>(a, st) : launch_split_keys<128>(a, st);
+    const int rc = a.head_dim == 512   ? launch_split_keys<512>(a, st)
+                   : a.head_dim == 256 ? launch_split_keys<256>(a, st)
+                                       : launch_split_keys<128>(a, st);
     if (rc != G4_OK) return rc;
     return check_launch("g4_decode_attention");
   }
   if (a.num_splits == G4_DECODE_SPLIT_KEYS)
-    return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: split-K needs bf16, head_dim 128/256, capacity > %d",
+    return fail(G4_ERR_UNSUPPORTED, "g4_decode_attention: split-K needs bf16, head_dim 128/256/512, capacity > %d",
                 kSplitSlots);
   if (a.dtype == G4_DTYPE_BF16) {
     if (a.head_dim == 128 || a.head_dim == 256) {

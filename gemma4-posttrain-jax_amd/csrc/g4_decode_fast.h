@@ -101,6 +101,42 @@ __device__ __forceinline__ float score_to_lds(const u32x4 (&kv)[2][D / 32], cons
   return mx;
 }
 
+// score_to_lds with the q operand read from LDS ([R][D] bf16) one 32-dim slice at a time
+// (inline-assembly reads, each waited for right before its two MFMAs), so the whole operand is
+// never held in registers
+template <int D>
+__device__ __forceinline__ float score_to_lds_qlds(const u32x4 (&kv)[2][D / 32], const uint16_t* q_lds, uint64_t vbits,
+                                                   uint16_t* sp, int t_alloc, int c0, int R, int col, int grp,
+                                                   float mx) {
+  floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  const uint32_t qa = lds_addr(q_lds + (col < R ? col : 0) * D + 8 * grp);
+  u32x4 q0 = lds_read16(qa), q1 = lds_read16(qa + 64u);
+#pragma unroll
+  for (int s = 0; s < D / 32; ++s) {
+    u32x4& q = (s & 1) ? q1 : q0;
+    lgkm_wait(s + 1 < D / 32 ? 1 : 0, q);
+    if (col >= R) q = u32x4{0u, 0u, 0u, 0u};
+    acc0 = mfma16x16x32(as_bf16x8(kv[0][s]), as_bf16x8(q), acc0);
+    acc1 = mfma16x16x32(as_bf16x8(kv[1][s]), as_bf16x8(q), acc1);
+    if (s + 2 < D / 32) q = lds_read16(qa + 64u * (s + 2));
+  }
+  uint32_t h[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int k0 = 8 * grp + j, k1 = k0 + 4;
+    const float s0 = ((vbits >> k0) & 1ull) ? round_bf16(acc0[j]) : kBf16Min;
+    const float s1 = ((vbits >> k1) & 1ull) ? round_bf16(acc1[j]) : kBf16Min;
+    mx = fmaxf(mx, fmaxf(s0, s1));
+    h[j] = f32_to_bf16_bits(s0);
+    h[4 + j] = f32_to_bf16_bits(s1);
+  }
+  if (col < R) {
+    const u32x4 word = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    *reinterpret_cast<u32x4*>(sp + col * t_alloc + c0 + 8 * grp) = word;
+  }
+  return mx;
+}
+
 // V^T operands of chunks [8g, 8g + 8) for d-blocks dblock0 .. dblock0 + DPW - 1.
 // (value dims 16 (dblock0 + ii) + col, slots 32 c + 8 grp .. + 7: operand group 4 c + grp)
 template <int DPW>

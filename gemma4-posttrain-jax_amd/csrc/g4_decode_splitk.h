@@ -45,6 +45,8 @@ template <int D>
 __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_scores_kernel(G4DecodeArgs a,
                                                                                        SplitKWorkspace ws) {
   __shared__ __attribute__((aligned(16))) uint16_t nk_lds[D];
+  // D = 512: the q rows [R][D] in LDS, read one 32-dim slice at a time (register budget)
+  __shared__ __attribute__((aligned(16))) uint16_t q_lds[D > 256 ? 16 * D : 1];
   extern __shared__ float smem[];
   const int R = a.group;
   uint16_t* sp = reinterpret_cast<uint16_t*>(smem);                // [R][stride] scores of the split
@@ -68,31 +70,58 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_scores_k
   u32x4 nkv = {0u, 0u, 0u, 0u};
   if (owner && lane < D / 8) nkv = load16(reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D + 8 * lane);
   bf16x8 qop[D / 32];
+  u32x4 qv[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};  // D = 512: thread t's q pieces t, t + 512
+  const uint16_t* qg = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)pair * R * D;
+  if constexpr (D <= 256) {
 #pragma unroll
-  for (int s = 0; s < D / 32; ++s) qop[s] = q_operand_global(a, pair, R, D, col, grp, s);
+    for (int s = 0; s < D / 32; ++s) qop[s] = q_operand_global(a, pair, R, D, col, grp, s);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      if (tid + 512 * j < R * D / 8) qv[j] = load16(qg + 8 * (tid + 512 * j));
+  }
   const int cc0 = cbase + w, cc1 = cbase + w + NW;  // this wave's chunks
   const int c0 = cc0 << 5, c1 = cc1 << 5;
   uint8_t mb0, mb1;
   const bool ok0 = slot_valid_flat(a, b, kr, c0 + (lane & 31), mb0);
   const bool ok1 = slot_valid_flat(a, b, kr, c1 + (lane & 31), mb1);
   __builtin_amdgcn_sched_barrier(0);
+  // both chunks' K in registers at once up to D = 256; at D = 512 (128 registers per chunk) the
+  // second chunk is loaded into the first one's registers after they are scored
+  constexpr bool kBothChunks = D <= 256;
   u32x4 k0[2][D / 32], k1[2][D / 32];
   load_k_chunk<D, true>(k0, rk, c0, col, grp);
-  load_k_chunk<D, true>(k1, rk, c1, col, grp);
+  if constexpr (kBothChunks) load_k_chunk<D, true>(k1, rk, c1, col, grp);
   __builtin_amdgcn_sched_barrier(0);
   if (owner && lane < D / 8) reinterpret_cast<u32x4*>(nk_lds)[lane] = nkv;  // read back by this wave only
   const uint64_t vb0 = __ballot(ok0 && mb0 != 0);
   const uint64_t vb1 = __ballot(ok1 && mb1 != 0);
+  if constexpr (D > 256) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      if (tid + 512 * j < R * D / 8) reinterpret_cast<u32x4*>(q_lds)[tid + 512 * j] = qv[j];
+    __syncthreads();  // q rows in LDS
+  }
+  auto score = [&](const u32x4(&kv)[2][D / 32], uint64_t vbits, int local, float m) {
+    if constexpr (D <= 256)
+      return score_to_lds<D>(kv, qop, vbits, sp, kStageStride, local, R, col, grp, m);
+    else
+      return score_to_lds_qlds<D>(kv, q_lds, vbits, sp, kStageStride, local, R, col, grp, m);
+  };
 
   // scores of the split at local slots [0, 512): chunk cc at local offset 32 * (cc - cbase)
   float mx = kBf16Min;
   if (cc0 < n_chunks) {
     patch_k_sel<D>(k0, nk_lds, kr.new_slot, c0, col, grp);
-    mx = score_to_lds<D>(k0, qop, vb0, sp, kStageStride, 32 * w, R, col, grp, mx);
+    mx = score(k0, vb0, 32 * w, mx);
   }
+  if constexpr (!kBothChunks) {
+    if (cc1 < n_chunks) load_k_chunk<D, true>(k0, rk, c1, col, grp);
+  }
+  u32x4(&kc1)[2][D / 32] = kBothChunks ? k1 : k0;
   if (cc1 < n_chunks) {
-    patch_k_sel<D>(k1, nk_lds, kr.new_slot, c1, col, grp);
-    mx = score_to_lds<D>(k1, qop, vb1, sp, kStageStride, 32 * (w + NW), R, col, grp, mx);
+    patch_k_sel<D>(kc1, nk_lds, kr.new_slot, c1, col, grp);
+    mx = score(kc1, vb1, 32 * (w + NW), mx);
   }
   mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
   mx = fmaxf(mx, __shfl_xor(mx, 32, 64));

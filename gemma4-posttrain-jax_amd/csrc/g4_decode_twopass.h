@@ -46,42 +46,11 @@ __host__ __device__ inline size_t twopass_workspace_bytes(int npairs, int R, int
 // and stored to the cache) and the new V row (stored as the V^T column the values launch reads).
 // The K chunk is requested before any of this, so the preparation runs while it is in flight.
 
-// score_to_lds with the q operand read from LDS one 32-dim slice at a time (inline-assembly reads,
-// each waited for right before its two MFMAs), so the whole operand is never held in registers
-template <int D>
-__device__ __forceinline__ void score_to_lds_qlds(const u32x4 (&kv)[2][D / 32], const uint16_t* q_lds, uint64_t vbits,
-                                                  uint16_t* sp, int t_alloc, int c0, int R, int col, int grp) {
-  floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  const uint32_t qa = lds_addr(q_lds + (col < R ? col : 0) * D + 8 * grp);
-  u32x4 q0 = lds_read16(qa), q1 = lds_read16(qa + 64u);
-#pragma unroll
-  for (int s = 0; s < D / 32; ++s) {
-    u32x4& q = (s & 1) ? q1 : q0;
-    lgkm_wait(s + 1 < D / 32 ? 1 : 0, q);
-    if (col >= R) q = u32x4{0u, 0u, 0u, 0u};
-    acc0 = mfma16x16x32(as_bf16x8(kv[0][s]), as_bf16x8(q), acc0);
-    acc1 = mfma16x16x32(as_bf16x8(kv[1][s]), as_bf16x8(q), acc1);
-    if (s + 2 < D / 32) q = lds_read16(qa + 64u * (s + 2));
-  }
-  uint32_t h[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int k0 = 8 * grp + j, k1 = k0 + 4;
-    const float s0 = ((vbits >> k0) & 1ull) ? round_bf16(acc0[j]) : kBf16Min;
-    const float s1 = ((vbits >> k1) & 1ull) ? round_bf16(acc1[j]) : kBf16Min;
-    h[j] = f32_to_bf16_bits(s0);
-    h[4 + j] = f32_to_bf16_bits(s1);
-  }
-  if (col < R) {
-    const u32x4 word = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-    *reinterpret_cast<u32x4*>(sp + col * t_alloc + c0 + 8 * grp) = word;
-  }
-}
-
 // PREP: at most 128 registers (4 waves per SIMD; the q operand is read from LDS slice by slice, so
-// nothing spills: E2B decode step 4.76 -> 4.72 ms against 3 waves per SIMD)
+// nothing spills: E2B decode step 4.76 -> 4.72 ms against 3 waves per SIMD). Head dim 512 holds
+// 128 registers of K alone, so it takes no occupancy bound.
 template <int D, bool PREP>
-__global__ __launch_bounds__(kTpWavesS * 64, PREP ? 4 : 1) void decode_bf16_tp_scores_kernel(G4DecodeArgs a, uint16_t* ws,
+__global__ __launch_bounds__(kTpWavesS * 64, (PREP && D <= 256) ? 4 : 1) void decode_bf16_tp_scores_kernel(G4DecodeArgs a, uint16_t* ws,
                                                                               int parts, int row_slots,
                                                                               G4DecodePrep pp) {
   constexpr int PER = D / 64;
@@ -167,7 +136,8 @@ __global__ __launch_bounds__(kTpWavesS * 64, PREP ? 4 : 1) void decode_bf16_tp_s
     const uint64_t vbits = __ballot(ok && mb != 0);
     if (writer && (!PREP || pp.k_raw)) patch_k_sel<D>(kv, nk, kr.new_slot, chunk << 5, col, grp);
     if constexpr (PREP)
-      score_to_lds_qlds<D>(kv, q_lds, vbits, ws + (int64_t)pair * R * row_slots, row_slots, chunk << 5, R, col, grp);
+      score_to_lds_qlds<D>(kv, q_lds, vbits, ws + (int64_t)pair * R * row_slots, row_slots, chunk << 5, R, col, grp,
+                           kBf16Min);
     else
       score_to_lds<D>(kv, qop, vbits, ws + (int64_t)pair * R * row_slots, row_slots, chunk << 5, R, col, grp,
                       kBf16Min);

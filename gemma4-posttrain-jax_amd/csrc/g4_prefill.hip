@@ -260,8 +260,8 @@ extern "C" int g4_prefill_attention(const G4PrefillArgs* args, void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (a.dtype == G4_DTYPE_BF16) {
     if (16 % a.group) return fail(G4_ERR_UNSUPPORTED, "g4_prefill_attention: bf16 needs group dividing 16");
-    if (a.head_dim > 256)
-      return fail(G4_ERR_UNSUPPORTED, "g4_prefill_attention: bf16 head_dim %d (bf16 prefill covers 32..256)",
+    if (a.head_dim < 32)
+      return fail(G4_ERR_UNSUPPORTED, "g4_prefill_attention: bf16 head_dim %d (bf16 prefill covers 32..512)",
                   a.head_dim);
     int dev = 0;
     const int rc = device_setup(&dev);
@@ -283,6 +283,7 @@ extern "C" int g4_prefill_attention(const G4PrefillArgs* args, void* stream) {
       case 64: hipLaunchKernelGGL(prefill_bf16_kernel<64>, grid, block, 0, st, a); break;
       case 128: hipLaunchKernelGGL(prefill_bf16_kernel<128>, grid, block, 0, st, a); break;
       case 256: hipLaunchKernelGGL(prefill_bf16_kernel<256>, grid, block, 0, st, a); break;
+      case 512: hipLaunchKernelGGL(prefill_bf16_kernel<512>, grid, block, 0, st, a); break;
       default: return fail(G4_ERR_UNSUPPORTED, "g4_prefill_attention: bf16 head_dim %d", a.head_dim);
     }
   } else {

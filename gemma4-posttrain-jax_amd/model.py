@@ -171,10 +171,6 @@ def pack_weights(params: Gemma4TextParams, config: Gemma4TextConfig) -> PackedWe
     for i, lp in enumerate(params.layers):
         a = lp.attention
         M, R, H, D = a.q_proj.shape
-        if params.embed_tokens.dtype == torch.bfloat16 and D > 256:
-            raise ValueError(
-                f"layer {i}: head dim {D} with bf16 parameters is not supported by the native kernels (bf16 "
-                "attention covers head dims 32..256); set global_head_dim <= 256 or run the layer in float32")
         wq = a.q_proj.permute(0, 2, 1, 3).reshape(M, H * R * D)
         parts = [wq]
         has_k = a.k_proj is not None
@@ -215,9 +211,9 @@ def _split_down(act: torch.Tensor, w_t: torch.Tensor) -> bool:
 def _fused_decode_prep(x: torch.Tensor, pairs: int, head_dim: int, cache) -> bool:
     """Whether a decode layer's q/k/v preparation and append run inside the two-launch attention
     (G4DecodePrep): the path the library takes at the rollout batch (>= 256 (b, kv head) pairs,
-    rows of at most 1024 slots, head dims 128 / 256, bf16)."""
+    rows of at most 1024 slots, head dims 128 / 256 / 512, bf16)."""
 
-    return (x.dtype == torch.bfloat16 and pairs >= 256 and head_dim in (128, 256) and cache is not None
+    return (x.dtype == torch.bfloat16 and pairs >= 256 and head_dim in (128, 256, 512) and cache is not None
             and cache.capacity <= 1024)
 
 

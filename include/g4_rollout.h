@@ -160,7 +160,7 @@ typedef struct G4DecodeArgs {
   int32_t batch;
   int32_t kv_heads;
   int32_t group;        /* R <= 16 */
-  int32_t head_dim;     /* bf16: 32, 64, 128 or 256; f32: 8 .. 512 */
+  int32_t head_dim;     /* bf16: 32, 64, 128, 256 or 512; f32: 8 .. 512 */
   int32_t capacity;     /* C or Wc */
   int32_t slot_stride;
   int32_t window;       /* sliding window W (ring caches); ignored for linear */
@@ -179,22 +179,23 @@ typedef struct G4DecodeArgs {
   size_t workspace_bytes;
   const G4DecodePrep* prep; /* optional (NULL: q / new_k / new_v are prepared); needs the two-launch path */
   int32_t num_splits;   /* 0 = choose automatically; 1 or 2 = workgroups per (b, kv head), one
-                           pass, each owning a slice of the head dim (2: head dim 256);
-                           G4_DECODE_SPLIT_KEYS = split the key range (bf16, head dims 128/256);
+                           pass, each owning a slice of the head dim (2: head dim 256; not
+                           at head dim 512, which always takes one of the two modes below);
+                           G4_DECODE_SPLIT_KEYS = split the key range (bf16, head dims 128/256/512);
                            G4_DECODE_TWO_PASS = scores and values in two launches (rows <= 1024) */
 } G4DecodeArgs;
 
 /* num_splits value: split-K over 512-slot key ranges in three launches (scores, values,
  * combine), for long rows over few (b, kv head) pairs. Uses the workspace. The automatic
  * choice takes it for bf16 rows longer than 512 slots when B * Hkv < 256 or when a one-pass
- * row does not fit in LDS. */
+ * row does not fit in LDS, and at head dim 512 for every row beyond the two-launch path's. */
 #define G4_DECODE_SPLIT_KEYS (-1)
 
 /* num_splits value: two stream-ordered launches for rows of at most 1024 slots (bf16, head dims
- * 128/256): the first scores K chunk by chunk into the workspace, the second forms the exact
+ * 128/256/512): the first scores K chunk by chunk into the workspace, the second forms the exact
  * probabilities and runs the value product, one wave per 16-row block of V^T. Uses the
  * workspace (bf16 scores [B * Hkv][R][512 or 1024]). The automatic choice takes it for such rows
- * when B * Hkv >= 256. */
+ * when B * Hkv >= 256, and at head dim 512 always. */
 #define G4_DECODE_TWO_PASS (-2)
 
 /* Bytes of workspace the call described by args needs (0 when the chosen path uses none). The
@@ -231,7 +232,7 @@ typedef struct G4PrefillArgs {
   int32_t seq;          /* S (queries = keys) */
   int32_t kv_heads;
   int32_t group;        /* R (bf16: a divisor of 16) */
-  int32_t head_dim;     /* bf16: 32, 64, 128 or 256; f32: 8 .. 512 */
+  int32_t head_dim;     /* bf16: 32, 64, 128, 256 or 512; f32: 8 .. 512 */
   int32_t window;       /* 0 = global (causal only) */
   const uint8_t* key_mask;   /* [B, key_mask_stride] */
   int32_t key_mask_stride;

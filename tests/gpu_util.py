@@ -105,6 +105,19 @@ def bf16_spacing(a: np.ndarray) -> np.ndarray:
     return np.where(mag > 0, 2.0 ** (np.floor(np.log2(np.maximum(mag, 2.0 ** -126))) - 7), 2.0 ** -133)
 
 
+def cache_rows_error(got: np.ndarray, want: np.ndarray) -> float:
+    """Model-level check of a written bf16 cache ([..., D] head rows) whose layer input came from
+    the device's own earlier layers: the largest |got - want| of each row divided by max(1, the
+    row's largest |want|), maximised over the rows (compare with the max-abs bar). K rows of a
+    512-wide head reach ~4, where one bf16 step (1/32) already exceeds 2e-2, and a last-bit
+    difference of the layer input moves an element by a step or two of its row's largest terms
+    through the norm and the rotation (x cos - y sin cancels)."""
+
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    scale = np.maximum(1.0, np.abs(want).max(axis=-1))
+    return float((np.abs(got - want).max(axis=-1) / scale).max())
+
+
 def ulp_stats(got: np.ndarray, want: np.ndarray, floor_frac: float = 0.125) -> tuple[float, float]:
     """(fraction of bit-equal elements, largest difference in bf16 ulps). An element's ulp is taken
     at its own magnitude, but not below ``floor_frac`` of the array's RMS: a value that results

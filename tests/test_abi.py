@@ -192,6 +192,28 @@ def test_decode_two_pass_workspace():
     assert L.g4_decode_attention(ctypes.byref(a), None) == _lib.G4_ERR_WORKSPACE
 
 
+
+def test_decode_head_dim_512_paths():
+    """bf16 head dim 512 (the reference's default global head dim, model.py:66) has no one-launch
+    kernel: rows of up to 1024 slots take the two-launch path at any pair count, longer rows the
+    split-K path, and a one-pass split count is refused."""
+
+    L = _lib.lib()
+    a = _decode_args(head_dim=512, batch=1)  # 2 pairs, 512-slot ring
+    assert L.g4_decode_workspace_size(ctypes.byref(a)) == 2 * 4 * 512 * 2
+    linear = dict(kind=_lib.G4_CACHE_LINEAR, capacity=1000, slot_stride=1024, key_mask_stride=1024)
+    assert L.g4_decode_workspace_size(ctypes.byref(_decode_args(head_dim=512, batch=1, **linear))) == 2 * 4 * 1024 * 2
+    # 1040 slots: 3 splits of 512, scores + statistics + f32 partials of the 512 value dims
+    long_rows = dict(kind=_lib.G4_CACHE_LINEAR, capacity=1040, slot_stride=1088, key_mask_stride=1088)
+    splits = 3
+    want = 2 * 4 * splits * 512 * 2 + 2 * splits * 4 * 2 * 4 + 2 * splits * 4 * 512 * 4
+    assert L.g4_decode_workspace_size(ctypes.byref(_decode_args(head_dim=512, batch=1, **long_rows))) == want
+    for n in (1, 2):
+        assert L.g4_decode_attention(ctypes.byref(_decode_args(head_dim=512, num_splits=n)), None) == \
+            _lib.G4_ERR_UNSUPPORTED
+        assert re.search("head_dim 512 takes num_splits", L.g4_last_error().decode())
+
+
 def _linear_args(**kw):
     base = dict(x=16, w=16, y=16, m=256, n=2048, k=8192, ldy=2048, ksplit=1, workspace=None, workspace_bytes=0,
                 epilogue=_lib.G4_LINEAR_PLAIN)

@@ -25,7 +25,9 @@ FLAGS_KV = _lib.G4_APPEND_NORM_K | _lib.G4_APPEND_ROPE_K | _lib.G4_APPEND_NORM_V
     # R != 4: waves with no q head of their own (R < 4) and the loop over heads w + 4.. (R > 4), at
     # and beyond 256 (b, kv head) pairs
     (128, 2, 1, 256, True, 512, False), (64, 4, 2, 256, False, 768, False), (128, 2, 8, 256, True, 512, False),
-    (128, 2, 8, 128, True, 512, True), (32, 8, 16, 128, False, 600, False), (8, 2, 16, 256, True, 512, False)])
+    (128, 2, 8, 128, True, 512, True), (32, 8, 16, 128, False, 600, False), (8, 2, 16, 256, True, 512, False),
+    # head dim 512 (the reference's default global head dim)
+    (128, 2, 4, 512, False, 768, False), (8, 2, 8, 512, True, 512, False), (16, 2, 4, 512, False, 300, True)])
 def test_decode_fused_prep_matches_append_then_attention(device, B, H, R, D, ring, cap, shared):
     W = 512 if ring else 0
     g = torch.Generator(device="cuda").manual_seed(B + cap + shared + 100 * R)

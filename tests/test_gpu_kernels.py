@@ -78,12 +78,13 @@ def test_append_fused_rope_is_bit_exact(device, dtype, D):
     np.testing.assert_array_equal(np_bits(gv, dtype), np_bits(ref.value, dtype))
 
 
-@pytest.mark.parametrize("dtype", [O.BF16, O.F32])
-def test_append_with_norms_and_q_matches_oracle(device, dtype):
-    """q/k norm + RoPE, unscaled v norm, prefill chunk outputs (model.py:463-482)."""
+@pytest.mark.parametrize("dtype,D", [(O.BF16, 128), (O.F32, 128), (O.BF16, 512)])
+def test_append_with_norms_and_q_matches_oracle(device, dtype, D):
+    """q/k norm + RoPE, unscaled v norm, prefill chunk outputs (model.py:463-482); also at head dim
+    512 (the reference's default global head dim)."""
 
     rng = np.random.default_rng(3)
-    B, S, H, R, D, cap = 2, 9, 2, 4, 128, 64
+    B, S, H, R, cap = 2, 9, 2, 4, 64
     width = (H * R + 2 * H) * D
     rows = _rand(rng, (B, S, width), dtype)
     qn, kn = O.cast(1 + 0.3 * rng.standard_normal(D), dtype), O.cast(1 + 0.3 * rng.standard_normal(D), dtype)
@@ -205,7 +206,7 @@ def test_decode_e2b_batch(device, ring, cap, num_splits):
                  key_mask=key_mask, fused=True, seed=26, num_splits=num_splits)
 
 
-@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("D", [128, 256, 512])
 @pytest.mark.parametrize("ring,cap", [(True, 48), (False, 48), (False, 768), (False, 1000), (True, 1024)])
 def test_decode_two_pass_edge_rows(device, D, ring, cap):
     """G4_DECODE_TWO_PASS on rows shorter than the capacity (16, 24 and 32 chunks of V^T in
@@ -241,7 +242,24 @@ def test_decode_two_pass_group_sizes(device, R, W):
                  fused=True, seed=28, num_splits=_lib.G4_DECODE_TWO_PASS)
 
 
-@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("R,ring,cap", [(1, True, 512), (4, True, 512), (8, False, 1000), (16, True, 96)])
+def test_decode_head_dim_512_automatic(device, R, ring, cap):
+    """bf16 head dim 512 (the reference's default global head dim, model.py:66) with the library's
+    own choice of path (num_splits 0): the two-launch path at any pair count for rows of up to 1024
+    slots (values workgroups of 8 or 4 waves: 4 or 8 per pair); 1..16 query heads per KV head, a
+    wrapped ring, a left-padded row, a fully masked row."""
+
+    rng = np.random.default_rng(R + cap)
+    B, H, D = 3, 2, 512
+    q_pos = rng.integers(cap, 2 * cap, B) if ring else np.array([999, 400, 37])
+    key_mask = np.ones((B, 2 * cap if ring else cap), bool)  # a linear cache's mask spans its capacity
+    key_mask[1, :20] = False
+    key_mask[2, :] = False
+    _decode_case(device, O.BF16, B=B, H=H, R=R, D=D, cap=cap, ring=ring, window=cap if ring else 0, q_pos=q_pos,
+                 key_mask=key_mask, fused=True, seed=29)
+
+
+@pytest.mark.parametrize("D", [128, 256, 512])
 def test_decode_split_keys_long_context(device, D):
     """BASELINE config 3 shape at reduced capacity: global-layer linear cache with ragged
     lengths over few (b, kv head) pairs, so the library splits the key range (scores / values /
@@ -258,7 +276,7 @@ def test_decode_split_keys_long_context(device, D):
                  fused=True, seed=24)
 
 
-@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("D", [128, 256, 512])
 def test_decode_split_keys_forced_matches_one_pass(device, D):
     """num_splits = G4_DECODE_SPLIT_KEYS on a 768-slot cache (where the one-pass kernel also
     applies) against the oracle; unfused (no append)."""
@@ -318,7 +336,7 @@ def test_decode_is_deterministic(device):
 # --- prefill attention ----------------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("dtype,D", [(O.BF16, 256), (O.BF16, 128), (O.BF16, 64), (O.F32, 64)])
+@pytest.mark.parametrize("dtype,D", [(O.BF16, 512), (O.BF16, 256), (O.BF16, 128), (O.BF16, 64), (O.F32, 64)])
 @pytest.mark.parametrize("window", [0, 48])
 def test_prefill_matches_oracle(device, dtype, D, window):
     """Causal + sliding-window prefill with left padding (fully masked pad queries); S not a
