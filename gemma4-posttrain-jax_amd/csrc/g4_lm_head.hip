@@ -135,7 +135,8 @@ __device__ __forceinline__ void lh_compute(uint32_t slot, floatx4 (&acc)[4][8], 
 
 // The epilogue of four consecutive columns n .. n + 3 of one row: bf16 rounding (the logits), the
 // optional logits store, the soft-cap, the running max / sum and the running argmax of the scores.
-template <bool SAMPLE, bool GREEDY>
+// UNIT_T: temperature 1, no division (the compiler would otherwise divide every logit and select).
+template <bool SAMPLE, bool GREEDY, bool UNIT_T>
 __device__ __forceinline__ void lh_epilogue(floatx4 v, LhState& sr, int row, int n, const G4LmHeadSampleArgs& a,
                                             const CapTable& ct, uint32_t k0, uint32_t k1) {
   uint32_t bits[4];
@@ -167,7 +168,7 @@ __device__ __forceinline__ void lh_epilogue(floatx4 v, LhState& sr, int row, int
     for (int j = 0; j < 4; ++j) {
       float score = x[j];
       if constexpr (!GREEDY) {
-        const float t = a.temperature == 1.0f ? x[j] : x[j] / a.temperature;
+        const float t = UNIT_T ? x[j] : x[j] / a.temperature;
         score = t + gumbel(k0, k1, (uint64_t)row * (uint64_t)a.vocab + (uint64_t)(n + j));
       }
       if (score > sr.best) {
@@ -179,8 +180,9 @@ __device__ __forceinline__ void lh_epilogue(floatx4 v, LhState& sr, int row, int
   }
 }
 
-// SAMPLE: run the sampler epilogue (else only the bf16 logits are written); GREEDY: no noise.
-template <bool SAMPLE, bool GREEDY>
+// SAMPLE: run the sampler epilogue (else only the bf16 logits are written); GREEDY: no noise;
+// UNIT_T: temperature 1.
+template <bool SAMPLE, bool GREEDY, bool UNIT_T = false>
 __global__ __launch_bounds__(kLhThreads, kLhWgPerCu) void lm_head_kernel(G4LmHeadSampleArgs a) {
   __shared__ __attribute__((aligned(1024))) unsigned char ring[kLhSlots][kLhSlotBytes];
   __shared__ uint16_t cap_tab[SAMPLE ? kCapTableEntries : 1];
@@ -257,7 +259,7 @@ __global__ __launch_bounds__(kLhThreads, kLhWgPerCu) void lm_head_kernel(G4LmHea
 #pragma unroll
           for (int i = 0; i < 7; ++i) acc[rb][i] = acc[rb][i + 1];
           acc[rb][7] = v;
-          lh_epilogue<SAMPLE, GREEDY>(v, st[rb], row, n0 + 16 * cb + 4 * grp, a, ct, k0, k1);
+          lh_epilogue<SAMPLE, GREEDY, UNIT_T>(v, st[rb], row, n0 + 16 * cb + 4 * grp, a, ct, k0, k1);
         }
       }
     }
@@ -390,6 +392,8 @@ extern "C" int g4_lm_head_sample(const G4LmHeadSampleArgs* args, void* stream) {
     hipLaunchKernelGGL((lm_head_kernel<false, true>), dim3((unsigned)grid), dim3(kLhThreads), 0, st, a);
   else if (greedy)
     hipLaunchKernelGGL((lm_head_kernel<true, true>), dim3((unsigned)grid), dim3(kLhThreads), 0, st, a);
+  else if (a.temperature == 1.0f)
+    hipLaunchKernelGGL((lm_head_kernel<true, false, true>), dim3((unsigned)grid), dim3(kLhThreads), 0, st, a);
   else
     hipLaunchKernelGGL((lm_head_kernel<true, false>), dim3((unsigned)grid), dim3(kLhThreads), 0, st, a);
   if (int rc = check_launch("g4_lm_head_sample")) return rc;

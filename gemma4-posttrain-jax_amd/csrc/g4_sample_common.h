@@ -30,6 +30,20 @@ __device__ __forceinline__ void threefry2x32(uint32_t k0, uint32_t k1, uint32_t&
   }
 }
 
+// Natural log of a positive, normal, finite x: log2(x) from v_log_f32, times ln 2 held as
+// kLn2Hi + kLn2Lo, with the rounding error of y * kLn2Hi recovered by an fma (Dekker's product).
+// On that domain this is the device library's logf, which adds only the scaling of subnormal
+// arguments and the selects for 0, inf and NaN; both logs of the Gumbel noise stay in it
+// (u >= 2^-126, and -log(u) >= -log(1 - 2^-23) > 2^-24).
+constexpr float kLn2Hi = 0x1.62e42ep-1f;  // ln 2 rounded to 24 bits
+constexpr float kLn2Lo = 0x1.efa39ep-25f;  // ln 2 - kLn2Hi
+
+__device__ __forceinline__ float log_pos_normal(float x) {
+  const float y = __builtin_amdgcn_logf(x);
+  const float hi = y * kLn2Hi;
+  return fmaf(kLn2Hi, y, fmaf(kLn2Lo, y, fmaf(y, kLn2Hi, -hi)));
+}
+
 // Gumbel noise of element `flat` (row-major index into the [batch, K] draw) under sample_key:
 // bits = xor of threefry2x32(key, (flat >> 32, flat & 0xffffffff)); u = float in [1, 2) from the
 // top 23 bits minus 1, floored at the smallest normal; g = -log(-log(u)).
@@ -39,7 +53,7 @@ __device__ __forceinline__ float gumbel(uint32_t k0, uint32_t k1, uint64_t flat)
   const uint32_t bits = x0 ^ x1;
   const float f = __uint_as_float((bits >> 9) | 0x3F800000u) - 1.0f;
   const float u = fmaxf(kF32Tiny, f + kF32Tiny);
-  return -logf(-logf(u));
+  return -log_pos_normal(-log_pos_normal(u));
 }
 
 struct RowState {
