@@ -10,9 +10,12 @@
 // is one LDS byte per lane and a ballot.
 //
 // Same two passes as prefill_bf16_kernel (the reference rounds probabilities after the full-row
-// softmax): pass 1 streams K for each row's max and sum, pass 2 streams K and V and forms exact
-// bf16 probabilities exp(s - m) * (1/l) for the value product. Workgroups are launched heaviest
-// (latest positions, longest causal key range) first.
+// softmax): pass 1 streams K for each row's max and sum, pass 2 streams K and V and forms the bf16
+// probabilities of the full-row softmax for the value product, evaluated as __expf(s - m) * (1/l):
+// the hardware exp and the row's reciprocal instead of expf and a division per score, a few f32
+// ulps from exp(s - m) / l, so a probability at a bf16 rounding boundary may round one bf16 step
+// the other way. Workgroups are launched heaviest (latest positions, longest causal key range)
+// first.
 //
 // What bounds it is the issue rate of each SIMD's two waves, VALU work included, more than the
 // MFMAs, so the schedule is built around three things:
