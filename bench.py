@@ -409,6 +409,34 @@ def bench_e2b_decode(steps: int, warmup: int, batch: int = 256, prompt: int = 25
             "cache": engine.kv_cache, "logits": logits}
 
 
+def lm_head_passes(n: int = 3) -> None:
+    """g4_lm_head_sample at configs[4]'s LM head, n launches: B = 256 rows of N(0, 1) hidden states
+    against the [262144, 2048] bf16 embedding ~N(0, 0.02), soft-cap 30, T = 1 with the key split.
+    The launches the LM head's rocprofv3 counter passes read (profiles/)."""
+
+    import torch
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    from gemma4_posttrain_jax_amd import config as C
+    from gemma4_posttrain_jax_amd import kernels
+    from gemma4_posttrain_jax_amd import sampler as SMP
+
+    dev = torch.device("cuda:0")
+    cfg = C.config_from_hf(E2B)
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(256, cfg.hidden_size, device=dev, generator=g).to(torch.bfloat16)
+    embed = (0.02 * torch.randn(cfg.vocab_size, cfg.hidden_size, device=dev, generator=g)).to(torch.bfloat16)
+    tok = torch.zeros(256, dtype=torch.int32, device=dev)
+    logp = torch.zeros(256, dtype=torch.float32, device=dev)
+    key = SMP.key_tensor(123, dev)
+    for _ in range(n):
+        kernels.lm_head_sample(x, embed, softcap=cfg.final_logit_softcapping, temperature=1.0, key=key,
+                               split_key=True, token_out=tok, logp_out=logp)
+    torch.cuda.synchronize()
+
+
 def bench_e2b_generate(params, cfg, batch: int = 256, prompt: int = 256, new_tokens: int = 512) -> dict:
     """sampler.generate itself at configs[4] (B=256, P=256, N=512, T=1 full-vocab sampling, no EOS),
     as the reference's harness times its compiled generate (scripts/benchmark_rollout.py:296-344):
@@ -496,6 +524,9 @@ def main() -> int:
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="first copy 256 MiB device-to-device once: the reference kernel whose FETCH_SIZE / "
                          "WRITE_SIZE counters scale the decode kernel's (see profiles/)")
+    ap.add_argument("--lm-head-only", action="store_true",
+                    help="only run g4_lm_head_sample at configs[4]'s shape three times (after the calibration "
+                         "copy, if asked for), for the LM head's counter passes; prints no bench line")
     ap.add_argument("--num-splits", type=int, default=0,
                     help="workgroups per (b, kv head) for decode attention (0: library default)")
     args = ap.parse_args()
@@ -512,6 +543,10 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.lm_head_only:
+        lm_head_passes()
+        print("lm head passes done")
+        return 0
     res = bench_decode_attention(args.steps, args.warmup, args.num_splits)
     bytes_step = algorithmic_bytes_per_step()
     gbs = bytes_step / (res["ms_per_step"] * 1e-3) / 1e9
