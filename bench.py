@@ -356,8 +356,9 @@ def random_params(cfg, dev, seed=0):
 
 def bench_e2b_decode(steps: int, warmup: int, batch: int = 256, prompt: int = 256, new_tokens: int = 512) -> dict:
     """A whole rollout at B=256: prefill of the 256-token prompts, then the
-    ``new_tokens - 1`` graphed decode steps that generate() runs (sample at T=1 + one-token forward
-    of all 30 layers + LM head; the last sampled token is not decoded, sampler.py:287-300).
+    ``new_tokens - 1`` decode steps that generate() runs, each its loop body: the bookkeeping launch
+    (g4_rollout_step) and one graph replay (one-token forward of all 30 layers + LM head with the
+    T=1 draw in its epilogue); the last sampled token is not decoded, sampler.py:287-300.
 
     ``steps`` = 0 times every decode step after ``warmup`` (the caches fill from 256 to 767
     positions over the rollout, so the average covers short and full rows alike); ``steps`` > 0
@@ -386,20 +387,33 @@ def bench_e2b_decode(steps: int, warmup: int, batch: int = 256, prompt: int = 25
     cache = out.kv_cache
     lengths = torch.full((batch,), prompt, dtype=torch.int32, device=dev)
     active = torch.ones(batch, dtype=torch.bool, device=dev)
-    # what generate() does per token at T=1: one graph replay = forward of all layers + LM head +
-    # fused soft-cap / log-softmax / Gumbel-max draw
+    # what generate() does per token at T=1 without EOS ids (sampler.generate's loop body): the
+    # bookkeeping launch (g4_rollout_step: the drawn token and logp into the completion columns, the
+    # next step's token / position / mask written into the graph's input buffers), then one graph
+    # replay = forward of all layers + LM head + fused soft-cap / log-softmax / Gumbel-max draw
     key = SMP.key_tensor(2, dev)  # PRNGKey(2), split once per step on the device
-    tok, _ = kernels.sample_tokens(out.logits[:, -1], softcap=None, temperature=1.0, key=key)
+    tok, logp = kernels.sample_tokens(out.logits[:, -1], softcap=None, temperature=1.0, key=key)
     engine = SMP.GraphedDecodeStep(params, cfg, cache, temperature=1.0, key=key)
+    completion_ids = torch.full((batch, new_tokens), cfg.pad_token_id, dtype=torch.int32, device=dev)
+    completion_mask = torch.zeros((batch, new_tokens), dtype=torch.bool, device=dev)
+    rollout_logps = torch.zeros((batch, new_tokens), dtype=torch.float32, device=dev)
+
+    def step(i, tok, logp):
+        kernels.rollout_step(i, tok, logp, active, completion_ids=completion_ids, completion_mask=completion_mask,
+                             rollout_logps=rollout_logps, pad_id=cfg.pad_token_id, eos_ids=None,
+                             prompt_lengths=lengths, next_token=engine.tok, next_pos=engine.pos,
+                             next_mask=engine.active)
+        return engine.replay_sample()
+
     n_decode = new_tokens - 1
     timed = n_decode - warmup if steps <= 0 else min(steps, n_decode - warmup)
     torch.cuda.synchronize()
     for i in range(warmup):
-        tok, logp = engine.step_sample(tok, lengths + i, active)
+        tok, logp = step(i, tok, logp)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(warmup, warmup + timed):
-        tok, logp = engine.step_sample(tok, lengths + i, active)
+        tok, logp = step(i, tok, logp)
     torch.cuda.synchronize()
     s = (time.perf_counter() - t0) / timed
     rollout_s = prefill_s + n_decode * s
