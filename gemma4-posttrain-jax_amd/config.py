@@ -44,17 +44,62 @@ class Gemma4TextConfig(NamedTuple):
     pad_token_id: int
 
 
+def _attention_dims(text: Mapping[str, Any], layer_types: list[str]) -> tuple[int, int, int, int | None]:
+    """(sliding head dim, global head dim, kv heads, global kv heads) of an HF text config
+    (model.py:61-97).
+
+    Without ``per_layer_config`` the legacy fields are read as they are. With it (transformers
+    writes the field and drops ``global_head_dim``), every layer starts from ``head_dim`` /
+    ``num_key_value_heads`` and takes its sparse override; each attention type must then resolve
+    to one (dim, kv heads) pair, and a separate global kv-head count only exists for K=V
+    global layers. Anything else cannot be represented by this parameter structure and raises
+    ``ValueError``, as the reference does.
+    """
+
+    head_dim = int(text.get("head_dim", 256))
+    kv_heads = int(text["num_key_value_heads"])
+    if "per_layer_config" not in text:
+        return head_dim, int(text.get("global_head_dim", 512)), kv_heads, text.get("num_global_key_value_heads")
+    raw = text["per_layer_config"]
+    if raw is not None and not isinstance(raw, Mapping):
+        raise ValueError("per_layer_config must map layer indices to overrides")
+    overrides: dict[int, Mapping[str, Any]] = {}
+    for key, value in (raw or {}).items():
+        index = int(key)
+        if str(index) != str(key) or not 0 <= index < len(layer_types) or index in overrides:
+            raise ValueError(f"invalid or repeated per_layer_config layer index: {key!r}")
+        if not isinstance(value, Mapping) or not set(value) <= {"head_dim", "num_key_value_heads"}:
+            raise ValueError(f"unsupported per_layer_config override for layer {index}: {value!r}")
+        overrides[index] = value
+    q_heads = int(text["num_attention_heads"])
+    per_type: dict[str, set[tuple[int, int]]] = {SLIDING: set(), FULL: set()}
+    for index, layer_type in enumerate(layer_types):
+        override = overrides.get(index, {})
+        dims = (int(override.get("head_dim", head_dim)), int(override.get("num_key_value_heads", kv_heads)))
+        if dims[0] <= 0 or dims[1] <= 0 or q_heads % dims[1]:
+            raise ValueError(f"layer {index}: head dim and kv heads must be positive, kv heads dividing {q_heads}")
+        per_type[layer_type].add(dims)
+    if len(per_type[SLIDING]) > 1 or len(per_type[FULL]) > 1:
+        raise ValueError("layers of one attention type have different dimensions, which these parameters cannot hold")
+    sliding_dim, sliding_kv = min(per_type[SLIDING], default=(head_dim, kv_heads))
+    global_dim, global_kv = min(per_type[FULL], default=(head_dim, kv_heads))
+    if global_kv != sliding_kv and not text.get("attention_k_eq_v", False):
+        raise ValueError("a separate global kv-head count needs K=V global attention (attention_k_eq_v)")
+    return sliding_dim, global_dim, sliding_kv, (global_kv if global_kv != sliding_kv else None)
+
+
 def config_from_hf(hf: Mapping[str, Any]) -> Gemma4TextConfig:
-    """model.py:100-147 (legacy global-attention fields; the last layer is forced FULL, line 112)."""
+    """model.py:100-147: a composite or text-only HF ``config.json`` dict, legacy global-attention
+    fields or the sparse ``per_layer_config`` of transformers' serialization (model.py:61-97);
+    the last layer is forced FULL (line 112)."""
 
     text = hf.get("text_config", hf)
     num_layers = int(text["num_hidden_layers"])
     layer_types = list(text["layer_types"])
     if len(layer_types) != num_layers:
         raise ValueError(f"layer_types has {len(layer_types)} entries for {num_layers} layers")
-    if "per_layer_config" in text and text["per_layer_config"]:
-        raise ValueError("per_layer_config overrides are not supported by this build")
     layer_types[-1] = FULL
+    head_dim, global_head_dim, kv_heads, global_kv_heads = _attention_dims(text, layer_types)
     rope = text.get("rope_parameters") or {}
     sliding_rope = rope.get(SLIDING) or {}
     full_rope = rope.get(FULL) or {}
@@ -66,10 +111,10 @@ def config_from_hf(hf: Mapping[str, Any]) -> Gemma4TextConfig:
         intermediate_size=int(text["intermediate_size"]),
         num_hidden_layers=num_layers,
         num_attention_heads=int(text["num_attention_heads"]),
-        num_key_value_heads=int(text["num_key_value_heads"]),
-        head_dim=int(text.get("head_dim", 256)),
-        global_head_dim=int(text.get("global_head_dim", 512)),
-        num_global_key_value_heads=text.get("num_global_key_value_heads"),
+        num_key_value_heads=kv_heads,
+        head_dim=head_dim,
+        global_head_dim=global_head_dim,
+        num_global_key_value_heads=global_kv_heads,
         layer_types=tuple(layer_types),
         sliding_window=int(text.get("sliding_window", 512)),
         num_kv_shared_layers=int(text.get("num_kv_shared_layers", 0)),
