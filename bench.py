@@ -275,8 +275,8 @@ def cpu_baseline_decode_attention(target_s: float = 12.0) -> dict:
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(0)
-    k = torch.randn((B, W, HKV, D), generator=g).to(torch.bfloat16)
-    v = torch.randn((B, W, HKV, D), generator=g).to(torch.bfloat16)
+    k = torch.randn((B, HKV, W, D), generator=g).to(torch.bfloat16)  # head-major ring (oracle/torch_cpu.py)
+    v = torch.randn((B, HKV, W, D), generator=g).to(torch.bfloat16)
     key_mask = torch.ones((B, CTX + 4096), dtype=torch.bool)
     pos = torch.from_numpy(np.random.default_rng(0).integers(1536, 2048, B).astype(np.int32))
     times = []
@@ -313,16 +313,17 @@ E2B = dict(
 )
 
 
-# q / k norm weights of the E2B-like model. With norm weights 1 the normed q and k of dimension 256
-# give scale-1.0 scores up to ~50 (one bf16 ulp 0.25) and the random model is chaotic: the oracle
-# run with f32 and with f64 accumulation disagrees by up to 3.8 on the logits. At 0.25 the scores
-# are O(1) and the model's outputs are determined well enough to test (the runtime does not depend
-# on the values).
+# q / k norm weights of the E2B-like model in the parity test (tests/test_gpu_e2b.py). With norm
+# weights 1 (the benchmarked model, as configs[4] fixes the norms) the normed q and k of dimension
+# 256 give scale-1.0 scores up to ~50 (one bf16 ulp 0.25) and the random model is chaotic: the
+# oracle run with f32 and with f64 accumulation disagrees by up to 3.8 on the logits. At 0.25 the
+# scores are O(1) and the model's outputs are determined well enough to test. The runtime does not
+# depend on the values.
 E2B_QK_NORM = 0.25
 
 
-def random_params(cfg, dev, seed=0):
-    """Random-init E2B-like bf16 weights ~N(0, 0.02), q / k norm weights E2B_QK_NORM, other norms 1,
+def random_params(cfg, dev, seed=0, qk_norm: float = 1.0):
+    """Random-init E2B-like bf16 weights ~N(0, 0.02), q / k norm weights ``qk_norm``, other norms 1,
     layer_scalar 1 (on the GPU)."""
 
     import torch
@@ -347,7 +348,7 @@ def random_params(cfg, dev, seed=0):
         sh = is_kv_shared(cfg, i)
         att = M.AttentionParams(w(Mh, Rr, H, Dh), None if sh else w(Mh, H, Dh),
                                 None if sh or not layer_has_v_proj(cfg, i) else w(Mh, H, Dh), w(Rr, H, Dh, Mh),
-                                n(Dh, E2B_QK_NORM), None if sh else n(Dh, E2B_QK_NORM))
+                                n(Dh, qk_norm), None if sh else n(Dh, qk_norm))
         F = layer_intermediate_size(cfg, i)
         layers.append(M.DecoderLayerParams(n(Mh), att, n(Mh), n(Mh), M.MLPParams(w(Mh, F), w(Mh, F), w(F, Mh)), n(Mh),
                                            None, torch.ones((), device=dev, dtype=torch.bfloat16)))
@@ -451,12 +452,17 @@ def lm_head_passes(n: int = 3) -> None:
     torch.cuda.synchronize()
 
 
-def bench_e2b_generate(params, cfg, batch: int = 256, prompt: int = 256, new_tokens: int = 512) -> dict:
-    """sampler.generate itself at configs[4] (B=256, P=256, N=512, T=1 full-vocab sampling, no EOS),
-    as the reference's harness times its compiled generate (scripts/benchmark_rollout.py:296-344):
+def bench_e2b_generate(params, cfg, batch: int = 256, prompt: int = 256, new_tokens: int = 512,
+                       eos_ids: tuple = ()) -> dict:
+    """sampler.generate itself at configs[4] (B=256, P=256, N=512, T=1 full-vocab sampling), timed
+    as the reference's harness times its compiled generate (scripts/benchmark_rollout.py:296-357):
     one untimed call, then one timed call from prompt ids to RolloutBatch (prefill, the HIP-graph
-    capture of the decode step, 511 graphed decode steps with fused sampling, the per-step
-    bookkeeping)."""
+    capture of the decode step, the graphed decode steps with fused sampling, the per-step
+    bookkeeping). Reports the harness's figures: decode steps = the longest completion, slot
+    tokens = batch x decode steps, actual tokens = the sum of the lengths, and its output-semantics
+    check (the mask is each row's prefix of its length, pad ids and zero log-probabilities outside
+    it, finite ones inside). With ``eos_ids`` rows finish at different steps and the loop exits
+    once none is active."""
 
     import torch
 
@@ -466,15 +472,24 @@ def bench_e2b_generate(params, cfg, batch: int = 256, prompt: int = 256, new_tok
     g = torch.Generator(device=dev).manual_seed(11)
     ids = torch.randint(0, cfg.vocab_size, (batch, prompt), device=dev, generator=g, dtype=torch.int32)
     mask = torch.ones_like(ids, dtype=torch.bool)
-    sc = SMP.SamplerConfig(max_prompt_len=prompt, max_new_tokens=new_tokens, temperature=1.0, seed=3)
-    SMP.generate(params, cfg, ids, mask, sampler_config=sc)
+    sc = SMP.SamplerConfig(max_prompt_len=prompt, max_new_tokens=new_tokens, temperature=1.0, seed=3,
+                           eos_ids=tuple(eos_ids))
+    SMP.generate(params, cfg, ids, mask, sampler_config=sc, key=1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    rb = SMP.generate(params, cfg, ids, mask, sampler_config=sc)
+    rb = SMP.generate(params, cfg, ids, mask, sampler_config=sc, key=2)
     torch.cuda.synchronize()
     s = time.perf_counter() - t0
-    assert int(rb.lengths.min()) == new_tokens
-    return {"generate_s": s, "generate_tok_s": batch * new_tokens / s}
+    lengths = rb.lengths.cpu().numpy().astype(np.int64)
+    cm = rb.completion_mask.cpu().numpy()
+    ok = bool(np.array_equal(cm, np.arange(new_tokens)[None, :] < lengths[:, None])
+              and (rb.completion_ids.cpu().numpy()[~cm] == cfg.pad_token_id).all()
+              and (rb.rollout_logps.cpu().numpy()[~cm] == 0).all()
+              and np.isfinite(rb.rollout_logps.cpu().numpy()[cm]).all())
+    steps = int(lengths.max())
+    return {"generate_s": s, "decode_steps": steps, "slot_tok_s": batch * steps / s,
+            "actual_tok_s": float(lengths.sum()) / s, "amortized_step_ms": s * 1e3 / steps,
+            "mean_length": float(lengths.mean()), "min_length": int(lengths.min()), "output_semantics_ok": ok}
 
 
 def cpu_baseline_e2b_decode(gpu: dict, steps: int = 3) -> dict:
@@ -611,8 +626,18 @@ def main() -> int:
         # the reference harness's slot tokens/s: batch x new tokens / (prefill + every decode step)
         line["rollout_tok_s_b256"] = round(e2b["rollout_tok_s"], 1)
         gen = bench_e2b_generate(e2b["params"], e2b["cfg"])
+        assert gen["min_length"] == 512 and gen["output_semantics_ok"]
         line["generate_s_b256"] = round(gen["generate_s"], 3)
-        line["generate_tok_s_b256"] = round(gen["generate_tok_s"], 1)
+        line["generate_tok_s_b256"] = round(gen["slot_tok_s"], 1)
+        # with EOS ids (every 64th vocab id: at T = 1 a row stops after ~64 tokens on average, the
+        # longest after a few hundred), the GRPO caller's configuration (train_grpo.py:854-856)
+        eos = bench_e2b_generate(e2b["params"], e2b["cfg"], eos_ids=tuple(range(1, e2b["cfg"].vocab_size, 64)))
+        line["generate_eos_b256"] = {
+            "workload": "configs[4] generate with 4096 EOS ids (every 64th id), rows finishing at varied steps",
+            "s": round(eos["generate_s"], 3), "decode_steps": eos["decode_steps"],
+            "mean_length": round(eos["mean_length"], 1), "slot_tok_s": round(eos["slot_tok_s"], 1),
+            "actual_tok_s": round(eos["actual_tok_s"], 1), "amortized_step_ms": round(eos["amortized_step_ms"], 3),
+            "output_semantics_ok": eos["output_semantics_ok"]}
         if not args.no_cpu:
             cpu5 = cpu_baseline_e2b_decode(e2b)
             line["cpu_decode_s_per_step_b256"] = round(cpu5["s_per_step"], 3)

@@ -33,7 +33,30 @@ std::once_flag g_setup_once[kMaxDevices];
 int g_setup_status[kMaxDevices];
 char g_setup_error[kMaxDevices][512];
 
+// Kernels whose dynamic-LDS limit the set-up raised, per device (written under the device's
+// std::call_once, read after it).
+constexpr int kMaxLdsKernels = 64;
+struct LdsRecord {
+  const void* fn;
+  bool ok;
+};
+LdsRecord g_lds[kMaxDevices][kMaxLdsKernels];
+int g_lds_count[kMaxDevices];
+
 }  // namespace
+
+bool raise_lds_limit(int device, const void* fn, int bytes) {
+  const bool ok = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
+  if (!ok) (void)hipGetLastError();  // the failure is recorded here, not left for the next launch to report
+  if (g_lds_count[device] < kMaxLdsKernels) g_lds[device][g_lds_count[device]++] = LdsRecord{fn, ok};
+  return ok;
+}
+
+bool lds_limit_raised(int device, const void* fn) {
+  for (int i = 0; i < g_lds_count[device]; ++i)
+    if (g_lds[device][i].fn == fn) return g_lds[device][i].ok;
+  return false;
+}
 
 int device_setup(int* device) {
   int dev = -1;

@@ -165,9 +165,21 @@ constexpr size_t kMaxLdsFast = 160 * 1024;  // gfx950: 160 KiB of LDS per workgr
 // block sums [R][2] (the V^T tiles and the new K row are static).
 size_t stage_lds_bytes(int R) { return (size_t)R * kStageStride * 2 + (size_t)kDecodeWaves * 16 * 4 + (size_t)R * 2 * 4; }
 
+// The set-up's record for kernel `fn` (device_setup first): G4_OK when its raised LDS limit is in
+// place, else the error a launch of it returns.
+int need_lds_limit(const void* fn, const char* what) {
+  int dev = 0;
+  const int setup = device_setup(&dev);
+  if (setup != G4_OK) return setup;
+  if (!lds_limit_raised(dev, fn))
+    return fail(G4_ERR_LAUNCH, "g4_decode_attention: the LDS limit of the %s kernel could not be raised on device %d",
+                what, dev);
+  return G4_OK;
+}
+
 template <int D, int NSPLIT>
 int launch_stage(const G4DecodeArgs& a, hipStream_t st) {
-  const int setup = device_setup(nullptr);  // raised LDS limits
+  const int setup = need_lds_limit((const void*)decode_bf16_stage_kernel<D, NSPLIT>, "ring-stage");
   if (setup != G4_OK) return setup;
   const int64_t npairs = (int64_t)a.batch * a.kv_heads;
   const int64_t blocks = NSPLIT == 1 ? npairs : (npairs + 7) / 8 * 8 * NSPLIT;
@@ -178,7 +190,7 @@ int launch_stage(const G4DecodeArgs& a, hipStream_t st) {
 
 template <int D, int NSPLIT, bool LONG>
 int launch_fast(const G4DecodeArgs& a, int t_alloc, size_t lds, hipStream_t st) {
-  const int setup = device_setup(nullptr);  // raised LDS limits
+  const int setup = need_lds_limit((const void*)decode_bf16_fast_kernel<D, NSPLIT, LONG>, "long-row");
   if (setup != G4_OK) return setup;
   const int64_t npairs = (int64_t)a.batch * a.kv_heads;
   const int64_t blocks = NSPLIT == 1 ? npairs : (npairs + 7) / 8 * 8 * NSPLIT;
@@ -207,7 +219,8 @@ bool use_split_keys(const G4DecodeArgs& a) {
 
 template <int D>
 int launch_split_keys(const G4DecodeArgs& a, hipStream_t st) {
-  const int setup = device_setup(nullptr);  // raised LDS limits
+  int setup = need_lds_limit((const void*)decode_bf16_splitk_scores_kernel<D>, "split-K scores");
+  if (setup == G4_OK) setup = need_lds_limit((const void*)decode_bf16_splitk_values_kernel<D>, "split-K values");
   if (setup != G4_OK) return setup;
   const int64_t npairs = (int64_t)a.batch * a.kv_heads;
   SplitKWorkspace ws;
@@ -291,9 +304,8 @@ void* g_scratch[kMaxDevices];
 int setup_decode_kernels(int device) {
   void* ptr = nullptr;
   const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-  if (e != hipSuccess || !ptr)
-    return fail(G4_ERR_LAUNCH, "g4_init: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
-  g_scratch[device] = ptr;
+  if (e != hipSuccess) (void)hipGetLastError();
+  g_scratch[device] = e == hipSuccess ? ptr : nullptr;  // null: g4_decode_attention_noalloc reports it
   const int stage = (int)stage_lds_bytes(16);
   const struct {
     const void* fn;
@@ -314,9 +326,8 @@ int setup_decode_kernels(int device) {
       {(const void*)decode_bf16_splitk_values_kernel<256>, stage},
       {(const void*)decode_bf16_splitk_values_kernel<512>, stage},
   };
-  for (const auto& k : kernels)
-    if (hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize, k.bytes) != hipSuccess)
-      return fail(G4_ERR_LAUNCH, "g4_init: cannot raise the LDS limit of a decode kernel to %d B", k.bytes);
+  // a kernel whose limit stays at the default is recorded as such: only its launches fail
+  for (const auto& k : kernels) raise_lds_limit(device, k.fn, k.bytes);
   return G4_OK;
 }
 
@@ -505,6 +516,9 @@ extern "C" int g4_decode_attention_noalloc(const G4DecodeArgs* args, void* strea
     int dev = 0;
     const int rc = device_setup(&dev);
     if (rc != G4_OK) return rc;
+    if (!g_scratch[dev])
+      return fail(G4_ERR_LAUNCH, "g4_decode_attention_noalloc: the scratch address of device %d is unknown "
+                  "(hipGetSymbolAddress failed at set-up)", dev);
     a.workspace = g_scratch[dev];
     a.workspace_bytes = kNoAllocScratchBytes;
   }

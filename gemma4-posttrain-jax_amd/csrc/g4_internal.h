@@ -22,10 +22,19 @@ constexpr int kMaxDevices = 64;
 // Returns G4_OK or the set-up's error code (message via g4_last_error), and the device ordinal.
 int device_setup(int* device);
 
-// Per-source set-up steps run by device_setup for `device` (the current device).
+// Per-source set-up steps run by device_setup for `device` (the current device). A step records
+// what it could not set up per kernel (see raise_lds_limit) and fails only on errors that leave no
+// path of its source usable.
 int setup_decode_kernels(int device);
 int setup_prefill_kernels(int device);
 int setup_lm_head(int device);
+
+// Raises kernel `fn`'s dynamic-LDS limit to `bytes` on `device` (the current device; called from the
+// set-up steps only) and records whether that worked. lds_limit_raised(device, fn) reads the record
+// after device_setup: a launcher whose kernel needs the raised limit checks it, so a kernel whose
+// limit could not be raised disables only the paths that launch it.
+bool raise_lds_limit(int device, const void* fn, int bytes);
+bool lds_limit_raised(int device, const void* fn);
 
 // Head dims with an instantiated kernel: powers of two 8..512 (bf16 attention: 32..256).
 inline bool supported_head_dim(int d) { return d >= 8 && d <= 512 && (d & (d - 1)) == 0; }

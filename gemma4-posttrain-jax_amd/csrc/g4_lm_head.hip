@@ -73,7 +73,7 @@ __device__ __forceinline__ void lh_merge(LhState& a, const LhState& b) {
   } else if (b.m > kF32Min) {
     a.s += b.s * expf(b.m - a.m);
   }
-  if (b.best > a.best || (b.best == a.best && b.idx < a.idx)) {  // ties: the first column (argmax)
+  if (beats(b.best, b.idx, a.best, a.idx)) {  // ties and NaNs: the first column (argmax)
     a.best = b.best;
     a.bx = b.bx;
     a.idx = b.idx;
@@ -171,7 +171,7 @@ __device__ __forceinline__ void lh_epilogue(floatx4 v, LhState& sr, int row, int
         const float t = UNIT_T ? x[j] : x[j] / a.temperature;
         score = t + gumbel(k0, k1, (uint64_t)row * (uint64_t)a.vocab + (uint64_t)(n + j));
       }
-      if (score > sr.best) {
+      if (takes_best(score, sr.best)) {
         sr.best = score;
         sr.bx = x[j];
         sr.idx = n + j;
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(kCombineThreads) void lm_head_combine_kernel(G4LmHe
   }
   if (threadIdx.x == 0) {
     const LhState t = red[0];
-    // a row of NaN scores keeps no best: clamp the token into the vocab
+    // only a row whose every score is -inf keeps no best: clamp the token into the vocab
     const int token = t.idx < 0 ? 0 : (t.idx >= a.vocab ? a.vocab - 1 : t.idx);
     a.token_out[row] = token;
     a.logp_out[row] = (t.bx - t.m) - logf(t.s);
@@ -335,10 +335,14 @@ int lh_grid(const G4LmHeadSampleArgs& a, int dev) {
 }  // namespace
 
 // The persistent grid of this device: two workgroups per CU (run once per device by device_setup).
+// Without a CU count the grid stays 0 and only g4_lm_head_sample reports it.
 int setup_lm_head(int device) {
   hipDeviceProp_t p;
-  if (hipGetDeviceProperties(&p, device) != hipSuccess || p.multiProcessorCount <= 0)
-    return fail(G4_ERR_LAUNCH, "g4_init: cannot read the CU count of device %d", device);
+  if (hipGetDeviceProperties(&p, device) != hipSuccess || p.multiProcessorCount <= 0) {
+    (void)hipGetLastError();
+    g_lh_grid[device] = 0;
+    return G4_OK;
+  }
   g_lh_grid[device] = kLhWgPerCu * p.multiProcessorCount;
   return G4_OK;
 }
@@ -379,6 +383,8 @@ extern "C" int g4_lm_head_sample(const G4LmHeadSampleArgs* args, void* stream) {
   int dev = 0;
   if (int rc = device_setup(&dev)) return rc;
   const int grid = lh_grid(a, dev);
+  if (grid <= 0)
+    return fail(G4_ERR_LAUNCH, "g4_lm_head_sample: the CU count of device %d could not be read at set-up", dev);
   if (sample) {
     const size_t need = (size_t)grid * kLhRows * 5u * 4u;
     if (!a.workspace || a.workspace_bytes < need)

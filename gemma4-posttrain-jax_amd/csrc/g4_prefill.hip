@@ -216,12 +216,14 @@ int raise_prefill_lds_limit(int device) {
   int& max_seq = g_lds_max_seq[device][D == 256];
   max_seq = 0;
   hipFuncAttributes attr;
-  if (hipFuncGetAttributes(&attr, (const void*)prefill_bf16_lds_kernel<D, kPfBlocks, kPfWaves>) != hipSuccess)
-    return fail(G4_ERR_LAUNCH, "g4_init: cannot query the prefill kernel's attributes");
+  // a failed query or limit leaves max_seq at 0: every row then takes the register kernel
+  if (hipFuncGetAttributes(&attr, (const void*)prefill_bf16_lds_kernel<D, kPfBlocks, kPfWaves>) != hipSuccess) {
+    (void)hipGetLastError();
+    return G4_OK;
+  }
   const int room = (kLdsBytes - (int)attr.sharedSizeBytes) / 16 * 16;
   const int cap = room < kPfMaxSeq ? room : kPfMaxSeq;
-  if (cap > 0 && hipFuncSetAttribute((const void*)prefill_bf16_lds_kernel<D, kPfBlocks, kPfWaves>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, cap) == hipSuccess)
+  if (cap > 0 && raise_lds_limit(device, (const void*)prefill_bf16_lds_kernel<D, kPfBlocks, kPfWaves>, cap))
     max_seq = cap;
   return G4_OK;
 }

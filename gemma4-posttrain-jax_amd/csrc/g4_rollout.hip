@@ -9,20 +9,38 @@ namespace g4 {
 namespace {
 
 constexpr int kRolloutThreads = 1024;
+constexpr int kEosChunk = 4096;  // EOS ids staged through LDS per pass
 
-// One workgroup; thread t takes rows t, t + 1024, ... (a rollout batch is a few hundred rows).
+// One workgroup; rows in blocks of blockDim.x (thread t takes row b0 + t of each block). The EOS
+// ids pass through LDS in chunks (16-byte reads, padded with a copy of the chunk's first id, which
+// changes no match), so a large EOS set costs one broadcast LDS read per four ids and row block.
 __global__ __launch_bounds__(kRolloutThreads) void rollout_step_kernel(G4RolloutStepArgs a) {
+  __shared__ __attribute__((aligned(16))) int32_t eos_lds[kEosChunk];
   bool stays_any = false;
-  for (int b = threadIdx.x; b < a.batch; b += blockDim.x) {
-    const bool act = a.active[b] != 0;                 // the step's mask
+  for (int b0 = 0; b0 < a.batch; b0 += blockDim.x) {
+    const int b = b0 + (int)threadIdx.x;
+    const bool row = b < a.batch;
+    const bool act = row && a.active[b] != 0;           // the step's mask
     const int32_t tok = act ? a.sampled[b] : a.pad_id;  // finished rows emit pad
+    bool eos = false;
+    for (int c0 = 0; c0 < a.n_eos; c0 += kEosChunk) {
+      const int n = a.n_eos - c0 < kEosChunk ? a.n_eos - c0 : kEosChunk;
+      const int n4 = (n + 3) / 4 * 4;
+      __syncthreads();  // the previous chunk's readers are done
+      for (int i = threadIdx.x; i < n4; i += blockDim.x) eos_lds[i] = a.eos_ids[c0 + (i < n ? i : 0)];
+      __syncthreads();
+      const int4* ids4 = reinterpret_cast<const int4*>(eos_lds);
+      for (int i = 0; i < n4 / 4; ++i) {
+        const int4 e = ids4[i];
+        eos = eos || tok == e.x || tok == e.y || tok == e.z || tok == e.w;
+      }
+    }
+    if (!row) continue;
     const int64_t at = (int64_t)b * a.max_new + a.step;
     if (a.id_bytes == 8) reinterpret_cast<int64_t*>(a.completion_ids)[at] = tok;
     else reinterpret_cast<int32_t*>(a.completion_ids)[at] = tok;
     a.completion_mask[at] = act ? 1 : 0;
     a.rollout_logps[at] = act ? a.logp[b] : 0.f;
-    bool eos = false;
-    for (int i = 0; i < a.n_eos; ++i) eos = eos || tok == a.eos_ids[i];
     const bool stays = act && !eos;
     stays_any = stays_any || stays;
     if (a.next_token) a.next_token[b] = tok;

@@ -80,7 +80,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) 
     }
 #pragma unroll
     for (int u = 0; u < N; ++u) {
-      if (score[u] > st.best) {
+      if (takes_best(score[u], st.best)) {
         st.best = score[u];
         st.idx = col0 + u * stride;
       }
@@ -134,7 +134,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) 
     const float* prow = a.proposal + (int64_t)row * a.proposal_width;
     for (int j = threadIdx.x; j < a.proposal_width; j += kSampleThreads) {
       const float score = prow[j] + gumbel(k0, k1, (uint64_t)row * (uint64_t)a.proposal_width + (uint64_t)j);
-      if (score > st.best) {
+      if (takes_best(score, st.best)) {
         st.best = score;
         st.idx = j;
       }
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(G4SampleArgs a) 
   if (threadIdx.x == 0) {
     RowState t = red[0];
     for (int i = 1; i < kSampleThreads / 64; ++i) merge(t, red[i]);
-    // a row of NaN scores keeps no best: clamp so that every read below stays in bounds
+    // only a row whose every score is -inf keeps no best: clamp so that every read below stays in bounds
     const int width = proposal ? a.proposal_width : a.vocab;
     int token = t.idx < 0 ? 0 : (t.idx >= width ? width - 1 : t.idx);
     if (proposal && a.proposal_index) token = a.proposal_index[(int64_t)row * a.proposal_width + token];

@@ -56,6 +56,19 @@ __device__ __forceinline__ float gumbel(uint32_t k0, uint32_t k1, uint64_t flat)
   return -log_pos_normal(-log_pos_normal(u));
 }
 
+// The running argmax under jnp.argmax's rule (argmax in _sample_token and inside
+// jax.random.categorical): a NaN score is greater than every number and the first NaN column wins.
+// takes_best: a score met after every column of `best` replaces it (columns arrive in increasing
+// order, so an equal score keeps the earlier column, and a NaN best is never replaced).
+__device__ __forceinline__ bool takes_best(float score, float best) { return !(score <= best) && best == best; }
+
+// beats: whether state (bb, bi) wins over (ab, ai) when two states of disjoint columns merge.
+__device__ __forceinline__ bool beats(float bb, int bi, float ab, int ai) {
+  const bool bn = bb != bb, an = ab != ab;
+  if (bn || an) return bn && (!an || bi < ai);
+  return bb > ab || (bb == ab && bi < ai);
+}
+
 struct RowState {
   float m, s;  // running max of x and sum of exp(x - m)
   float best;  // best score so far
@@ -69,7 +82,7 @@ __device__ __forceinline__ void merge(RowState& a, const RowState& b) {
   } else if (b.m > kF32Min) {
     a.s += b.s * expf(b.m - a.m);
   }
-  if (b.best > a.best || (b.best == a.best && b.idx < a.idx)) {  // ties: the first column (argmax)
+  if (beats(b.best, b.idx, a.best, a.idx)) {  // ties and NaNs: the first column (argmax)
     a.best = b.best;
     a.idx = b.idx;
   }

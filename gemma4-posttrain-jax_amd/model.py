@@ -17,7 +17,6 @@ norm, and post-MLP norm + residual + layer scalar + the next layer's input norm)
 from __future__ import annotations
 
 import math
-import weakref
 from typing import Literal, NamedTuple
 
 import numpy as np
@@ -142,7 +141,6 @@ class PackedWeights(NamedTuple):
     embed_scale_f: float  # the same rounded scale as a host float (no device read inside a graph)
 
 
-_PACKED: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
 _PACKED_BY_ID: dict = {}
 
 
@@ -160,12 +158,29 @@ def _rope_inv_freq(config: Gemma4TextConfig) -> dict:
     return {SLIDING: inv_s, FULL: inv_f}
 
 
+def _tensor_versions(tree) -> tuple:
+    """The version counters of every tensor in a params pytree (torch bumps a tensor's counter on
+    each in-place write: ``copy_``, ``mul_``, optimizer steps)."""
+
+    if isinstance(tree, torch.Tensor):
+        return (tree._version,)
+    if isinstance(tree, (tuple, list)):
+        return sum((_tensor_versions(x) for x in tree), ())
+    return ()
+
+
 def pack_weights(params: Gemma4TextParams, config: Gemma4TextConfig) -> PackedWeights:
-    """Fuse and reorder the projection weights once per params object (cached)."""
+    """Fuse and reorder the projection weights once per params object (cached).
+
+    The packed copy is rebuilt when ``params`` is another object or when any of its tensors was
+    written in place since the packing (their version counters moved), so an in-place weight
+    update is never served stale weights. Writes that bypass the counters (through ``.data`` or
+    another framework's view of the memory) are not seen: pass a new params object after those."""
 
     key = id(params)
+    versions = _tensor_versions(params)
     hit = _PACKED_BY_ID.get(key)
-    if hit is not None and hit[0] is params:
+    if hit is not None and hit[0] is params and hit[2] == versions:
         return hit[1]
     layers = []
     for i, lp in enumerate(params.layers):
@@ -190,7 +205,7 @@ def pack_weights(params: Gemma4TextParams, config: Gemma4TextConfig) -> PackedWe
     scale = torch.tensor(math.sqrt(config.hidden_size), dtype=dt)
     packed = PackedWeights(tuple(layers), scale.to(dev), inv, float(scale.float()))
     _PACKED_BY_ID.clear()  # one live params object at a time (rollout reuses the same weights)
-    _PACKED_BY_ID[key] = (params, packed)
+    _PACKED_BY_ID[key] = (params, packed, versions)
     return packed
 
 
@@ -288,6 +303,7 @@ def forward_gemma4_text(
     kv_cache: KVCache | None = None,
     cache_mode: Literal["prefill", "append"] = "prefill",
     layer_outputs: list | None = None,
+    remat_layers: bool = False,
     lora=None,
     write_pos: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, KVCache | None]:
@@ -295,9 +311,23 @@ def forward_gemma4_text(
 
     Without a cache the forward runs in prefill form over a scratch cache (the reference's
     cache-less path computes the same attention). ``layer_outputs`` collects every decoder
-    layer's output (the reference's parity hook, model.py:580). ``lora`` must be None: the
-    rollout path runs without adapters (the reference applies LoRA inside the projections,
+    layer's output (the reference's parity hook, model.py:580). ``remat_layers`` is accepted for
+    the reference's signature: it only changes which activations the reference's backward keeps
+    (jax.checkpoint, model.py:651), and this forward-only path keeps none. ``lora`` must be None:
+    the rollout path runs without adapters (the reference applies LoRA inside the projections,
     lora.py:107-113).
+
+    Prefill mode into a cache that already holds ``length`` positions (model.py:604-623): the
+    chunk attends to itself only (its own key mask, physical query indices from 0), its K/V are
+    written from slot ``length`` (ring slots modulo the window; a linear cache's start and the key
+    mask's are clamped into the capacity like ``lax.dynamic_update_slice``), and ``length``
+    grows by the chunk.
+
+    The caches are written in place, and the returned ``KVCache`` shares them. A later call on
+    the input ``KVCache`` object (its own ``length``) still computes what the reference computes
+    on it: an append at ``length`` overwrites the one slot this call wrote before anything reads it
+    (a ring slot's earlier position lies outside the window of every query from ``length`` on).
+    Only a caller that reads the input cache's arrays directly sees this call's writes.
 
     ``write_pos`` (append mode only): int32 ``[B]`` device tensor holding the physical slot of
     this step (``kv_cache.length``) for every row. The kernels then read the slot on the device
@@ -338,6 +368,9 @@ def forward_gemma4_text(
     if cache_mode == "append" and S != 1:
         raise ValueError(f'cache_mode="append" requires one token, got {S}')
     length = int(kv_cache.length)
+    capacity = kv_cache.key_mask.shape[1]
+    if S > capacity:
+        raise ValueError(f"{S} tokens do not fit a cache of {capacity} positions")
     if write_pos is not None:
         if cache_mode != "append":
             raise ValueError("write_pos is only used in append mode")
@@ -347,8 +380,10 @@ def forward_gemma4_text(
         slot = write_pos
     else:
         key_mask = kv_cache.key_mask.clone()
-        key_mask[:, length:length + S] = attention_mask
+        mask_start = min(max(length, 0), capacity - S)  # lax.dynamic_update_slice's clamp (model.py:602)
+        key_mask[:, mask_start:mask_start + S] = attention_mask
         slot = length
+    chunk_prefill = cache_mode == "prefill" and length != 0  # model.py:615-617: the chunk attends to itself
     if not fused_prologue:
         rot = {t: rotary_tables(pw.inv_freq[t], position_ids) for t in (SLIDING, FULL)}
     sources = kv_source_layers(config)
@@ -396,7 +431,7 @@ def forward_gemma4_text(
                 k = qkv[..., H * R * D: (H * R + H) * D].view(B, S, H, D)
                 v = qkv[..., (H * R + H) * D:].view(B, S, H, D) if pk.has_v else k
                 k_out = vt_out = None
-                if cache_mode == "prefill" and layer_cache.ring:
+                if cache_mode == "prefill" and (layer_cache.ring or chunk_prefill):
                     sp = slot_stride_for(S)
                     k_out = torch.empty(key_shape(B, H, sp, D), dtype=x.dtype, device=dev)
                     vt_out = torch.zeros((B, H, sp // 8, D, 8), dtype=x.dtype, device=dev)
@@ -410,13 +445,12 @@ def forward_gemma4_text(
                 src_cache = layer_cache
                 new_layers.append(layer_cache)
             if cache_mode == "prefill":
-                if length != 0:
-                    raise NotImplementedError("prefill into a non-empty cache is not supported")
                 if src in prompt_kv:
                     kk, vt = prompt_kv[src]
                 else:
                     kk, vt = src_cache.key, src_cache.value_t
-                attn = kernels.prefill_attention(q_out, kk, vt, key_mask, window=window)
+                attn = kernels.prefill_attention(q_out, kk, vt, attention_mask.contiguous() if chunk_prefill else key_mask,
+                                                 window=window)
             else:
                 attn = kernels.decode_attention(src_cache, q_out.view(B, H, R, D), key_mask, q_pos=slot,
                                                 window=config.sliding_window).view(B, 1, H, R, D)
@@ -463,9 +497,24 @@ def forward_gemma4_text(
     return hidden, KVCache(tuple(new_layers), key_mask, length + S)
 
 
+def checked_softcap(cap: float | None) -> float | None:
+    """``final_logit_softcapping`` as every LM-head path here applies it (``forward_lm_head``, the
+    graphed decode step's fused draw, ``generate``): None (no cap) or a positive finite float.
+    A cap of 0 or below would make the reference's ``tanh(x / cap) * cap`` (model.py:678-679) all
+    zeros or NaN; every path rejects it with the same ``ValueError`` instead."""
+
+    if cap is None:
+        return None
+    cap = float(cap)
+    if not (math.isfinite(cap) and cap > 0):
+        raise ValueError(f"final_logit_softcapping must be None or a positive finite number, got {cap}")
+    return cap
+
+
 def forward_lm_head(embed_tokens: torch.Tensor, hidden: torch.Tensor, softcap: float | None) -> torch.Tensor:
     """model.py:676-680: tied-embedding logits, ``tanh(x / cap) * cap``."""
 
+    softcap = checked_softcap(softcap)
     B, S, M = hidden.shape
     x = hidden.reshape(B * S, M)
     if x.is_cuda and kernels.lm_head_supported(x, embed_tokens):
@@ -507,6 +556,6 @@ def forward_gemma4_lm(
 __all__ = [
     "RMSNormParams", "AttentionParams", "MLPParams", "PerLayerInputParams", "DecoderLayerParams",
     "Gemma4TextParams", "Gemma4Output", "Gemma4TextConfig", "KVCache", "LayerKVCache", "init_kv_cache",
-    "forward_gemma4_text", "forward_gemma4_lm", "forward_lm_head", "params_from_numpy", "pack_weights",
+    "forward_gemma4_text", "forward_gemma4_lm", "forward_lm_head", "checked_softcap", "params_from_numpy", "pack_weights",
     "rms_norm", "layer_head_dim", "layer_kv_heads", "layer_has_v_proj", "layer_intermediate_size",
 ]

@@ -20,7 +20,7 @@ import torch
 from . import _lib, kernels
 from .config import Gemma4TextConfig
 from .kvcache import KVCache, init_kv_cache
-from .model import Gemma4Output, Gemma4TextParams, _proj, forward_gemma4_lm, forward_gemma4_text
+from .model import Gemma4Output, Gemma4TextParams, _proj, checked_softcap, forward_gemma4_lm, forward_gemma4_text
 
 
 class SamplerConfig(NamedTuple):
@@ -175,7 +175,7 @@ class GraphedDecodeStep:
                                         attention_mask=self.active[:, None], kv_cache=self.cache,
                                         cache_mode="append", write_pos=self.slot)
         head_in = hidden[:, -1]
-        cap = self.config.final_logit_softcapping
+        cap = checked_softcap(self.config.final_logit_softcapping)
         if kernels.lm_head_supported(head_in, self.params.embed_tokens):
             # the LM head with the draw in its epilogue: the [B, V] logits never reach HBM
             kernels.lm_head_sample(head_in, self.params.embed_tokens, softcap=cap, temperature=self.temperature,
@@ -234,6 +234,10 @@ class GraphedDecodeStep:
     @property
     def kv_cache(self) -> KVCache:
         return self.cache._replace(length=self.length)
+
+
+# Steps the generation loop may run ahead of the device's any-active flag when EOS ids are set.
+EOS_LAG = 4
 
 
 def _fused_sampling(sc: SamplerConfig, vocab: int) -> bool:
@@ -331,6 +335,7 @@ def generate(
         raise ValueError("temperature must be finite")
     if not math.isfinite(sc.top_p) or not 0 < sc.top_p <= 1:
         raise ValueError("top_p must be finite and in (0, 1]")
+    checked_softcap(config.final_logit_softcapping)
 
     prompt_mask = prompt_mask.to(torch.bool)
     out = prefill(params, config, prompt_ids, prompt_mask, max_new_tokens=sc.max_new_tokens, mesh=mesh, lora=lora)
@@ -355,6 +360,17 @@ def generate(
                                     key=key_state) if N > 1 else None
     else:
         graphed = GraphedDecodeStep(params, config, cache) if N > 1 else None
+    # With EOS ids the loop stops once no row is active (while_loop's cond, sampler.py:267-320).
+    # The device's any-active flag of each step is copied to pinned host memory behind the step's
+    # work, and the host reads the flag of EOS_LAG - 1 steps earlier, waiting only when it runs that
+    # far ahead of the device: the device always has queued steps, and the loop may run up to
+    # EOS_LAG - 1 steps past the last active one. Those steps change no output: every row is
+    # inactive, so g4_rollout_step writes pad / False / 0 into columns that already hold them, and
+    # the extra appends land in cache slots that generate never returns.
+    watch = eos.numel() > 0
+    if watch:
+        flags = torch.ones(EOS_LAG, dtype=torch.bool, pin_memory=True)
+        events = [torch.cuda.Event() for _ in range(EOS_LAG)]
     step = 0
     while step < N:
         if fused:
@@ -373,17 +389,20 @@ def generate(
                              next_pos=graphed.pos if decode_next else None,
                              next_mask=graphed.active if decode_next else None,
                              any_active=any_dev if eos.numel() else None)
-        # with EOS ids, whether a row is still active is the only host sync per step (while_loop's
-        # cond); without them no row finishes and the loop never waits on the device
-        any_active = bool(any_dev.item()) if eos.numel() else True
-        if decode_next and any_active:
+        if watch:
+            flags[step % EOS_LAG: step % EOS_LAG + 1].copy_(any_dev, non_blocking=True)
+            events[step % EOS_LAG].record()
+        if decode_next:
             if fused:
                 nxt = graphed.replay_sample()
             else:
                 logits = graphed.replay_logits()
         step += 1
-        if not any_active:
-            break
+        if watch and step >= EOS_LAG:
+            seen = step % EOS_LAG  # the flag written after step (step - 1) - (EOS_LAG - 1)
+            events[seen].synchronize()
+            if not bool(flags[seen]):
+                break
     lengths = completion_mask.sum(dim=-1, dtype=torch.int32)
     return RolloutBatch(prompt_ids, completion_ids.to(prompt_ids.dtype), completion_mask, rollout_logps, lengths)
 

@@ -665,7 +665,8 @@ def forward_text(params: Params, ids, position_ids, *, cfg: Config, attention_ma
         cache_length = None
     else:
         key_mask = kv_cache.key_mask.copy()
-        key_mask[:, kv_cache.length:kv_cache.length + S] = attention_mask
+        start = min(max(kv_cache.length, 0), key_mask.shape[1] - S)  # lax.dynamic_update_slice clamps (model.py:602)
+        key_mask[:, start:start + S] = attention_mask
         cache_length = kv_cache.length
     if kv_cache is not None and cache_mode == "append":
         if S != 1:

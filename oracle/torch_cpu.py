@@ -9,7 +9,9 @@ costs: bf16 tensors and bf16 matmuls (f32 accumulation), dense masked attention 
 cache capacity with full score tensors (model.py:496-499), f32 softmax, the per-layer op order of
 forward_decoder_layer (model.py:505-554), the full-vocab f32 log-softmax of _sample_token
 (sampler.py:151-159). Elementwise chains round after every torch op (torch's bf16 semantics; the
-numpy oracle rounds once per XLA-fused line), which changes no cost.
+numpy oracle rounds once per XLA-fused line), which changes no cost. The caches are held
+head-major, ``[B, H, C, D]``, so both attention products read them in place (the key operand as a
+transposed view): no per-layer copy of a cache, which makes the baseline faster, not slower.
 """
 
 from __future__ import annotations
@@ -50,7 +52,7 @@ class TorchCPUModel:
         self.inv_freq = {k: torch.from_numpy(v) for k, v in inv.items()}
 
     def init_cache(self, batch: int, capacity: int):
-        """model.py:557-568: [B, C_i, H, D] bf16 key / value per non-shared layer."""
+        """model.py:557-568: bf16 key / value per non-shared layer, head-major [B, H, C_i, D]."""
 
         cfg, layers = self.cfg, []
         for i in range(cfg.num_hidden_layers):
@@ -58,7 +60,7 @@ class TorchCPUModel:
                 layers.append(None)
                 continue
             c = min(cfg.sliding_window, capacity) if cfg.layer_types[i] == O.SLIDING else capacity
-            shape = (batch, c, O.layer_kv_heads(cfg, i), O.layer_head_dim(cfg, i))
+            shape = (batch, O.layer_kv_heads(cfg, i), c, O.layer_head_dim(cfg, i))
             layers.append([torch.zeros(shape, dtype=BF16), torch.zeros(shape, dtype=BF16)])
         return dict(layers=layers, key_mask=torch.zeros((batch, capacity), dtype=torch.bool), length=0)
 
@@ -129,16 +131,16 @@ def decode_step(model: TorchCPUModel, tokens: torch.Tensor, positions: torch.Ten
             k = _rope(_rms(k, lp["k_norm"], eps), *rots[lt])
             v = _rms(v, None, eps)
             kc, vc = cache["layers"][i]
-            slot = length % kc.shape[1] if lt == O.SLIDING else length
-            kc[:, slot] = k[:, 0]
-            vc[:, slot] = v[:, 0]
+            slot = length % kc.shape[2] if lt == O.SLIDING else length
+            kc[:, :, slot] = k[:, 0]
+            vc[:, :, slot] = v[:, 0]
             shared[lt] = (kc, vc)
         # dense attention over the whole capacity (model.py:496-499)
         qh = q[:, 0].permute(0, 2, 1, 3)  # [B, H, R, D]
-        scores = qh @ kc.permute(0, 2, 3, 1).contiguous()  # [B, H, R, T]
+        scores = qh @ kc.transpose(-1, -2)  # [B, H, R, T]
         scores = torch.where(masks[lt][:, None, None, :], scores, torch.full_like(scores, fill))
         probs = torch.softmax(scores.float(), -1).to(BF16)
-        attn = probs @ vc.permute(0, 2, 1, 3).contiguous()  # [B, H, R, D]
+        attn = probs @ vc  # [B, H, R, D]
         attn = attn.permute(0, 2, 1, 3).reshape(B, R * H * D)
         o = (attn @ lp["o"].reshape(R * H * D, M_)).reshape(B, 1, M_)
         x = residual + _rms(o, lp["post_attn"], eps)
@@ -164,20 +166,20 @@ def ring_decode_attention(q: torch.Tensor, cache_k: torch.Tensor, cache_v: torch
                           window: int) -> torch.Tensor:
     """One sliding-window layer's decode attention with its append (model.py:338-390, 496-499), per
     row b at position q_pos[b]: K/V stored at ring slot q_pos mod Wc, then dense masked attention
-    over every ring slot. q [B, R, H, D], caches [B, Wc, H, D] (updated in place), new_k / new_v
-    [B, H, D], key_mask [B, C] over absolute positions. Returns [B, R, H, D]."""
+    over every ring slot. q [B, R, H, D], caches head-major [B, H, Wc, D] (updated in place), new_k /
+    new_v [B, H, D], key_mask [B, C] over absolute positions. Returns [B, R, H, D]."""
 
-    B, Wc = cache_k.shape[:2]
+    B, Wc = cache_k.shape[0], cache_k.shape[2]
     rows = torch.arange(B)
     slot = q_pos.long() % Wc
-    cache_k[rows, slot] = new_k
-    cache_v[rows, slot] = new_v
+    cache_k[rows, :, slot] = new_k
+    cache_v[rows, :, slot] = new_v
     slots = torch.arange(Wc)[None, :]
     qp = q_pos.long()[:, None]
     pos = slots + torch.div(qp - slots, Wc, rounding_mode="floor") * Wc  # [B, Wc]
     valid = (pos >= 0) & (pos <= qp) & (pos > qp - window)
     valid &= torch.gather(key_mask, 1, pos.clamp(0, key_mask.shape[1] - 1))
-    scores = q.permute(0, 2, 1, 3) @ cache_k.permute(0, 2, 3, 1).contiguous()  # [B, H, R, Wc]
+    scores = q.permute(0, 2, 1, 3) @ cache_k.transpose(-1, -2)  # [B, H, R, Wc]
     scores = torch.where(valid[:, None, None, :], scores, torch.full_like(scores, torch.finfo(BF16).min))
     probs = torch.softmax(scores.float(), -1).to(BF16)
-    return (probs @ cache_v.permute(0, 2, 1, 3).contiguous()).permute(0, 2, 1, 3)
+    return (probs @ cache_v).permute(0, 2, 1, 3)

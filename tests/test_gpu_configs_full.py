@@ -118,6 +118,9 @@ def test_config4_prompt_append_is_bit_exact(config4, device):
                                   np_bits(v, O.BF16))
 
 
+MAX_F64_ROWS = 4  # of the 16,384 (query, head) rows of a pair
+
+
 @pytest.mark.parametrize("window", [0, 512])
 def test_config4_prefill_attention_full_size(config4, device, window):
     """Causal (global) and sliding(512) attention over the 4096-token prompts of all 8 rows on
@@ -125,7 +128,7 @@ def test_config4_prefill_attention_full_size(config4, device, window):
     left-padded row whose first 100 queries have no valid key. N(0, 1) q and k of dimension 256 give
     scores up to ~50, where one bf16 ulp is 0.25: each output row must match the oracle within 2e-2,
     or, where a score sits within f32 rounding of a bf16 boundary, the f64-accumulated oracle
-    (gpu_util.attention_rows; at most 1 % of the rows)."""
+    (gpu_util.attention_rows; at most MAX_F64_ROWS rows per pair)."""
 
     c = config4
     B, S, H, R, D = c["B"], c["S"], c["H"], c["R"], c["D"]
@@ -147,4 +150,4 @@ def test_config4_prefill_attention_full_size(config4, device, window):
         _say(f"config 4 window {window} pair ({b}, {h}): max |out - oracle| {err:.3g}; rows matching only the "
              f"f64-accumulated oracle {n64} of {S * R}; rows matching neither {bad}")
         assert bad == 0, f"pair ({b}, {h}): {bad} rows outside 2e-2 of both oracle evaluations"
-        assert n64 <= S * R // 100, f"pair ({b}, {h}): {n64} rows differ from the f32 oracle"
+        assert n64 <= MAX_F64_ROWS, f"pair ({b}, {h}): {n64} rows differ from the f32 oracle"

@@ -58,7 +58,7 @@ def e2b(device):
     torch.set_grad_enabled(False)
     cfg = C.config_from_hf(bench.E2B)
     ocfg = O.config_from_hf(bench.E2B)
-    params = bench.random_params(cfg, device, seed=0)
+    params = bench.random_params(cfg, device, seed=0, qk_norm=bench.E2B_QK_NORM)
     g = torch.Generator(device=device).manual_seed(5)
     ids = torch.randint(0, cfg.vocab_size, (B, P), device=device, generator=g, dtype=torch.int32)
     mask = torch.ones_like(ids, dtype=torch.bool)

@@ -142,3 +142,24 @@ def test_fused_back_to_back_calls(device):
 
     _draw_and_check(device, 256, 2048, 128, 1.0, 30.0, seed=21, key_words=(1, 2))
     _draw_and_check(device, 9, 2048, 128, 1.0, 30.0, seed=22, key_words=(1, 2))
+
+
+@pytest.mark.parametrize("temperature", [0.0, 1.0, 0.7])
+def test_fused_draw_takes_the_first_nan_column(device, temperature):
+    """jnp.argmax's rule (the greedy argmax and the one inside jax.random.categorical,
+    sampler.py:145-183): a NaN score beats every number and the first NaN column wins. Embedding
+    rows 7 and 3000 hold a NaN, so every row's logits there are NaN: every row draws column 7 with
+    a NaN log-probability, as the oracle's numpy argmax gives."""
+
+    B, V, M = 6, 4096, 128
+    x, e = _operands(device, B, V, M, seed=3)
+    e[7, 5] = float("nan")
+    e[3000, 9] = float("nan")
+    key = SMP.key_tensor([5, 6], device)
+    logits = torch.empty((B, V), dtype=torch.bfloat16, device=device)
+    tok, logp = kernels.lm_head_sample(x, e, softcap=30.0, temperature=temperature, key=key, logits_out=logits)
+    torch.cuda.synchronize()
+    assert tok.cpu().tolist() == [7] * B
+    assert torch.isnan(logp).all()
+    want_tok, _ = O.sample_token(_capped(logits, 30.0), temperature=temperature, key=JR.split(np.uint32([5, 6]))[1])
+    np.testing.assert_array_equal(tok.cpu().numpy(), want_tok)

@@ -52,6 +52,29 @@ def test_greedy_ties_take_the_first_column(device):
     np.testing.assert_allclose(logp[2].item(), -np.log(4099.0), atol=LOGP_ATOL)
 
 
+@pytest.mark.parametrize("width", [4096, 4099])
+@pytest.mark.parametrize("temperature", [0.0, 1.0])
+def test_nan_scores_take_the_first_nan_column(device, width, temperature):
+    """jnp.argmax's rule (sampler.py:145-183): a NaN beats every number and the first NaN column
+    wins, on both column paths (16-byte and strided). Row 1 holds NaNs at columns 50 and 9 (two
+    threads' columns, the later one met first by its thread), row 2 at 4095 only; row 0 has none.
+    Tokens as the oracle's numpy argmax gives, NaN log-probabilities on the NaN rows."""
+
+    rng = np.random.default_rng(4)
+    x = torch.from_numpy(rng.standard_normal((3, width)).astype(np.float32)).to(device).to(torch.bfloat16)
+    x[1, 50] = x[1, 9] = x[2, 4095] = float("nan")
+    key_words = JR.split(np.uint32([8, 9]))[1]
+    tok, logp = kernels.sample_tokens(x, softcap=30.0, temperature=temperature, key=_key(key_words, device),
+                                      split_key=False)
+    torch.cuda.synchronize()
+    capped = (torch.tanh(x.float() / 30.0) * 30.0).to(torch.bfloat16).float().cpu().numpy()
+    want, _ = O.sample_token(capped, temperature=temperature, key=key_words)
+    assert tok.cpu().tolist()[1:] == [9, 4095]
+    np.testing.assert_array_equal(tok.cpu().numpy(), want)
+    lp = logp.cpu().numpy()
+    assert np.isfinite(lp[0]) and np.isnan(lp[1:]).all()
+
+
 def test_greedy_ties_take_the_first_column_vectorized(device):
     """Rows of 8-column multiples take the 16-byte path (8 consecutive columns per thread and
     step): ties across threads, inside one thread's 8 columns, and an all-equal row."""
@@ -229,3 +252,34 @@ def test_rollout_step_bookkeeping(device, B, ids_dtype):
                          eos_ids=eos_t, any_active=anyd)
     assert not bool(anyd.item()) and not bool(active.any())
     np.testing.assert_array_equal(mask[:, 2].cpu().numpy(), act_np)
+
+
+def test_generate_with_eos_rows_finishing_at_different_steps_matches_oracle(device):
+    """sampler.py:267-320 with EOS ids: rows finish at different steps and the loop ends once none
+    is active (generate reads the device's flag a few steps behind, sampler.EOS_LAG). TINY_A f32 at
+    T = 1 with a set of 24 EOS ids: the completion ids, mask, lengths and logps equal the oracle's
+    generate under the same key (the oracle stops at the reference's step)."""
+
+    kw = H.TINY_A
+    hf = H.build_hf_model(kw, seed=0)
+    ocfg = O.config_from_hf(kw)
+    oparams = H.hf_to_params(hf, ocfg)
+    cfg = C.config_from_hf(kw)
+    params = M.params_from_numpy(oparams, cfg, dtype=torch.float32, device=device)
+    ids = np.random.default_rng(3).integers(3, 97, (6, 3)).astype(np.int32)
+    ids[1, 0] = 0
+    eos = tuple(range(4, 97, 4))
+    finished = []
+    for key in (5, 6, 7):
+        sc = SMP.SamplerConfig(3, 20, temperature=1.0, eos_ids=eos, seed=17)
+        rb = SMP.generate(params, cfg, torch.from_numpy(ids).to(device), torch.from_numpy(ids != 0).to(device),
+                          sampler_config=sc, key=key)
+        osc = O.SamplerConfig(3, 20, temperature=1.0, eos_ids=eos, seed=17)
+        orb = O.generate(oparams, ocfg, ids, ids != 0, sampler_config=osc, key=JR.prng_key(key))
+        np.testing.assert_array_equal(rb.completion_ids.cpu().numpy(), orb.completion_ids)
+        np.testing.assert_array_equal(rb.completion_mask.cpu().numpy(), orb.completion_mask)
+        np.testing.assert_array_equal(rb.lengths.cpu().numpy(), orb.lengths)
+        np.testing.assert_allclose(rb.rollout_logps.cpu().numpy(), orb.rollout_logps, rtol=0, atol=1e-5)
+        finished.append(int(orb.lengths.max()))
+    print("longest completion per key:", finished)
+    assert min(finished) < 20 - SMP.EOS_LAG  # at least one rollout ends early enough to exit the loop

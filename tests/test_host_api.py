@@ -72,3 +72,18 @@ def test_top_p_matches_the_oracle_on_random_rows():
         np.testing.assert_array_equal(ids.numpy(), order)
         sorted_scores = np.take_along_axis(s, order, axis=-1)
         np.testing.assert_array_equal(torch.isfinite(scores).numpy(), _oracle_keep(sorted_scores, top_p))
+
+
+def test_softcap_of_zero_or_below_is_rejected_on_every_path():
+    """One behaviour for a non-positive final_logit_softcapping: ValueError from the check every LM-head
+    path applies (forward_lm_head here; the graphed step and generate call the same check)."""
+
+    from gemma4_posttrain_jax_amd import model as M
+
+    e = torch.randn(16, 8)
+    h = torch.randn(1, 2, 8)
+    for cap in (0.0, -3.0, float("nan"), float("inf")):
+        with pytest.raises(ValueError, match="final_logit_softcapping"):
+            M.forward_lm_head(e, h, cap)
+    assert M.checked_softcap(None) is None and M.checked_softcap(30) == 30.0
+    np.testing.assert_allclose(M.forward_lm_head(e, h, None).numpy(), (h @ e.t()).numpy(), rtol=1e-6)

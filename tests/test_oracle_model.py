@@ -142,3 +142,46 @@ def test_bf16_mode_tracks_f32_mode():
     b, _, _ = O.forward_lm(p32, ids, pos, cfg=cfg, dtype=O.BF16)
     assert np.abs(a - b).max() < 0.1
     np.testing.assert_array_equal(b, O.bf16_round(b))
+
+
+def test_prefill_into_a_filled_cache_attends_to_the_chunk_only(tiny):
+    """model.py:604-623 with kv_cache.length > 0 in prefill mode: the chunk's attention uses its own
+    K/V and mask only (make_qk_masks over the chunk, query_start 0), so its hidden states equal the
+    cache-less forward of the chunk; its K/V land at slots length + s (ring: modulo the window,
+    only the last Wc kept), every other slot keeps its contents, and the key mask gains the chunk's
+    mask at length."""
+
+    _, params, cfg = tiny
+    rng = np.random.default_rng(9)
+    B, P0, S, C = 2, 5, 4, 16
+    cache = O.init_kv_cache(cfg, B, C, O.F32)
+    first = rng.integers(3, cfg.vocab_size, (B, P0))
+    _, _, cache = O.forward_lm(params, first, np.tile(np.arange(P0), (B, 1)), cfg=cfg,
+                               attention_mask=np.ones((B, P0), bool), kv_cache=cache, cache_mode="prefill")
+    chunk = rng.integers(3, cfg.vocab_size, (B, S))
+    cmask = np.array([[True] * S, [False] + [True] * (S - 1)])
+    cpos = P0 + np.tile(np.arange(S), (B, 1))
+    hidden, new = O.forward_text(params, chunk, cpos, cfg=cfg, attention_mask=cmask, kv_cache=cache,
+                                 cache_mode="prefill")
+    alone, _ = O.forward_text(params, chunk, cpos, cfg=cfg, attention_mask=cmask)
+    np.testing.assert_array_equal(hidden, alone)
+    fresh = O.init_kv_cache(cfg, B, S, O.F32)
+    _, chunk_cache = O.forward_text(params, chunk, cpos, cfg=cfg, attention_mask=cmask, kv_cache=fresh,
+                                    cache_mode="prefill")
+    for i, (old, got, ref) in enumerate(zip(cache.layers, new.layers, chunk_cache.layers)):
+        if old is None:
+            assert got is None
+            continue
+        ring = cfg.layer_types[i] == O.SLIDING
+        wc = old.key.shape[1]
+        keep = min(S, wc)
+        slots = [(P0 + s) % wc if ring else P0 + s for s in range(S - keep, S)]
+        # a fresh ring of min(W, S) slots holds the chunk's last tokens at slot s mod min(W, S)
+        src = [s % ref.key.shape[1] if ring else s for s in range(S - keep, S)]
+        np.testing.assert_array_equal(got.key[:, slots], ref.key[:, src])
+        np.testing.assert_array_equal(got.value[:, slots], ref.value[:, src])
+        others = [c for c in range(wc) if c not in slots]
+        np.testing.assert_array_equal(got.key[:, others], old.key[:, others])
+    np.testing.assert_array_equal(new.key_mask[:, P0:P0 + S], cmask)
+    np.testing.assert_array_equal(new.key_mask[:, :P0], cache.key_mask[:, :P0])
+    assert new.length == P0 + S

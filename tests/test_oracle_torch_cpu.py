@@ -33,8 +33,8 @@ def test_torch_cpu_decode_steps_track_the_oracle():
     cache = model.init_cache(B, P + N)
     for i, layer in enumerate(rc.layers):
         if layer is not None:
-            cache["layers"][i][0].copy_(torch.from_numpy(layer.key))
-            cache["layers"][i][1].copy_(torch.from_numpy(layer.value))
+            cache["layers"][i][0].copy_(torch.from_numpy(layer.key).transpose(1, 2))
+            cache["layers"][i][1].copy_(torch.from_numpy(layer.value).transpose(1, 2))
     cache["key_mask"].copy_(torch.from_numpy(rc.key_mask))
     cache["length"] = rc.length
     tok = logits[:, -1].argmax(-1).astype(np.int32)
@@ -47,8 +47,10 @@ def test_torch_cpu_decode_steps_track_the_oracle():
         tok = ref[:, -1].argmax(-1).astype(np.int32)
     for i, layer in enumerate(rc.layers):
         if layer is not None:
-            np.testing.assert_allclose(cache["layers"][i][0].float().numpy(), layer.key, atol=0.05, rtol=0)
-            np.testing.assert_allclose(cache["layers"][i][1].float().numpy(), layer.value, atol=0.05, rtol=0)
+            np.testing.assert_allclose(cache["layers"][i][0].transpose(1, 2).float().numpy(), layer.key, atol=0.05,
+                                       rtol=0)
+            np.testing.assert_allclose(cache["layers"][i][1].transpose(1, 2).float().numpy(), layer.value, atol=0.05,
+                                       rtol=0)
     assert cache["length"] == rc.length
 
 
@@ -73,9 +75,9 @@ def test_torch_cpu_ring_decode_attention_equals_the_oracle():
     def t(a):
         return torch.from_numpy(a).to(torch.bfloat16)
 
-    ck, cv = t(k), t(v)
+    ck, cv = t(k).transpose(1, 2).contiguous(), t(v).transpose(1, 2).contiguous()  # head-major
     got = T.ring_decode_attention(t(q[:, 0]), ck, cv, t(nk[:, 0]), t(nv[:, 0]),
                                   torch.from_numpy(pos.astype(np.int32)), torch.from_numpy(km), W)
     assert np.abs(got.float().numpy() - ref).max() <= 2e-2
-    np.testing.assert_array_equal(ck.float().numpy(), layer.key)
-    np.testing.assert_array_equal(cv.float().numpy(), layer.value)
+    np.testing.assert_array_equal(ck.transpose(1, 2).float().numpy(), layer.key)
+    np.testing.assert_array_equal(cv.transpose(1, 2).float().numpy(), layer.value)
