@@ -90,7 +90,8 @@ __device__ __forceinline__ void fused_append(const G4DecodeArgs& a, int pair, co
 #include "g4_decode_twopass.h"
 
 // ----------------------------------------------------------------------------------------------
-// f32, VALU
+// f32, VALU. Both products accumulate in f64 and round once to f32 (the exactly rounded dot
+// products up to one f64 rounding), as the f32 prefill kernel does.
 // ----------------------------------------------------------------------------------------------
 
 template <int D>
@@ -114,9 +115,10 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(G4DecodeArgs a, int t_a
   for (int key = tid; key < kr.n_keys; key += blockDim.x) {
     const bool valid = key_valid(a, b, kr, key);
     for (int r = 0; r < R; ++r) {
-      float s = 0.f;
-      for (int d = 0; d < D; ++d) s = fmaf(qh[r * D + d], key == kr.new_slot ? newk[d] : kbase[kt_index(key, d, D)], s);
-      sc[r * t_alloc + key] = valid ? s : kF32Min;
+      double s = 0.0;
+      for (int d = 0; d < D; ++d)
+        s = fma((double)qh[r * D + d], (double)(key == kr.new_slot ? newk[d] : kbase[kt_index(key, d, D)]), s);
+      sc[r * t_alloc + key] = valid ? (float)s : kF32Min;
     }
   }
   __syncthreads();
@@ -139,13 +141,13 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(G4DecodeArgs a, int t_a
   for (int idx = tid; idx < R * D; idx += blockDim.x) {
     const int r = idx / D, d = idx - r * D;
     const float m = stats[2 * r], l = all_masked ? (float)a.capacity : stats[2 * r + 1];
-    float o = 0.f;
+    double o = 0.0;
     for (int key = 0; key < n2; ++key) {
       const float p = all_masked ? 1.0f / l : expf(sc[r * t_alloc + key] - m) / l;
       const float v = key == kr.new_slot ? newv[d] : vbase[vt_index(key, d, D)];
-      o = fmaf(p, v, o);
+      o = fma((double)p, (double)v, o);
     }
-    out[idx] = o;
+    out[idx] = (float)o;
   }
 }
 

@@ -155,6 +155,9 @@ __global__ __launch_bounds__(kPrefillWaves * 64) void prefill_bf16_kernel(G4Pref
 }
 
 // f32 VALU kernel: one workgroup per (position, kv head, batch row); wave w owns heads w, w+4, ...
+// Both products accumulate in f64 and round once to f32 (the exactly rounded dot products up to one
+// f64 rounding): two f32 accumulation orders differ by more than the fp32 parity bar at the model
+// level, the exactly rounded result is the one every order approximates.
 template <int D>
 __global__ __launch_bounds__(256) void prefill_f32_kernel(G4PrefillArgs a, int t_alloc) {
   extern __shared__ float smem[];  // [4 waves][t_alloc] scores
@@ -171,9 +174,9 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(G4PrefillArgs a, int t
     const float* qrow = reinterpret_cast<const float*>(a.q) + ((((int64_t)b * S + pos) * H + h) * R + r) * D;
     float mx = kF32Min;
     for (int key = kmin + lane; key <= pos; key += 64) {
-      float s = 0.f;
-      for (int d = 0; d < D; ++d) s = fmaf(qrow[d], kbase[kt_index(key, d, D)], s);
-      s = km[key] ? s : kF32Min;
+      double acc = 0.0;
+      for (int d = 0; d < D; ++d) acc = fma((double)qrow[d], (double)kbase[kt_index(key, d, D)], acc);
+      const float s = km[key] ? (float)acc : kF32Min;
       sc[key - kmin] = s;
       mx = fmaxf(mx, s);
     }
@@ -186,12 +189,12 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(G4PrefillArgs a, int t
     const float lt = masked ? (float)S : l;
     float* orow = reinterpret_cast<float*>(a.out) + ((((int64_t)b * S + pos) * H + h) * R + r) * D;
     for (int d = lane; d < D; d += 64) {
-      float o = 0.f;
+      double o = 0.0;
       for (int key = k0; key <= k1; ++key) {
         const float p = masked ? 1.0f / lt : expf(sc[key - kmin] - mx) / lt;
-        o = fmaf(p, vbase[vt_index(key, d, D)], o);
+        o = fma((double)p, (double)vbase[vt_index(key, d, D)], o);
       }
-      orow[d] = o;
+      orow[d] = (float)o;
     }
   }
 }

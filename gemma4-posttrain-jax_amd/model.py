@@ -242,11 +242,24 @@ def _native_gate_up(h: torch.Tensor, w_t: torch.Tensor) -> bool:
             and w_t.is_contiguous())
 
 
+def _mm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``a @ b`` in a's dtype. bf16: hipBLASLt, f32 accumulation, one rounding. f32 (the parity
+    configs): the product accumulates in f64 and rounds once to f32, i.e. the exactly rounded dot
+    products up to one f64 rounding. Two f32 accumulation orders disagree by more than the 1e-5
+    fp32 bar at the model level (BASELINE config 1's logits: the oracle's f32 matmuls against its
+    f64-accumulated ones 2.7e-5, HF's torch-CPU f32 against the latter 4.1e-5); the exactly rounded
+    product is the one every order approximates."""
+
+    if a.dtype == torch.float32:
+        return (a.double() @ b.double()).float()
+    return a @ b
+
+
 def _proj(x: torch.Tensor, w_t: torch.Tensor) -> torch.Tensor:
     """``x [T, K] . w_t[N, K]^T`` in x's dtype (hipBLASLt; the [N, K] weight layout is its faster
     one for the prefill shapes and equal at decode)."""
 
-    return x @ w_t.t()
+    return _mm(x, w_t.t())
 
 
 # --- elementwise glue (PyTorch-ROCm ops, reference rounding points) ----------------------------------
@@ -287,7 +300,7 @@ def _per_layer_inputs(params: Gemma4TextParams, config: Gemma4TextConfig, ids: t
     token = params.embed_tokens_per_layer[ids]  # [B, S, L, P]
     scale = float(torch.tensor(math.sqrt(P), dtype=dt))  # sqrt(P) rounded to the activation dtype, on the host
     token = (token.float() * scale).to(dt)
-    ctx = (x.reshape(B * S, M) @ params.per_layer_model_projection.reshape(M, L * P)).reshape(B, S, L, P)
+    ctx = _mm(x.reshape(B * S, M), params.per_layer_model_projection.reshape(M, L * P)).reshape(B, S, L, P)
     ctx = (ctx.float() * (config.hidden_size ** -0.5)).to(dt)
     ctx = rms_norm(ctx, params.per_layer_projection_norm.weight, config.rms_norm_eps)
     return ((ctx.float() + token.float()).to(dt).float() * (2.0 ** -0.5)).to(dt)
@@ -482,9 +495,9 @@ def forward_gemma4_text(
         else:
             x, _ = kernels.residual_norm(d, lp.post_feedforward_norm.weight, x, scalar=None, next_weight=None,
                                          eps=eps, with_next=False)
-            g = x.reshape(B * S, -1) @ lp.per_layer_input.gate
+            g = _mm(x.reshape(B * S, -1), lp.per_layer_input.gate)
             g = (gelu_tanh_f32(g) * pli[:, :, i].reshape(B * S, -1).float()).to(x.dtype)
-            g = (g @ lp.per_layer_input.projection).reshape(B, S, -1)
+            g = _mm(g, lp.per_layer_input.projection).reshape(B, S, -1)
             g = rms_norm(g, lp.per_layer_input.post_norm.weight, eps)
             x = x + g
             x = (x.float() * lp.layer_scalar.float()).to(x.dtype)

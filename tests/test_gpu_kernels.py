@@ -124,6 +124,16 @@ def test_append_with_norms_and_q_matches_oracle(device, dtype, D):
 # --- decode attention -----------------------------------------------------------------------------
 
 
+def _attention_ref(q, k, v, mask, dtype):
+    """The oracle's attention core (model.py:496-499). fp32: with f64-accumulated products, as the
+    f32 kernels compute them (the exactly rounded dot products); bf16: f32 accumulation."""
+
+    if dtype == O.F32:
+        with O.accumulate_f64():
+            return O.attention_core(q, k, v, mask, dtype)
+    return O.attention_core(q, k, v, mask, dtype)
+
+
 def _decode_case(device, dtype, *, B, H, R, D, cap, ring, window, q_pos, key_mask, fused, seed, num_splits=0):
     rng = np.random.default_rng(seed)
     td = __import__("gpu_util").TORCH_DTYPE[dtype]
@@ -146,7 +156,7 @@ def _decode_case(device, dtype, *, B, H, R, D, cap, ring, window, q_pos, key_mas
     masks = O.make_cached_qk_masks(key_mask, window if ring else 1 << 30, q_pos, 1)
     mask = masks[O.SLIDING] if ring else masks[O.FULL]
     q_ref = q.transpose(0, 2, 1, 3)[:, None]  # [B, 1, R, H, D]
-    o_ref = O.attention_core(q_ref, ref_kv.key, ref_kv.value, mask, dtype)[:, 0].transpose(0, 2, 1, 3)
+    o_ref = _attention_ref(q_ref, ref_kv.key, ref_kv.value, mask, dtype)[:, 0].transpose(0, 2, 1, 3)
     got = to_np(out)
     err = np.abs(got - o_ref).max()
     assert err <= TOL[dtype], f"max |out - oracle| = {err}"
@@ -360,7 +370,7 @@ def test_prefill_matches_oracle(device, dtype, D, window):
                                     window=window)
     masks = O.make_qk_masks(key_mask, window if window else 1 << 30, 0, S)
     q_ref = q.transpose(0, 1, 3, 2, 4)  # [B, S, R, H, D]
-    o_ref = O.attention_core(q_ref, k, v, masks[O.SLIDING], dtype).transpose(0, 1, 3, 2, 4)
+    o_ref = _attention_ref(q_ref, k, v, masks[O.SLIDING], dtype).transpose(0, 1, 3, 2, 4)
     err = np.abs(to_np(out) - o_ref).max()
     assert err <= TOL[dtype], f"max |out - oracle| = {err}"
 
