@@ -453,7 +453,7 @@ def lm_head_passes(n: int = 3) -> None:
 
 
 def bench_e2b_generate(params, cfg, batch: int = 256, prompt: int = 256, new_tokens: int = 512,
-                       eos_ids: tuple = ()) -> dict:
+                       eos_ids: tuple = (), top_k: int = 0, top_p: float = 1.0) -> dict:
     """sampler.generate itself at configs[4] (B=256, P=256, N=512, T=1 full-vocab sampling), timed
     as the reference's harness times its compiled generate (scripts/benchmark_rollout.py:296-357):
     one untimed call, then one timed call from prompt ids to RolloutBatch (prefill, the HIP-graph
@@ -473,7 +473,7 @@ def bench_e2b_generate(params, cfg, batch: int = 256, prompt: int = 256, new_tok
     ids = torch.randint(0, cfg.vocab_size, (batch, prompt), device=dev, generator=g, dtype=torch.int32)
     mask = torch.ones_like(ids, dtype=torch.bool)
     sc = SMP.SamplerConfig(max_prompt_len=prompt, max_new_tokens=new_tokens, temperature=1.0, seed=3,
-                           eos_ids=tuple(eos_ids))
+                           eos_ids=tuple(eos_ids), top_k=top_k, top_p=top_p)
     SMP.generate(params, cfg, ids, mask, sampler_config=sc, key=1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -632,6 +632,13 @@ def main() -> int:
         # with EOS ids (every 64th vocab id: at T = 1 a row stops after ~64 tokens on average, the
         # longest after a few hundred), the GRPO caller's configuration (train_grpo.py:854-856)
         eos = bench_e2b_generate(e2b["params"], e2b["cfg"], eos_ids=tuple(range(1, e2b["cfg"].vocab_size, 64)))
+        tk = bench_e2b_generate(e2b["params"], e2b["cfg"], top_k=50)
+        assert tk["min_length"] == 512 and tk["output_semantics_ok"]
+        line["generate_top_k50_b256"] = {
+            "workload": "configs[4] generate at the reference harness's default draw: T = 1, top_k = 50 "
+                        "(scripts/benchmark_rollout.py:62-67), native top-k draw in the decode graph",
+            "s": round(tk["generate_s"], 3), "slot_tok_s": round(tk["slot_tok_s"], 1),
+            "amortized_step_ms": round(tk["amortized_step_ms"], 3)}
         line["generate_eos_b256"] = {
             "workload": "configs[4] generate with 4096 EOS ids (every 64th id), rows finishing at varied steps",
             "s": round(eos["generate_s"], 3), "decode_steps": eos["decode_steps"],

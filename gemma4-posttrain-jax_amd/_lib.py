@@ -81,6 +81,14 @@ class G4SampleArgs(ctypes.Structure):
     ]
 
 
+class G4SampleTopKArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32), ("batch", c_int32), ("vocab", c_int32), ("top_k", c_int32), ("logits", c_void_p),
+        ("row_stride", c_int64), ("softcap", c_float), ("temperature", c_float), ("top_p", c_float),
+        ("split_key", c_int32), ("key", c_void_p), ("token_out", c_void_p), ("logp_out", c_void_p),
+    ]
+
+
 class G4RolloutStepArgs(ctypes.Structure):
     _fields_ = [
         ("batch", c_int32), ("max_new", c_int32), ("step", c_int32), ("pad_id", c_int32), ("n_eos", c_int32),
@@ -127,6 +135,7 @@ PROTOTYPES = {
     "g4_kv_source_layers": (c_int32, [c_int32, c_int32, POINTER(c_int32), POINTER(c_int32)]),
     "g4_ring_slot_positions": (c_int32, [c_int32, c_int32, POINTER(c_int32)]),
     "g4_sample_tokens": (c_int32, [POINTER(G4SampleArgs), c_void_p]),
+    "g4_sample_top_k": (c_int32, [POINTER(G4SampleTopKArgs), c_void_p]),
     "g4_softcap_bf16": (c_int32, [c_int64, c_void_p, c_float, c_void_p, c_void_p]),
     "g4_lm_head_sample_workspace_size": (c_size_t, [POINTER(G4LmHeadSampleArgs)]),
     "g4_lm_head_sample": (c_int32, [POINTER(G4LmHeadSampleArgs), c_void_p]),

@@ -401,6 +401,34 @@ def sample_tokens(logits: torch.Tensor, *, softcap: float | None, temperature: f
     return token_out, logp_out
 
 
+TOP_K_MAX = 256  # the largest top_k g4_sample_top_k takes
+
+
+def sample_top_k(logits: torch.Tensor, *, softcap: float | None, temperature: float, top_k: int, top_p: float,
+                 key: torch.Tensor, split_key: bool = True, token_out: torch.Tensor | None = None,
+                 logp_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """g4_sample_top_k on ``[B, V]`` logits (bf16 or f32, rows may be strided): the top-k (+ top-p)
+    categorical draw of sampler.py:162-183 over ``capped logits / temperature`` (0 < top_k < V,
+    top_k <= TOP_K_MAX, temperature > 0), scored under the full f32 policy; ``key`` as in
+    sample_tokens. Returns ``(token int32 [B], logp f32 [B])``."""
+
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [B, V] with unit inner stride")
+    B, V = logits.shape
+    dev = logits.device
+    if key is None or key.dtype != torch.int32 or key.numel() != 2 or not key.is_contiguous() or key.device != dev:
+        raise ValueError("key must be a contiguous 2-element int32 tensor on the logits' device")
+    token_out = torch.empty(B, dtype=torch.int32, device=dev) if token_out is None else token_out
+    logp_out = torch.empty(B, dtype=torch.float32, device=dev) if logp_out is None else logp_out
+    a = _lib.G4SampleTopKArgs(
+        dtype=_code(logits), batch=B, vocab=V, top_k=int(top_k), logits=_ptr(logits), row_stride=logits.stride(0),
+        softcap=float(softcap or 0.0), temperature=float(temperature), top_p=float(top_p),
+        split_key=int(bool(split_key)), key=_ptr(key), token_out=_ptr(token_out), logp_out=_ptr(logp_out),
+    )
+    _lib.check(_lib.lib().g4_sample_top_k(ctypes.byref(a), _stream()), "g4_sample_top_k")
+    return token_out, logp_out
+
+
 def rollout_step(step: int, sampled: torch.Tensor, logp: torch.Tensor, active: torch.Tensor, *,
                  completion_ids: torch.Tensor, completion_mask: torch.Tensor, rollout_logps: torch.Tensor,
                  pad_id: int, eos_ids: torch.Tensor | None, prompt_lengths: torch.Tensor | None = None,

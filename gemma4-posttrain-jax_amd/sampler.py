@@ -137,7 +137,8 @@ class GraphedDecodeStep:
     """
 
     def __init__(self, params: Gemma4TextParams, config: Gemma4TextConfig, cache: KVCache, *,
-                 temperature: float | None = None, key: torch.Tensor | None = None) -> None:
+                 temperature: float | None = None, key: torch.Tensor | None = None, top_k: int = 0,
+                 top_p: float = 1.0) -> None:
         dev = cache.key_mask.device
         B = cache.key_mask.shape[0]
         self.params, self.config, self.cache = params, config, cache
@@ -149,6 +150,9 @@ class GraphedDecodeStep:
         if temperature is not None and temperature > 0 and key is None:
             raise ValueError("sampling in the graph needs the device key")
         self.temperature, self.key = temperature, key
+        self.top_k, self.top_p = top_k, top_p
+        if top_k and not _native_top_k(temperature or 0.0, top_k, top_p, config.vocab_size):
+            raise ValueError(f"top_k={top_k} is not a native in-graph draw (0 < top_k <= {kernels.TOP_K_MAX}, T > 0)")
         self.token_out = torch.zeros(B, dtype=torch.int32, device=dev)
         self.logp_out = torch.zeros(B, dtype=torch.float32, device=dev)
         saved_key = None if key is None else key.clone()
@@ -176,6 +180,15 @@ class GraphedDecodeStep:
                                         cache_mode="append", write_pos=self.slot)
         head_in = hidden[:, -1]
         cap = checked_softcap(self.config.final_logit_softcapping)
+        if self.top_k:
+            # top-k (+ top-p) draw over the raw LM head logits (the kernel applies the soft-cap)
+            if kernels.lm_head_supported(head_in, self.params.embed_tokens):
+                raw = kernels.lm_head(head_in.contiguous(), self.params.embed_tokens)
+            else:
+                raw = _proj(head_in, self.params.embed_tokens)
+            kernels.sample_top_k(raw, softcap=cap, temperature=self.temperature, top_k=self.top_k, top_p=self.top_p,
+                                 key=self.key, split_key=True, token_out=self.token_out, logp_out=self.logp_out)
+            return None
         if kernels.lm_head_supported(head_in, self.params.embed_tokens):
             # the LM head with the draw in its epilogue: the [B, V] logits never reach HBM
             kernels.lm_head_sample(head_in, self.params.embed_tokens, softcap=cap, temperature=self.temperature,
@@ -241,10 +254,18 @@ EOS_LAG = 4
 
 
 def _fused_sampling(sc: SamplerConfig, vocab: int) -> bool:
-    """No top-k / top-p truncation (the RL configuration): the draw runs over the whole row, so it
-    can end the captured decode graph."""
+    """Greedy, or no top-k / top-p truncation (the RL configuration): the draw runs over the whole
+    row, so it can end the captured decode graph (greedy ignores top-k / top-p, sampler.py:160-161)."""
 
-    return (sc.top_k <= 0 or sc.top_k >= vocab) and sc.top_p >= 1.0
+    return sc.temperature <= 0 or ((sc.top_k <= 0 or sc.top_k >= vocab) and sc.top_p >= 1.0)
+
+
+def _native_top_k(temperature: float, top_k: int, top_p: float, vocab: int) -> bool:
+    """A top-k draw (with or without top-p) that g4_sample_top_k runs on the device: T > 0 and
+    0 < top_k <= kernels.TOP_K_MAX below the vocabulary. top-p without top-k (a sort of the whole
+    row) stays a host-built proposal."""
+
+    return temperature > 0 and 0 < top_k < vocab and top_k <= kernels.TOP_K_MAX and 0 < top_p <= 1
 
 
 def _key_words(key, seed: int) -> list[int]:
@@ -292,6 +313,10 @@ def _proposal(logits32: torch.Tensor, temperature: float, top_k: int,
 
 def _draw(logits: torch.Tensor, key: torch.Tensor, *, temperature: float, top_k: int, top_p: float,
           split_key: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    if logits.is_cuda and _native_top_k(temperature, top_k, top_p, logits.shape[-1]):
+        x = logits if logits.dtype in (torch.bfloat16, torch.float32) and logits.stride(-1) == 1 else logits.float()
+        return kernels.sample_top_k(x, softcap=None, temperature=temperature, top_k=top_k, top_p=top_p, key=key,
+                                    split_key=split_key)
     logits32 = logits.float().contiguous()
     proposal, index = (None, None) if temperature <= 0 else _proposal(logits32, temperature, top_k, top_p)
     return kernels.sample_tokens(logits32, softcap=None, temperature=temperature, key=key, split_key=split_key,
@@ -354,10 +379,16 @@ def generate(
     logits = out.logits[:, -1].float()
     cache = out.kv_cache
     fused = _fused_sampling(sc, config.vocab_size)
-    if fused:  # first token from the prefill logits (already soft-capped), then one graph per step
-        nxt = kernels.sample_tokens(out.logits[:, -1], softcap=None, temperature=sc.temperature, key=key_state)
-        graphed = GraphedDecodeStep(params, config, cache, temperature=sc.temperature,
-                                    key=key_state) if N > 1 else None
+    top_k = sc.top_k if _native_top_k(sc.temperature, sc.top_k, sc.top_p, config.vocab_size) else 0
+    if fused or top_k:
+        # first token from the prefill logits (already soft-capped), then one graph per step that
+        # ends in the draw (the fused LM head sampler, or the LM head and the native top-k draw)
+        nxt = _draw(out.logits[:, -1], key_state, temperature=sc.temperature, top_k=top_k, top_p=sc.top_p,
+                    split_key=True) if top_k else kernels.sample_tokens(
+                        out.logits[:, -1], softcap=None, temperature=sc.temperature, key=key_state)
+        graphed = GraphedDecodeStep(params, config, cache, temperature=sc.temperature, key=key_state, top_k=top_k,
+                                    top_p=sc.top_p) if N > 1 else None
+        fused = True
     else:
         graphed = GraphedDecodeStep(params, config, cache) if N > 1 else None
     # With EOS ids the loop stops once no row is active (while_loop's cond, sampler.py:267-320).

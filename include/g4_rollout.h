@@ -294,6 +294,34 @@ typedef struct G4SampleArgs {
 int g4_sample_tokens(const G4SampleArgs* args, void* stream);
 
 /*
+ * g4_sample_top_k: the truncated branch of _sample_token (sampler.py:162-183) for 0 < top_k < vocab,
+ * top_k <= 256, temperature > 0: the scores s = soft-capped logit / temperature, the top_k largest in
+ * descending order (ties: the lower vocab id first, as lax.top_k), the top-p nucleus over them
+ * (top_p < 1; the first column always kept), then jax.random.categorical over the top_k columns
+ * (Gumbel noise of column j at flat index row * top_k + j) and the drawn column's vocab id; logp is
+ * the full unmodified policy's (full-vocab f32 log-softmax of the capped logits). Replaces the
+ * torch.sort proposal the host would otherwise build per step. The key as in G4SampleArgs
+ * (split_key: split in place after the draw, a second launch). One workgroup per row; no workspace.
+ */
+typedef struct G4SampleTopKArgs {
+  int32_t dtype;        /* of logits: G4_DTYPE_BF16 or G4_DTYPE_F32 */
+  int32_t batch;
+  int32_t vocab;
+  int32_t top_k;        /* 1 .. 256, < vocab */
+  const void* logits;   /* [batch, row_stride] */
+  int64_t row_stride;   /* elements, >= vocab */
+  float softcap;        /* 0 = none (logits already capped) */
+  float temperature;    /* > 0 */
+  float top_p;          /* (0, 1]; 1 = no nucleus cut */
+  int32_t split_key;    /* as G4SampleArgs.split_key */
+  uint32_t* key;        /* device [2] */
+  int32_t* token_out;   /* device [batch] */
+  float* logp_out;      /* device [batch] */
+} G4SampleTopKArgs;
+
+int g4_sample_top_k(const G4SampleTopKArgs* args, void* stream);
+
+/*
  * g4_softcap_bf16: out[i] = cast_bf16(tanh(x[i] / cap) * cap) over n bf16 values, the division,
  * tanh and multiply in f32 -- the soft-cap of forward_lm_head (model.py:676-680) as the samplers
  * apply it. cap finite and > 0; x and out 16-byte aligned (out may alias x).

@@ -44,7 +44,7 @@ def test_ctypes_structs_match_the_compiled_header(tmp_path):
     if cc is None:
         pytest.skip("no C compiler")
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
-    for st in (_lib.G4AppendArgs, _lib.G4DecodeArgs, _lib.G4PrefillArgs, _lib.G4SampleArgs,
+    for st in (_lib.G4AppendArgs, _lib.G4DecodeArgs, _lib.G4PrefillArgs, _lib.G4SampleArgs, _lib.G4SampleTopKArgs,
                _lib.G4LmHeadSampleArgs, _lib.G4LinearArgs, _lib.G4PrologueArgs, _lib.G4RolloutStepArgs):
         lines.append(f'printf("{st.__name__} size %zu\\n", sizeof({st.__name__}));')
         for f, _ in st._fields_:
@@ -412,4 +412,34 @@ def test_rollout_step_rejects_invalid_arguments(override, match):
     a = _rollout_step_args(**override)
     rc = _lib.lib().g4_rollout_step(ctypes.byref(a), None)
     assert rc == _lib.G4_ERR_INVALID
+    assert re.search(match, _lib.lib().g4_last_error().decode())
+
+
+def _top_k_args(**kw):
+    base = dict(dtype=_lib.G4_DTYPE_BF16, batch=4, vocab=1000, top_k=50, logits=16, row_stride=1000, softcap=30.0,
+                temperature=1.0, top_p=0.9, split_key=1, key=16, token_out=16, logp_out=16)
+    base.update(kw)
+    return _lib.G4SampleTopKArgs(**base)
+
+
+@pytest.mark.parametrize("override,match", [
+    (dict(dtype=3), "dtype"),
+    (dict(row_stride=999), "row_stride"),
+    (dict(batch=0), "batch"),
+    (dict(top_k=0), "top_k"),
+    (dict(top_k=1000), "top_k"),
+    (dict(top_k=257, vocab=4096, row_stride=4096), "top_k"),
+    (dict(temperature=0.0), "temperature"),
+    (dict(temperature=float("inf")), "temperature"),
+    (dict(top_p=0.0), "top_p"),
+    (dict(top_p=1.5), "top_p"),
+    (dict(softcap=-1.0), "softcap"),
+    (dict(key=None), "NULL"),
+    (dict(logits=None), "NULL"),
+    (dict(split_key=2), "split_key"),
+])
+def test_sample_top_k_rejects_invalid_arguments(override, match):
+    a = _top_k_args(**override)
+    rc = _lib.lib().g4_sample_top_k(ctypes.byref(a), None)
+    assert rc in (_lib.G4_ERR_INVALID, _lib.G4_ERR_UNSUPPORTED)
     assert re.search(match, _lib.lib().g4_last_error().decode())

@@ -284,3 +284,75 @@ def test_generate_with_eos_rows_finishing_at_different_steps_matches_oracle(devi
         finished.append(int(orb.lengths.max()))
     print("longest completion per key:", finished)
     assert min(finished) < 20 - SMP.EOS_LAG  # at least one rollout ends early enough to exit the loop
+
+
+def _top_k_case(device, B, V, temperature, top_k, top_p, *, dtype=torch.bfloat16, cap=30.0, scale=3.0, seed=0,
+                logits=None):
+    """g4_sample_top_k against the oracle's _sample_token (sampler.py:162-183) on the same capped
+    logits: tokens equal, logp within the reference's 2e-6; the loop key advanced to split(key)[0]."""
+
+    if logits is None:
+        rng = np.random.default_rng(seed)
+        logits = (rng.standard_normal((B, V)) * scale).astype(np.float32)
+    x = torch.from_numpy(logits).to(device).to(dtype)
+    words = [seed + 3, 77]
+    key = _key(words, device)
+    tok, logp = kernels.sample_top_k(x, softcap=cap, temperature=temperature, top_k=top_k, top_p=top_p, key=key)
+    torch.cuda.synchronize()
+    xf = x.float()
+    capped = xf if cap is None else (torch.tanh(xf / cap) * cap).to(dtype).float()
+    nxt, sub = JR.split(np.uint32(words))
+    want_tok, want_logp = O.sample_token(capped.cpu().numpy(), temperature=temperature, top_k=top_k, top_p=top_p,
+                                         key=sub)
+    np.testing.assert_array_equal(tok.cpu().numpy(), want_tok)
+    np.testing.assert_allclose(logp.cpu().numpy(), want_logp, rtol=0, atol=LOGP_ATOL)
+    assert _words(key) == nxt.tolist()
+    return tok
+
+
+@pytest.mark.parametrize("B,V,temperature,top_k,top_p,dtype,cap", [
+    (7, 97, 1.0, 7, 1.0, torch.float32, None),
+    (64, 1000, 0.8, 1, 1.0, torch.bfloat16, 30.0),
+    (64, 1000, 0.8, 50, 0.9, torch.bfloat16, 30.0),
+    (33, 4099, 1.3, 256, 0.5, torch.float32, 30.0),
+    (16, 32768, 1.0, 64, 0.95, torch.bfloat16, None),
+    (256, 262144, 1.0, 50, 1.0, torch.bfloat16, 30.0),
+    (256, 262144, 0.7, 50, 0.9, torch.bfloat16, 30.0),
+])
+def test_native_top_k_matches_oracle(device, B, V, temperature, top_k, top_p, dtype, cap):
+    """Vocabularies from TINY_A's 97 to the E2B shape's 262,144 columns (the reference harness's
+    default draw: T = 1, top_k = 50, scripts/benchmark_rollout.py:62-67), k from 1 to the kernel's
+    largest 256, with and without top-p, bf16 and f32 logits, with and without the soft-cap."""
+
+    _top_k_case(device, B, V, temperature, top_k, top_p, dtype=dtype, cap=cap, seed=B + V)
+
+
+def test_native_top_k_ties_take_the_lower_ids(device):
+    """Ties as lax.top_k breaks them (the lower vocab id first): an all-equal row (every column
+    ties at the k-th value: the exact-threshold path), a row whose k-th value repeats across the
+    cut, bf16 rows with many equal values, and +0.0 / -0.0 as equal scores."""
+
+    V = 5000
+    logits = np.zeros((6, V), np.float32)
+    logits[1, ::7] = 1.0  # 715 equal maxima: the top 40 are the first 40 of them
+    logits[2] = np.round(np.random.default_rng(1).standard_normal(V) * 2) / 2  # coarse values: many ties
+    logits[3, :100] = -0.0
+    logits[3, 100:] = -1.0  # +0.0 and -0.0 tie: the first k ids of the zeros
+    logits[4, 4000:] = 3.0  # 1000 equal maxima at high ids
+    logits[5] = np.random.default_rng(2).standard_normal(V)
+    tok = _top_k_case(device, 6, V, 1.0, 40, 1.0, dtype=torch.float32, cap=None, logits=logits)
+    t = tok.cpu().numpy()
+    assert t[0] < 40 and t[1] % 7 == 0 and t[1] < 7 * 40 and t[3] < 40 and 4000 <= t[4] < 4040
+    _top_k_case(device, 6, V, 0.9, 7, 0.6, dtype=torch.float32, cap=None, logits=logits, seed=5)
+
+
+def test_native_top_k_draw_distribution(device):
+    """The reference's top-k distribution case (tests/test_sampler.py:175-205): 8192 copies of the
+    two rows, PRNGKey(128); the tokens equal the oracle's, whose frequencies the CPU suite checks
+    against transformers' top-k warper."""
+
+    values = np.repeat(LOGITS, 8192, axis=0)
+    tok, logp = SMP._sample_token(torch.from_numpy(values).to(device), 128, temperature=0.8, top_k=3, top_p=1.0)
+    want_tok, want_logp = O.sample_token(values, temperature=0.8, top_k=3, top_p=1.0, key=JR.prng_key(128))
+    np.testing.assert_array_equal(tok.cpu().numpy(), want_tok)
+    np.testing.assert_allclose(logp.cpu().numpy(), want_logp, rtol=0, atol=LOGP_ATOL)
