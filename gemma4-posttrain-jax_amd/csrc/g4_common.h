@@ -124,6 +124,22 @@ __device__ __forceinline__ float gelu_tanh_mul(float g, float u) {
   return 0.5f * g * (1.0f + tanhf(inner)) * u;
 }
 
+// exp(x) of an f32 value evaluated in f64 and rounded once to f32 (the f32 kernels' softmax).
+__device__ __forceinline__ float exp_f32_exact(float x) { return (float)exp((double)x); }
+
+// gelu_tanh(g) * u of an f32 model, each f32 operation of jax.nn.gelu(approximate=True) rounded
+// once in its own order, x * (0.5 * (1 + tanh(c * (x + 0.044715 * ((x * x) * x))))), with tanh
+// evaluated in f64 (the exactly rounded evaluation the fp32 parity configs are checked against).
+__device__ __forceinline__ float gelu_tanh_mul_exact(float g, float u) {
+#pragma clang fp contract(off)
+  const float kBeta = 0.7978845608028654f;  // sqrt(2 / pi) rounded to f32
+  const float x3 = (g * g) * g;
+  const float inner = kBeta * (g + 0.044715f * x3);
+  const float th = (float)tanh((double)inner);
+  const float gel = g * (0.5f * (1.0f + th));
+  return gel * u;
+}
+
 // 16-byte LDS read issued from inline assembly, for operand tiles that buffer_load ... lds fills:
 // the compiler does not see the read, so it adds no wait for DMAs in flight into other buffers (it
 // cannot always tell them apart and then waits for all of them). The caller orders the read after

@@ -91,7 +91,8 @@ __device__ __forceinline__ void fused_append(const G4DecodeArgs& a, int pair, co
 
 // ----------------------------------------------------------------------------------------------
 // f32, VALU. Both products accumulate in f64 and round once to f32 (the exactly rounded dot
-// products up to one f64 rounding), as the f32 prefill kernel does.
+// products up to one f64 rounding), and the softmax's exponentials and sum are evaluated in f64
+// and rounded once, as the f32 prefill kernel does.
 // ----------------------------------------------------------------------------------------------
 
 template <int D>
@@ -126,12 +127,12 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(G4DecodeArgs a, int t_a
     float mx = kF32Min;
     for (int key = lane; key < kr.n_keys; key += 64) mx = fmaxf(mx, sc[r * t_alloc + key]);
     mx = wave_max(mx);
-    float l = 0.f;
-    for (int key = lane; key < kr.n_keys; key += 64) l += expf(sc[r * t_alloc + key] - mx);
-    l = wave_sum(l);
+    double l = 0.0;  // the softmax sum in f64 of the f32 exponentials, rounded once
+    for (int key = lane; key < kr.n_keys; key += 64) l += (double)exp_f32_exact(sc[r * t_alloc + key] - mx);
+    for (int m = 32; m >= 1; m >>= 1) l += __shfl_xor(l, m, 64);
     if (lane == 0) {
       stats[2 * r] = mx;
-      stats[2 * r + 1] = l;
+      stats[2 * r + 1] = (float)l;
     }
   }
   __syncthreads();
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(G4DecodeArgs a, int t_a
     const float m = stats[2 * r], l = all_masked ? (float)a.capacity : stats[2 * r + 1];
     double o = 0.0;
     for (int key = 0; key < n2; ++key) {
-      const float p = all_masked ? 1.0f / l : expf(sc[r * t_alloc + key] - m) / l;
+      const float p = all_masked ? 1.0f / l : exp_f32_exact(sc[r * t_alloc + key] - m) / l;
       const float v = key == kr.new_slot ? newv[d] : vbase[vt_index(key, d, D)];
       o = fma((double)p, (double)v, o);
     }

@@ -13,6 +13,10 @@
 #include "g4_common.h"
 #include "g4_internal.h"
 
+// Products and sums stay separate roundings (no multiply-add contraction), as in the reference's
+// elementwise ops; the f32 paths evaluate the norm's sum of squares and x^-0.5 in f64, rounded once.
+#pragma clang fp contract(off)
+
 namespace g4 {
 namespace {
 
@@ -31,19 +35,49 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return s;
 }
 
-// x * (mean(x^2) + eps)^-0.5 * w over the row held in v[] (column c = threadIdx.x + 256 * i)
+__device__ __forceinline__ double block_sum_f64(double v, double* red) {
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < kFuseThreads / 64; ++i) s += red[i];
+  return s;
+}
+
+// x * (mean(x^2) + eps)^-0.5 * w over the row held in v[] (column c = threadIdx.x + 256 * i).
+// f32 (the parity configs): every f32 operation of the reference's formula rounded once: the
+// squares, their sum (f64, then f32), / cols, + eps, x^-0.5 (f64, then f32), * r, * w.
 template <bool BF16>
 __device__ __forceinline__ void norm_row(float (&v)[kFuseMaxPerThread], int cols, const void* weight, float eps,
                                          float* red) {
   using E = Elem<BF16>;
-  float ss = 0.f;
+  float inv;
+  if constexpr (BF16) {
+    float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < kFuseMaxPerThread; ++i) {
-    const int c = threadIdx.x + kFuseThreads * i;
-    if (c < cols) ss += v[i] * v[i];
+    for (int i = 0; i < kFuseMaxPerThread; ++i) {
+      const int c = threadIdx.x + kFuseThreads * i;
+      if (c < cols) ss += v[i] * v[i];
+    }
+    const float ms = block_sum(ss, red) / (float)cols;
+    inv = 1.0f / sqrtf(ms + eps);
+  } else {
+    __shared__ double red64[kFuseThreads / 64];
+    double ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < kFuseMaxPerThread; ++i) {
+      const int c = threadIdx.x + kFuseThreads * i;
+      if (c < cols) {
+        const float sq = v[i] * v[i];
+        ss += (double)sq;
+      }
+    }
+    const float ms = (float)block_sum_f64(ss, red64) / (float)cols;
+    inv = (float)(1.0 / sqrt((double)(ms + eps)));
   }
-  const float ms = block_sum(ss, red) / (float)cols;
-  const float inv = 1.0f / sqrtf(ms + eps);
 #pragma unroll
   for (int i = 0; i < kFuseMaxPerThread; ++i) {
     const int c = threadIdx.x + kFuseThreads * i;
@@ -124,7 +158,7 @@ __global__ __launch_bounds__(kFuseThreads) void gelu_mul_kernel(int64_t n, int c
     const int64_t row = i / cols, c = i - row * cols;
     const float g = E::load(reinterpret_cast<const T*>(gate_up), row * 2 * cols + c);
     const float u = E::load(reinterpret_cast<const T*>(gate_up), row * 2 * cols + cols + c);
-    E::store(reinterpret_cast<T*>(out), i, gelu_tanh_mul(g, u));
+    E::store(reinterpret_cast<T*>(out), i, BF16 ? gelu_tanh_mul(g, u) : gelu_tanh_mul_exact(g, u));
   }
 }
 

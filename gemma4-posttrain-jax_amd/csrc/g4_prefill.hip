@@ -156,8 +156,9 @@ __global__ __launch_bounds__(kPrefillWaves * 64) void prefill_bf16_kernel(G4Pref
 
 // f32 VALU kernel: one workgroup per (position, kv head, batch row); wave w owns heads w, w+4, ...
 // Both products accumulate in f64 and round once to f32 (the exactly rounded dot products up to one
-// f64 rounding): two f32 accumulation orders differ by more than the fp32 parity bar at the model
-// level, the exactly rounded result is the one every order approximates.
+// f64 rounding), and the softmax's exponentials and sum are evaluated in f64 and rounded once: two
+// f32 evaluation orders differ by more than the fp32 parity bar at the model level, the exactly
+// rounded result is the one every order approximates.
 template <int D>
 __global__ __launch_bounds__(256) void prefill_f32_kernel(G4PrefillArgs a, int t_alloc) {
   extern __shared__ float smem[];  // [4 waves][t_alloc] scores
@@ -181,9 +182,10 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(G4PrefillArgs a, int t
       mx = fmaxf(mx, s);
     }
     mx = wave_max(mx);
-    float l = 0.f;
-    for (int key = kmin + lane; key <= pos; key += 64) l += expf(sc[key - kmin] - mx);
-    l = wave_sum(l);
+    double l64 = 0.0;  // the softmax sum in f64 of the f32 exponentials, rounded once
+    for (int key = kmin + lane; key <= pos; key += 64) l64 += (double)exp_f32_exact(sc[key - kmin] - mx);
+    for (int m = 32; m >= 1; m >>= 1) l64 += __shfl_xor(l64, m, 64);
+    const float l = (float)l64;
     const bool masked = mx == kF32Min;
     const int k0 = masked ? 0 : kmin, k1 = masked ? S - 1 : pos;
     const float lt = masked ? (float)S : l;
@@ -191,7 +193,7 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(G4PrefillArgs a, int t
     for (int d = lane; d < D; d += 64) {
       double o = 0.0;
       for (int key = k0; key <= k1; ++key) {
-        const float p = masked ? 1.0f / lt : expf(sc[key - kmin] - mx) / lt;
+        const float p = masked ? 1.0f / lt : exp_f32_exact(sc[key - kmin] - mx) / lt;
         o = fma((double)p, (double)vbase[vt_index(key, d, D)], o);
       }
       orow[d] = (float)o;

@@ -104,12 +104,27 @@ __device__ __forceinline__ void prep_math(PrepIn<BF16, D>& in, bool norm, bool h
   constexpr int PARTNER = D >= 64 ? 32 : D / 2;
   const int lane = threadIdx.x & 63;
   if (norm) {
-    // forward_rms_norm (model.py:278-285): f32 statistics, x * (mean(x^2) + eps)^-0.5 * w.
-    float ss = 0.f;
+    // forward_rms_norm (model.py:278-285): f32 statistics, x * (mean(x^2) + eps)^-0.5 * w. f32
+    // vectors (the parity configs): each f32 operation rounded once, the sum of the squares and
+    // x^-0.5 evaluated in f64.
+#pragma clang fp contract(off)
+    float inv;
+    if constexpr (BF16) {
+      float ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < PER; ++e) ss += in.x[e] * in.x[e];
-    ss = wave_sum(ss);
-    const float inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
+      for (int e = 0; e < PER; ++e) ss += in.x[e] * in.x[e];
+      ss = wave_sum(ss);
+      inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
+    } else {
+      double ss = 0.0;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const float sq = in.x[e] * in.x[e];
+        ss += (double)sq;
+      }
+      for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+      inv = (float)(1.0 / sqrt((double)((float)ss / (float)D + eps)));
+    }
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
       float y = in.x[e] * inv;

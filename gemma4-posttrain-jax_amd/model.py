@@ -266,24 +266,42 @@ def _proj(x: torch.Tensor, w_t: torch.Tensor) -> torch.Tensor:
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.Tensor:
-    """model.py:278-285: f32 ``x * (mean(x^2) + eps)^-0.5 * w``, cast back to x's dtype."""
+    """model.py:278-285: f32 ``x * (mean(x^2) + eps)^-0.5 * w``, cast back to x's dtype. f32 x: each
+    f32 operation rounded once, the sum of the squares and x^-0.5 evaluated in f64 (the native
+    norms' f32 path)."""
 
     x32 = x.float()
+    if x.dtype == torch.float32:
+        ms = (x32 * x32).double().sum(-1, keepdim=True).float() / x.shape[-1]
+        y = x32 * (1.0 / (ms + eps).double().sqrt()).float()
+        return y * weight.float() if weight is not None else y
     y = x32 * torch.pow(x32.square().mean(-1, keepdim=True) + eps, -0.5)
     if weight is not None:
         y = y * weight.float()
     return y.to(x.dtype)
 
 
-def gelu_tanh_f32(x: torch.Tensor) -> torch.Tensor:
-    return torch.nn.functional.gelu(x.float(), approximate="tanh")
+def gelu_tanh_f32(x: torch.Tensor, exact: bool = False) -> torch.Tensor:
+    """jax.nn.gelu(approximate=True) in f32. ``exact``: its own op order,
+    ``x * (0.5 * (1 + tanh(c * (x + 0.044715 * ((x * x) * x)))))``, each op rounded to f32 and tanh
+    evaluated in f64 (the fp32 parity configs)."""
+
+    x = x.float()
+    if exact:
+        inner = math.sqrt(2.0 / math.pi) * (x + 0.044715 * ((x * x) * x))
+        return x * (0.5 * (1.0 + torch.tanh(inner.double()).float()))
+    return torch.nn.functional.gelu(x, approximate="tanh")
 
 
-def rotary_tables(inv_freq: torch.Tensor, position_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """model.py:288-291: f32 cos/sin ``[B, S, D]`` of ``concat(f, f)``, f = pos * inv_freq."""
+def rotary_tables(inv_freq: torch.Tensor, position_ids: torch.Tensor,
+                  exact: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """model.py:288-291: f32 cos/sin ``[B, S, D]`` of ``concat(f, f)``, f = pos * inv_freq
+    (``exact``: cos / sin evaluated in f64 and rounded once, for f32 models)."""
 
     freqs = position_ids.float()[..., None] * inv_freq[None, None, :]
     emb = torch.cat([freqs, freqs], dim=-1)
+    if exact:
+        return torch.cos(emb.double()).float().contiguous(), torch.sin(emb.double()).float().contiguous()
     return torch.cos(emb).contiguous(), torch.sin(emb).contiguous()
 
 
@@ -398,7 +416,8 @@ def forward_gemma4_text(
         slot = length
     chunk_prefill = cache_mode == "prefill" and length != 0  # model.py:615-617: the chunk attends to itself
     if not fused_prologue:
-        rot = {t: rotary_tables(pw.inv_freq[t], position_ids) for t in (SLIDING, FULL)}
+        exact = x.dtype == torch.float32
+        rot = {t: rotary_tables(pw.inv_freq[t], position_ids, exact) for t in (SLIDING, FULL)}
     sources = kv_source_layers(config)
 
     flags_q = _lib.G4_APPEND_NORM_Q | _lib.G4_APPEND_ROPE_Q
@@ -496,7 +515,7 @@ def forward_gemma4_text(
             x, _ = kernels.residual_norm(d, lp.post_feedforward_norm.weight, x, scalar=None, next_weight=None,
                                          eps=eps, with_next=False)
             g = _mm(x.reshape(B * S, -1), lp.per_layer_input.gate)
-            g = (gelu_tanh_f32(g) * pli[:, :, i].reshape(B * S, -1).float()).to(x.dtype)
+            g = (gelu_tanh_f32(g, x.dtype == torch.float32) * pli[:, :, i].reshape(B * S, -1).float()).to(x.dtype)
             g = _mm(g, lp.per_layer_input.projection).reshape(B, S, -1)
             g = rms_norm(g, lp.per_layer_input.post_norm.weight, eps)
             x = x + g
@@ -539,6 +558,8 @@ def forward_lm_head(embed_tokens: torch.Tensor, hidden: torch.Tensor, softcap: f
     if softcap is not None:
         if logits.dtype == torch.bfloat16 and logits.is_cuda and logits.is_contiguous():
             logits = kernels.softcap(logits, softcap, out=logits)  # one native pass, the same bits
+        elif logits.dtype == torch.float32:  # tanh in f64, rounded once; the division and product in f32
+            logits = torch.tanh((logits / softcap).double()).float() * softcap
         else:
             logits = (torch.tanh(logits.float() / softcap) * softcap).to(logits.dtype)
     return logits

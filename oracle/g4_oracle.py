@@ -310,6 +310,21 @@ class accumulate_f64:
         _ACCUMULATE.pop()
 
 
+def exact_f32(dtype: str) -> bool:
+    """Under ``accumulate_f64`` an f32 model is evaluated exactly rounded: besides the products,
+    every reduction (the norms' sums of squares, the softmax sums) is summed in f64 and rounded
+    once, and every transcendental (exp, tanh, x^-0.5, cos, sin) is evaluated in f64 and rounded
+    once, while the reference's single IEEE operations (+, -, *, /) round to f32 one at a time in
+    its own order. Every f32 evaluation order (XLA's, numpy's, torch's) lies within its own rounding
+    noise of this one; the native fp32 path computes it too. bf16 models keep the f32 evaluation."""
+
+    return dtype == F32 and _ACCUMULATE[-1] is np.float64
+
+
+def _f32(x) -> np.ndarray:
+    return np.asarray(x, np.float64).astype(np.float32)
+
+
 def matmul(x: np.ndarray, w: np.ndarray, dtype: str) -> np.ndarray:
     """f32-accumulated product rounded once to ``dtype`` (an einsum / ``@`` in the reference)."""
 
@@ -328,6 +343,12 @@ def rms_norm(weight: np.ndarray | None, x: np.ndarray, eps: float, dtype: str) -
     Pinned against HF ``Gemma4RMSNorm`` (test_oracle_model.py) and the closed form on constants."""
 
     x32 = x.astype(np.float32)
+    if exact_f32(dtype):  # square, sum (f64, one rounding), / n, + eps, ^-0.5 (f64), * r, * w
+        sq = x32 * x32
+        ms = _f32(sq.astype(np.float64).sum(axis=-1, keepdims=True)) / np.float32(x.shape[-1])
+        r = _f32(1.0 / np.sqrt((ms + np.float32(eps)).astype(np.float64)))
+        y = x32 * r
+        return y * weight.astype(np.float32) if weight is not None else y
     ms = np.mean(np.square(x32), axis=-1, keepdims=True, dtype=np.float32)
     y = x32 * np.power(ms + np.float32(eps), np.float32(-0.5), dtype=np.float32)
     if weight is not None:
@@ -353,17 +374,22 @@ def rope_inv_freq(cfg: Config) -> dict:
     return {SLIDING: inv_sliding, FULL: inv_full}
 
 
-def rotary_values(inv_freq: np.ndarray, position_ids: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-    """model.py:288-291: ``emb = concat(f, f)``, f = pos * inv_freq; f32 cos/sin ``[B, S, D]``."""
+def rotary_values(inv_freq: np.ndarray, position_ids: np.ndarray, exact: bool = False) -> tuple[np.ndarray, np.ndarray]:
+    """model.py:288-291: ``emb = concat(f, f)``, f = pos * inv_freq; f32 cos/sin ``[B, S, D]``
+    (``exact``: cos / sin in f64, rounded once)."""
 
     freqs = position_ids.astype(np.float32)[..., None] * inv_freq[None, None, :]
     emb = np.concatenate([freqs, freqs], axis=-1).astype(np.float32)
+    if exact:
+        e64 = emb.astype(np.float64)
+        return _f32(np.cos(e64)), _f32(np.sin(e64))
     return np.cos(emb).astype(np.float32), np.sin(emb).astype(np.float32)
 
 
-def make_rotary(cfg: Config, position_ids: np.ndarray) -> dict:
+def make_rotary(cfg: Config, position_ids: np.ndarray, dtype: str | None = None) -> dict:
     inv = rope_inv_freq(cfg)
-    return {t: rotary_values(inv[t], position_ids) for t in (SLIDING, FULL)}
+    exact = dtype is not None and exact_f32(dtype)
+    return {t: rotary_values(inv[t], position_ids, exact) for t in (SLIDING, FULL)}
 
 
 def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, dtype: str) -> np.ndarray:
@@ -382,10 +408,16 @@ def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, dtype: str) -> np.ndar
     return cast(x32 * c + rotated * s, dtype)
 
 
-def gelu_tanh(x: np.ndarray) -> np.ndarray:
-    """jax.nn.gelu(approximate=True) in f32 (model.py:396)."""
+def gelu_tanh(x: np.ndarray, exact: bool = False) -> np.ndarray:
+    """jax.nn.gelu(approximate=True) in f32 (model.py:396). ``exact``: its own op order,
+    ``x * (0.5 * (1 + tanh(c * (x + 0.044715 * ((x * x) * x)))))``, each op rounded to f32 and
+    tanh evaluated in f64."""
 
     x = x.astype(np.float32)
+    if exact:
+        u = x + np.float32(0.044715) * ((x * x) * x)
+        th = _f32(np.tanh((np.float32(math.sqrt(2.0 / math.pi)) * u).astype(np.float64)))
+        return x * (np.float32(0.5) * (np.float32(1.0) + th))
     inner = np.float32(math.sqrt(2.0 / math.pi)) * (x + np.float32(0.044715) * x * x * x)
     return (np.float32(0.5) * x * (np.float32(1.0) + np.tanh(inner))).astype(np.float32)
 
@@ -545,8 +577,12 @@ def attention_core(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask: np.ndarray
         sc = cast(np.matmul(qt[:, :, :, s0:s1], kt[:, None]).astype(np.float32), dtype)  # [B,R,H,s,T]
         sc = np.where(np.broadcast_to(mask, (B, R, H, S, T))[:, :, :, s0:s1], sc, fill)
         m = sc.max(axis=-1, keepdims=True)
-        e = np.exp(sc - m)
-        p = cast(e / e.sum(axis=-1, keepdims=True, dtype=np.float32), dtype)
+        if exact_f32(dtype):  # exp in f64, the sum in f64, each rounded once
+            e = _f32(np.exp((sc - m).astype(np.float64)))
+            p = e / _f32(e.astype(np.float64).sum(axis=-1, keepdims=True))
+        else:
+            e = np.exp(sc - m)
+            p = cast(e / e.sum(axis=-1, keepdims=True, dtype=np.float32), dtype)
         o = cast(np.matmul(p.astype(acc), vt[:, None]).astype(np.float32), dtype)  # [B,R,H,s,D]
         out[:, s0:s1] = o.transpose(0, 3, 1, 2, 4)
     return out
@@ -602,7 +638,7 @@ def forward_mlp(p: MLPParams, x: np.ndarray, dtype: str) -> np.ndarray:
 
     g = matmul(x, p.gate_proj, dtype)
     u = matmul(x, p.up_proj, dtype)
-    h = cast(gelu_tanh(g) * u, dtype) if dtype == BF16 else gelu_tanh(g) * u
+    h = cast(gelu_tanh(g) * u, dtype) if dtype == BF16 else gelu_tanh(g, exact_f32(dtype)) * u
     return matmul(h, p.down_proj, dtype)
 
 
@@ -641,7 +677,7 @@ def forward_decoder_layer(lp: LayerParams, seq, pli, masks, rots, *, layer_index
     seq = cast(residual + h, dtype)
     if lp.per_layer_input is not None:
         g = matmul(seq, lp.per_layer_input.gate, dtype)
-        g = cast(gelu_tanh(g) * pli, dtype)
+        g = cast(gelu_tanh(g, exact_f32(dtype)) * pli, dtype)
         g = matmul(g, lp.per_layer_input.projection, dtype)
         g = rms_norm(lp.per_layer_input.post_norm, g, eps, dtype)
         seq = cast(seq + g, dtype)
@@ -676,7 +712,7 @@ def forward_text(params: Params, ids, position_ids, *, cfg: Config, attention_ma
         masks = make_qk_masks(attention_mask, cfg.sliding_window, 0, S)
     else:
         masks = make_qk_masks(key_mask, cfg.sliding_window, 0, S)
-    rots = make_rotary(cfg, position_ids)
+    rots = make_rotary(cfg, position_ids, dtype)
     shared: dict = {}
     new_layers = []
     for i, lp in enumerate(params.layers):
@@ -698,7 +734,10 @@ def lm_head(embed: np.ndarray, hidden: np.ndarray, softcap: float | None, dtype:
 
     logits = matmul(hidden, embed.T, dtype)
     if softcap is not None:
-        logits = cast(np.tanh(logits / np.float32(softcap)) * np.float32(softcap), dtype)
+        if exact_f32(dtype):
+            logits = _f32(np.tanh((logits / np.float32(softcap)).astype(np.float64))) * np.float32(softcap)
+        else:
+            logits = cast(np.tanh(logits / np.float32(softcap)) * np.float32(softcap), dtype)
     return logits
 
 
