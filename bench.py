@@ -369,6 +369,9 @@ def bench_e2b_decode(steps: int, warmup: int, batch: int = 256, prompt: int = 25
 
     import torch
 
+    import __graft_entry__
+
+    __graft_entry__.load_package()
     from gemma4_posttrain_jax_amd import config as C
     from gemma4_posttrain_jax_amd import kernels
     from gemma4_posttrain_jax_amd import sampler as SMP
@@ -556,6 +559,9 @@ def main() -> int:
     ap.add_argument("--lm-head-only", action="store_true",
                     help="only run g4_lm_head_sample at configs[4]'s shape three times (after the calibration "
                          "copy, if asked for), for the LM head's counter passes; prints no bench line")
+    ap.add_argument("--e2b-only", action="store_true",
+                    help="only the configs[4] decode (prefill, then --e2b-steps graphed steps, default 4), for the "
+                         "decode step's counter passes; prints the step time, not the bench line")
     ap.add_argument("--num-splits", type=int, default=0,
                     help="workgroups per (b, kv head) for decode attention (0: library default)")
     args = ap.parse_args()
@@ -575,6 +581,11 @@ def main() -> int:
     if args.lm_head_only:
         lm_head_passes()
         print("lm head passes done")
+        return 0
+    if args.e2b_only:
+        e2b = bench_e2b_decode(args.e2b_steps if args.e2b_steps > 0 else 4, 2)
+        print(json.dumps({"e2b_decode_ms_per_step": round(e2b["decode_s_per_step"] * 1e3, 3),
+                          "steps_timed": e2b["steps_timed"]}))
         return 0
     res = bench_decode_attention(args.steps, args.warmup, args.num_splits)
     bytes_step = algorithmic_bytes_per_step()
