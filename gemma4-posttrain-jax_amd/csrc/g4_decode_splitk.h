@@ -7,9 +7,11 @@
 //            max m_s and l_s = sum exp(s - m_s). Also the fused append: the split holding the
 //            appended slot substitutes the new K row and writes the slot (K row and V^T column)
 //            back to the cache after its loads.
-//   values   V^T loads of the split are issued first; meanwhile the row statistics
+//   values   V^T loads of the split are issued first, then the split's scores and every split's
+//            (m_s, l_s), so that one wait covers them; the row statistics
 //            m = max m_s, l = sum_s l_s * exp(m_s - m) are formed (fixed split order), then the
-//            exact probabilities bf16(exp(s - m) / l) of the split and its f32 partial of O.
+//            exact probabilities bf16(exp(s - m) / l) of the split and its f32 partial of O
+//            (configs[2]: 119 -> 116-117 us per step against three dependent round trips).
 //   combine  O = sum of the partials in split order, rounded to bf16.
 // The probabilities are rounded exactly as the single-pass kernels round them (after the
 // division by the full-row sum), so the result differs from theirs only in f32 summation order.
@@ -41,12 +43,18 @@ __device__ __forceinline__ bf16x8 q_operand_global(const G4DecodeArgs& a, int pa
   return as_bf16x8(v);
 }
 
+// From D = 256 the q rows sit in LDS (read one 32-dim slice at a time) and a wave holds one K chunk
+// at a time (its second chunk is loaded into the first one's registers after that is scored): 96
+// registers at D = 256, so two workgroups share a CU and one's loads overlap the other's scoring
+// and statistics (configs[2]: 130.5 -> 117.6 us per step; with both chunks and q in registers, 206
+// registers and one workgroup per CU).
 template <int D>
-__global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_scores_kernel(G4DecodeArgs a,
+__global__ __launch_bounds__(kDecodeWaves * 64) __attribute__((amdgpu_waves_per_eu(D == 256 ? 4 : 1))) void
+decode_bf16_splitk_scores_kernel(G4DecodeArgs a,
                                                                                        SplitKWorkspace ws) {
   __shared__ __attribute__((aligned(16))) uint16_t nk_lds[D];
-  // D = 512: the q rows [R][D] in LDS, read one 32-dim slice at a time (register budget)
-  __shared__ __attribute__((aligned(16))) uint16_t q_lds[D > 256 ? 16 * D : 1];
+  // D >= 256: the q rows [R][D] in LDS, read one 32-dim slice at a time (register budget)
+  __shared__ __attribute__((aligned(16))) uint16_t q_lds[D > 128 ? 16 * D : 1];
   extern __shared__ float smem[];
   const int R = a.group;
   uint16_t* sp = reinterpret_cast<uint16_t*>(smem);                // [R][stride] scores of the split
@@ -70,9 +78,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_scores_k
   u32x4 nkv = {0u, 0u, 0u, 0u};
   if (owner && lane < D / 8) nkv = load16(reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D + 8 * lane);
   bf16x8 qop[D / 32];
-  u32x4 qv[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};  // D = 512: thread t's q pieces t, t + 512
+  u32x4 qv[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};  // D >= 256: thread t's q pieces t, t + 512
   const uint16_t* qg = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)pair * R * D;
-  if constexpr (D <= 256) {
+  if constexpr (D <= 128) {
 #pragma unroll
     for (int s = 0; s < D / 32; ++s) qop[s] = q_operand_global(a, pair, R, D, col, grp, s);
   } else {
@@ -86,9 +94,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_scores_k
   const bool ok0 = slot_valid_flat(a, b, kr, c0 + (lane & 31), mb0);
   const bool ok1 = slot_valid_flat(a, b, kr, c1 + (lane & 31), mb1);
   __builtin_amdgcn_sched_barrier(0);
-  // both chunks' K in registers at once up to D = 256; at D = 512 (128 registers per chunk) the
-  // second chunk is loaded into the first one's registers after they are scored
-  constexpr bool kBothChunks = D <= 256;
+  // both chunks' K in registers at once at D = 128; from D = 256 the second chunk is loaded into the
+  // first one's registers after they are scored
+  constexpr bool kBothChunks = D <= 128;
   u32x4 k0[2][D / 32], k1[2][D / 32];
   load_k_chunk<D, true>(k0, rk, c0, col, grp);
   if constexpr (kBothChunks) load_k_chunk<D, true>(k1, rk, c1, col, grp);
@@ -96,14 +104,14 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_scores_k
   if (owner && lane < D / 8) reinterpret_cast<u32x4*>(nk_lds)[lane] = nkv;  // read back by this wave only
   const uint64_t vb0 = __ballot(ok0 && mb0 != 0);
   const uint64_t vb1 = __ballot(ok1 && mb1 != 0);
-  if constexpr (D > 256) {
+  if constexpr (D > 128) {
 #pragma unroll
     for (int j = 0; j < 2; ++j)
       if (tid + 512 * j < R * D / 8) reinterpret_cast<u32x4*>(q_lds)[tid + 512 * j] = qv[j];
     __syncthreads();  // q rows in LDS
   }
   auto score = [&](const u32x4(&kv)[2][D / 32], uint64_t vbits, int local, float m) {
-    if constexpr (D <= 256)
+    if constexpr (D <= 128)
       return score_to_lds<D>(kv, qop, vbits, sp, kStageStride, local, R, col, grp, m);
     else
       return score_to_lds_qlds<D>(kv, q_lds, vbits, sp, kStageStride, local, R, col, grp, m);
@@ -172,18 +180,30 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_scores_k
 }
 
 // Row statistics from the per-split ones (fixed split order): m, l per head into LDS; returns
-// whether the row has no valid slot.
+// whether the row has no valid slot. One pass over the statistics: the (m_s, l_s) pairs of the
+// first 256 splits stay in registers between the max and the sum (no second round trip).
 __device__ __forceinline__ bool splitk_row_stats(const SplitKWorkspace& ws, int pair, int R, int n_splits_row,
                                                   float* mh, float* lh, int w, int n_waves, int lane) {
   const float* st = ws.stats + (int64_t)pair * ws.n_splits * R * 2;
   for (int hh = w; hh < R; hh += n_waves) {  // one wave per head
+    float2 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int s = lane + 64 * j;
+      v[j] = s < n_splits_row ? *reinterpret_cast<const float2*>(st + (s * R + hh) * 2) : make_float2(kBf16Min, 0.f);
+    }
     float m = kBf16Min;
-    for (int s = lane; s < n_splits_row; s += 64) m = fmaxf(m, st[(s * R + hh) * 2]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = fmaxf(m, v[j].x);
+    for (int s = lane + 256; s < n_splits_row; s += 64) m = fmaxf(m, st[(s * R + hh) * 2]);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
     // l = sum_s l_s * exp(m_s - m), per lane in split order, then across lanes in a fixed tree
     float l = 0.f;
-    for (int s = lane; s < n_splits_row; s += 64) l += st[(s * R + hh) * 2 + 1] * expf(st[(s * R + hh) * 2] - m);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (lane + 64 * j < n_splits_row) l += v[j].y * expf(v[j].x - m);
+    for (int s = lane + 256; s < n_splits_row; s += 64) l += st[(s * R + hh) * 2 + 1] * expf(st[(s * R + hh) * 2] - m);
     l = wave_sum64(l);
     if (lane == 0) {
       mh[hh] = m;
@@ -233,12 +253,21 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_k
       for (int ii = 0; ii < DPW; ++ii) vv[i][ii] = buffer_load16_nt(rv, voff, 256u * ((dh * NW + w) * DPW + ii));
     }
   }
+  // this thread's scores of the split (4 slots of up to 4 heads), requested with the statistics so
+  // that one wait covers both
+  const int slot = 256 * (w & 1) + 4 * lane;
+  uint2 svh[4] = {{0u, 0u}, {0u, 0u}, {0u, 0u}, {0u, 0u}};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int hh = 4 * i + (w >> 1);
+    if (hh < R && n_here > 0)
+      svh[i] = *reinterpret_cast<const uint2*>(ws.scores + ((int64_t)pair * R + hh) * ws.c_pad + split * kSplitSlots + slot);
+  }
   __builtin_amdgcn_sched_barrier(0);
   const bool all_masked = splitk_row_stats(ws, pair, R, n_splits_row, mh, lh, w, NW, lane);
   if (!all_masked && split >= n_splits_row) return;  // nothing of the row here (whole workgroup)
   // a row without any valid slot: uniform bf16(1/capacity) over every slot below the capacity
   const int n_mine = all_masked ? (n_chunks_cap - cbase < 2 * NW ? n_chunks_cap - cbase : 2 * NW) : n_here;
-  const int slot = 256 * (w & 1) + 4 * lane;
   const float pu = round_bf16(1.0f / (float)a.capacity);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -250,8 +279,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_k
 #pragma unroll
         for (int j = 0; j < 4; ++j) p[j] = gslot + j < a.capacity ? pu : 0.f;
       } else {
-        const uint2 sv =
-            *reinterpret_cast<const uint2*>(ws.scores + ((int64_t)pair * R + hh) * ws.c_pad + gslot);
+        const uint2 sv = svh[i];
         const float s4[4] = {bf16_lo(sv.x), bf16_hi(sv.x), bf16_lo(sv.y), bf16_hi(sv.y)};
         const float m = mh[hh], l = lh[hh];
 #pragma unroll
