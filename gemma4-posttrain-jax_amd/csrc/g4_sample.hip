@@ -261,7 +261,7 @@ __device__ __forceinline__ float pairwise_sum_f32(const float* a, int n) {
   return pairwise_block_f32(a, n2) + right;
 }
 
-template <bool BF16>
+template <bool BF16, bool VEC>
 __global__ __launch_bounds__(kSampleThreads) void sample_top_k_kernel(G4SampleTopKArgs a) {
   using T = typename Elem<BF16>::T;
   __shared__ uint16_t cap_tab[BF16 ? kCapTableEntries : 1];
@@ -292,32 +292,70 @@ __global__ __launch_bounds__(kSampleThreads) void sample_top_k_kernel(G4SampleTo
   auto capped_x = [&](int c) { return capped_at<BF16>(lrow, c, ct); };
   auto key_of = [&](float x) { return score_key(unit_t ? x : x / a.temperature); };
 
-  // ---- pass 1: log-softmax state and each thread's four largest keys -----------------------------
-  RowState st = {kF32Min, 0.f, -INFINITY, 0x7fffffff};
-  uint32_t t0 = 0u, t1 = 0u, t2 = 0u, t3 = 0u;
-  for (int c0 = tid; c0 < V; c0 += 4 * kSampleThreads) {
-    float x[4];
+  // The columns a thread owns: VEC, 8 consecutive columns per 16-byte (bf16) or 2 x 16-byte (f32)
+  // load, chunks j = tid, tid + 1024, ...; otherwise columns tid, tid + 1024, ...
+  const int nchunks = a.vocab / 8;
+  auto load_x8 = [&](int jj, float (&x)[8]) {
+    using E = Elem<BF16>;
+    constexpr int kRaw = BF16 ? 1 : 2;
+    u32x4 r[kRaw];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = c0 + u * kSampleThreads;
-      x[u] = c < V ? capped_x(c) : -INFINITY;
+    for (int q = 0; q < kRaw; ++q) r[q] = *reinterpret_cast<const u32x4*>(lrow + 8 * jj + 4 * q * (BF16 ? 2 : 1));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t word = r[BF16 ? 0 : e / 4][BF16 ? e / 2 : e % 4];
+      if constexpr (BF16) {
+        const uint32_t bits = e & 1 ? word >> 16 : word & 0xffffu;
+        x[e] = a.softcap > 0.f ? capped(bits, ct) : bf16_bits_to_f32(bits);
+      } else {
+        x[e] = __uint_as_float(word);
+        if (a.softcap > 0.f) x[e] = E::round(tanhf(x[e] / a.softcap) * a.softcap);  // the reference divides by the cap
+      }
     }
-    float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  };
+
+  // ---- pass 1: log-softmax state and each thread's four largest keys (with their columns) ----------
+  RowState st = {kF32Min, 0.f, -INFINITY, 0x7fffffff};
+  uint32_t t0 = 0u, t1 = 0u, t2 = 0u, t3 = 0u;  // key 0 is no element (every score's key is above it)
+  int i0 = 0, i1 = 0, i2 = 0, i3 = 0;
+  auto keep = [&](uint32_t k, int c) {  // the four largest keys, the earlier column first among equal ones
+    if (k > t3) {
+      t3 = k;
+      i3 = c;
+      if (t3 > t2) { const uint32_t t = t2; t2 = t3; t3 = t; const int ic = i2; i2 = i3; i3 = ic; }
+      if (t2 > t1) { const uint32_t t = t1; t1 = t2; t2 = t; const int ic = i1; i1 = i2; i2 = ic; }
+      if (t1 > t0) { const uint32_t t = t0; t0 = t1; t1 = t; const int ic = i0; i0 = i1; i1 = ic; }
+    }
+  };
+  auto add_state = [&](const float* x, int n) {
+    float mx = x[0];
+    for (int u = 1; u < n; ++u) mx = fmaxf(mx, x[u]);
     if (mx > st.m) {
       st.s *= expf(st.m - mx);
       st.m = mx;
     }
+    for (int u = 0; u < n; ++u) st.s += expf(x[u] - st.m);
+  };
+  if constexpr (VEC) {
+    for (int jj = tid; jj < nchunks; jj += kSampleThreads) {
+      float x[8];
+      load_x8(jj, x);
+      add_state(x, 8);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (c0 + u * kSampleThreads >= V) continue;
-      st.s += expf(x[u] - st.m);
-      const uint32_t k = key_of(x[u]);
-      if (k > t3) {  // keep the four largest (any subset of the row gives a lower bound)
-        t3 = k;
-        if (t3 > t2) { const uint32_t t = t2; t2 = t3; t3 = t; }
-        if (t2 > t1) { const uint32_t t = t1; t1 = t2; t2 = t; }
-        if (t1 > t0) { const uint32_t t = t0; t0 = t1; t1 = t; }
+      for (int e = 0; e < 8; ++e) keep(key_of(x[e]), 8 * jj + e);
+    }
+  } else {
+    for (int c0 = tid; c0 < V; c0 += 4 * kSampleThreads) {
+      float x[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int c = c0 + u * kSampleThreads;
+        x[u] = c < V ? capped_x(c) : -INFINITY;
       }
+      add_state(x, 4);  // the -inf of a column past the row adds exp(-inf) = 0
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (c0 + u * kSampleThreads < V) keep(key_of(x[u]), c0 + u * kSampleThreads);
     }
   }
   tk4[4 * tid] = t0;
@@ -359,9 +397,15 @@ __global__ __launch_bounds__(kSampleThreads) void sample_top_k_kernel(G4SampleTo
     }
     return prefix;
   };
-  const uint32_t lower = select_kth(tk4, 4 * kSampleThreads, K);  // <= the row's K-th largest key
+  // the K-th largest of the 4096 kept keys: <= the row's K-th largest key, and >= 1 (the kept keys
+  // hold at least min(4096, V) > K real ones)
+  const uint32_t lower = select_kth(tk4, 4 * kSampleThreads, K);
 
   // ---- pass 2: candidates with key >= lower ------------------------------------------------------
+  // A thread whose fourth kept key is below `lower` has every such element among its first three
+  // kept ones (any other is at most its fourth key); only a thread whose fourth kept key reaches
+  // `lower` may hold more, and rescans its columns. For a row without heavy ties at the top that is
+  // almost no thread, so the row is read about once.
   auto gather = [&](int c, float x, uint32_t k, bool take) {
     const uint64_t m = __ballot(take);
     if (m == 0ull) return;
@@ -379,14 +423,40 @@ __global__ __launch_bounds__(kSampleThreads) void sample_top_k_kernel(G4SampleTo
   };
   if (tid == 0) s_count = 0u;
   __syncthreads();
-  for (int c = tid; c - lane < V; c += kSampleThreads) {  // whole waves iterate together (ballots)
-    float x = 0.f;
-    uint32_t k = 0u;
-    if (c < V) {
-      x = capped_x(c);
-      k = key_of(x);
+  const bool rescan = t3 >= lower;
+  {
+    const uint32_t tk[3] = {t0, t1, t2};
+    const int ik[3] = {i0, i1, i2};
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const bool take = !rescan && tk[q] >= lower;
+      gather(ik[q], take ? capped_x(ik[q]) : 0.f, tk[q], take);
     }
-    gather(c, x, k, c < V && k >= lower);
+  }
+  if (__ballot(rescan) != 0ull) {  // whole waves iterate together (ballots)
+    if constexpr (VEC) {
+      for (int jj = tid; jj - lane < nchunks; jj += kSampleThreads) {
+        float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        const bool live = rescan && jj < nchunks;
+        if (live) load_x8(jj, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t k = live ? key_of(x[e]) : 0u;
+          gather(8 * jj + e, x[e], k, live && k >= lower);
+        }
+      }
+    } else {
+      for (int c = tid; c - lane < V; c += kSampleThreads) {
+        float x = 0.f;
+        uint32_t k = 0u;
+        const bool live = rescan && c < V;
+        if (live) {
+          x = capped_x(c);
+          k = key_of(x);
+        }
+        gather(c, x, k, live && k >= lower);
+      }
+    }
   }
   __syncthreads();
   uint32_t n_cand = s_count;
@@ -603,10 +673,20 @@ extern "C" int g4_sample_top_k(const G4SampleTopKArgs* args, void* stream) {
   if (!a.logits || !a.key || !a.token_out || !a.logp_out) return fail(G4_ERR_INVALID, "g4_sample_top_k: NULL pointer");
   if (a.split_key != 0 && a.split_key != 1) return fail(G4_ERR_INVALID, "g4_sample_top_k: split_key %d", a.split_key);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (a.dtype == G4_DTYPE_BF16)
-    hipLaunchKernelGGL((sample_top_k_kernel<true>), dim3(a.batch), dim3(kSampleThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL((sample_top_k_kernel<false>), dim3(a.batch), dim3(kSampleThreads), 0, st, a);
+  const int esize = a.dtype == G4_DTYPE_BF16 ? 2 : 4;
+  const bool vec = a.vocab % 8 == 0 && (a.row_stride * esize) % 16 == 0 && reinterpret_cast<uintptr_t>(a.logits) % 16 == 0;
+  const dim3 grid(a.batch), block(kSampleThreads);
+  if (a.dtype == G4_DTYPE_BF16) {
+    if (vec)
+      hipLaunchKernelGGL((sample_top_k_kernel<true, true>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((sample_top_k_kernel<true, false>), grid, block, 0, st, a);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((sample_top_k_kernel<false, true>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((sample_top_k_kernel<false, false>), grid, block, 0, st, a);
+  }
   if (int rc = check_launch("g4_sample_top_k")) return rc;
   if (a.split_key) {
     hipLaunchKernelGGL(advance_key_kernel, dim3(1), dim3(64), 0, st, a.key);
