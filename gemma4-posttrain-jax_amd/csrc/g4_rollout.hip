@@ -9,31 +9,59 @@ namespace g4 {
 namespace {
 
 constexpr int kRolloutThreads = 1024;
-constexpr int kEosChunk = 4096;  // EOS ids staged through LDS per pass
+constexpr int kEosRowLoop = 64;  // up to this many EOS ids each row scans them; more: the ids are split over the threads
 
 // One workgroup; rows in blocks of blockDim.x (thread t takes row b0 + t of each block). The EOS
-// ids pass through LDS in chunks (16-byte reads, padded with a copy of the chunk's first id, which
-// changes no match), so a large EOS set costs one broadcast LDS read per four ids and row block.
+// test of a row block: with few ids each row scans them (staged in LDS, 16-byte reads padded with a
+// copy of the first id, which changes no match); with many, each thread holds up to four ids per
+// pass and scans the block's tokens (an LDS broadcast read per row), flagging the rows that match,
+// so a thread does rows x 4 compares per pass instead of one per id (4096 ids at B = 256:
+// ~150 us -> a few us per step).
 __global__ __launch_bounds__(kRolloutThreads) void rollout_step_kernel(G4RolloutStepArgs a) {
-  __shared__ __attribute__((aligned(16))) int32_t eos_lds[kEosChunk];
+  __shared__ __attribute__((aligned(16))) int32_t eos_lds[kEosRowLoop];
+  __shared__ int32_t tok_lds[kRolloutThreads];
+  __shared__ int32_t hit_lds[kRolloutThreads];
   bool stays_any = false;
-  for (int b0 = 0; b0 < a.batch; b0 += blockDim.x) {
+  const int nt = (int)blockDim.x;
+  for (int b0 = 0; b0 < a.batch; b0 += nt) {
     const int b = b0 + (int)threadIdx.x;
     const bool row = b < a.batch;
     const bool act = row && a.active[b] != 0;           // the step's mask
     const int32_t tok = act ? a.sampled[b] : a.pad_id;  // finished rows emit pad
     bool eos = false;
-    for (int c0 = 0; c0 < a.n_eos; c0 += kEosChunk) {
-      const int n = a.n_eos - c0 < kEosChunk ? a.n_eos - c0 : kEosChunk;
-      const int n4 = (n + 3) / 4 * 4;
-      __syncthreads();  // the previous chunk's readers are done
-      for (int i = threadIdx.x; i < n4; i += blockDim.x) eos_lds[i] = a.eos_ids[c0 + (i < n ? i : 0)];
-      __syncthreads();
-      const int4* ids4 = reinterpret_cast<const int4*>(eos_lds);
-      for (int i = 0; i < n4 / 4; ++i) {
-        const int4 e = ids4[i];
-        eos = eos || tok == e.x || tok == e.y || tok == e.z || tok == e.w;
+    if (a.n_eos <= kEosRowLoop) {
+      if (a.n_eos > 0) {
+        const int n4 = (a.n_eos + 3) / 4 * 4;
+        __syncthreads();  // the previous row block's readers are done
+        for (int i = threadIdx.x; i < n4; i += nt) eos_lds[i] = a.eos_ids[i < a.n_eos ? i : 0];
+        __syncthreads();
+        const int4* ids4 = reinterpret_cast<const int4*>(eos_lds);
+        for (int i = 0; i < n4 / 4; ++i) {
+          const int4 e = ids4[i];
+          eos = eos || tok == e.x || tok == e.y || tok == e.z || tok == e.w;
+        }
       }
+    } else {
+      const int nrows = a.batch - b0 < nt ? a.batch - b0 : nt;
+      __syncthreads();  // the previous row block's readers are done
+      tok_lds[threadIdx.x] = tok;
+      hit_lds[threadIdx.x] = 0;
+      __syncthreads();
+      for (int c0 = 0; c0 < a.n_eos; c0 += 4 * nt) {
+        const int i0 = c0 + (int)threadIdx.x;
+        if (i0 < a.n_eos) {  // ids i0, i0 + nt, ... of this pass (a missing one repeats the first)
+          const int32_t e0 = a.eos_ids[i0];
+          const int32_t e1 = i0 + nt < a.n_eos ? a.eos_ids[i0 + nt] : e0;
+          const int32_t e2 = i0 + 2 * nt < a.n_eos ? a.eos_ids[i0 + 2 * nt] : e0;
+          const int32_t e3 = i0 + 3 * nt < a.n_eos ? a.eos_ids[i0 + 3 * nt] : e0;
+          for (int r = 0; r < nrows; ++r) {
+            const int32_t t = tok_lds[r];
+            if (t == e0 || t == e1 || t == e2 || t == e3) hit_lds[r] = 1;
+          }
+        }
+      }
+      __syncthreads();
+      eos = hit_lds[threadIdx.x] != 0;
     }
     if (!row) continue;
     const int64_t at = (int64_t)b * a.max_new + a.step;

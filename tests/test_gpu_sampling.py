@@ -209,15 +209,23 @@ def test_draws_over_long_rows_follow_the_jax_stream(device, scale):
     np.testing.assert_allclose(logp.cpu().numpy(), want_logp, rtol=0, atol=LOGP_ATOL)
 
 
-@pytest.mark.parametrize("B,ids_dtype", [(5, torch.int32), (300, torch.int64), (1500, torch.int32)])
-def test_rollout_step_bookkeeping(device, B, ids_dtype):
+@pytest.mark.parametrize("B,ids_dtype,n_eos", [(5, torch.int32, 3), (300, torch.int64, 3), (1500, torch.int32, 3),
+                                                (256, torch.int32, 5000), (1500, torch.int64, 5000)])
+def test_rollout_step_bookkeeping(device, B, ids_dtype, n_eos):
     """g4_rollout_step over two steps against the loop body of sampler.py:279-296 stated with numpy:
     finished rows emit pad with logp 0 and mask 0, the EOS test clears `active`, the next decode
     inputs are (token, prompt_length + step, the step's mask); rows beyond 1024 take the kernel's
-    strided loop. A last call whose rows all hit EOS reports no active row."""
+    strided loop. A last call whose rows all hit EOS reports no active row. With 5000 EOS ids the
+    kernel splits the ids over its threads (two passes of 4 x 1024); the matching ids sit in the
+    first pass, the second pass and the last slot."""
 
     rng = np.random.default_rng(B)
-    N, pad, eos = 6, 7, np.array([3, 11, 2**20], np.int32)
+    N, pad = 6, 7
+    if n_eos == 3:
+        eos = np.array([3, 11, 2**20], np.int32)
+    else:
+        eos = rng.integers(16, 2**20, n_eos).astype(np.int32)  # never a drawn token (those are < 16)
+        eos[1500], eos[4500], eos[-1] = 3, 11, 2**20
     ids = torch.full((B, N), pad, dtype=ids_dtype, device=device)
     mask = torch.zeros((B, N), dtype=torch.bool, device=device)
     logps = torch.zeros((B, N), dtype=torch.float32, device=device)
