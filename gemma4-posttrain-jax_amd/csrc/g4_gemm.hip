@@ -3,10 +3,11 @@
 // projections of forward_attention / forward_mlp (model.py:463-482, 393-396, 500) at S = 1.
 //
 // At M = 256 the projection is a stream of the weight matrix: every weight byte is used by all
-// 256 rows once. One workgroup owns all M rows and 64 columns of W, so W is read from HBM exactly
-// once, and X (shared by every workgroup) comes from L2. K is walked in stages of 64: the X
-// stage (256 x 64) and the W stage (64 x 64) are DMA'd into a 4-deep LDS ring
-// (buffer_load ... lds), three stages in flight while the fourth is multiplied.
+// 256 rows once. A workgroup owns 128 rows x 128 columns of the output (the two row halves of a
+// column tile on one XCD, so W is read from HBM once; 256 rows x 64 columns below 129 rows), and
+// X (shared by every workgroup) comes from L2. K is walked in stages of 64: the X and W stages are
+// DMA'd into a 4-deep LDS ring (buffer_load ... lds), three stages in flight while the fourth is
+// multiplied.
 //
 // LDS layout of a stage: groups of 8 rows x 128 bytes (one DMA instruction: 64 lanes x 16 bytes,
 // 8 full 128-byte lines of the row-major operand); within a group, row r's
@@ -15,10 +16,10 @@
 //
 // MFMA v_mfma_f32_16x16x32_bf16 with A = 16 rows of W (output columns) and B = 16 rows of X
 // (output rows): lane (grp, col) accumulates Y[m = 16 rb + col][n = 16 cb + 4 grp .. + 3], four
-// consecutive outputs of one row. Wave w owns rows [64 w, 64 w + 64) x the workgroup's 64 columns
-// (4 x 4 accumulator blocks).
+// consecutive outputs of one row. Each wave owns a 64 x 64 block of the tile (4 x 4 accumulator
+// blocks).
 //
-// Split-K (ksplit > 1): workgroup (n-tile, s) covers K range s; partial sums go to an f32
+// Split-K (ksplit > 1): a workgroup of split s covers K range s; partial sums go to an f32
 // workspace [ksplit][M][N] and a second kernel adds them in split order and rounds to bf16, or,
 // with no y given, they are left there for a consumer that adds them itself
 // (g4_residual_norm_splitk, the residual norm after the MLP's down projection).
@@ -28,34 +29,52 @@
 namespace g4 {
 namespace {
 
-constexpr int kGemmRows = 256;  // M rows per workgroup (all of them)
-constexpr int kGemmCols = 64;   // N columns per workgroup
+constexpr int kGemmRows = 256;  // M rows at most
 constexpr int kGemmKT = 64;     // K per stage
 constexpr int kGemmThreads = 256;
-constexpr int kGroupBytes = 1024;                   // 8 rows x 128 B (a 4-stage ring fills the 160 KiB)
-constexpr int kXGroups = kGemmRows / 8;             // 32
-constexpr int kWGroups = kGemmCols / 8;             // 8
-constexpr int kStageBytes = (kXGroups + kWGroups) * kGroupBytes;
-constexpr int kDmaPerWave = (kXGroups + kWGroups) / (kGemmThreads / 64);  // 10 DMA instructions per wave and stage
+constexpr int kGroupBytes = 1024;  // 8 rows x 128 B
 
-typedef unsigned char StageBuf[kStageBytes];
+// A workgroup's tile: TR rows x TC columns, 4 waves of 64 x 64 (TR / 64 along the rows, TC / 64
+// along the columns). TR = 256: all rows, 64 columns (X re-read once per 64 columns). TR = 128: half
+// the rows, 128 columns (per CU 1/4 less X + W traffic; the two row halves of a column tile go to
+// one XCD, so the second read of its W is an L2 hit).
+template <int TR>
+struct GemmTile {
+  static constexpr int TC = 16384 / TR;
+  static constexpr int WR = TR / 64;  // waves along the rows
+  static constexpr int XG = TR / 8;   // 8-row groups of X per stage
+  static constexpr int WG = TC / 8;   // of W
+  static constexpr int DMA = (XG + WG) / (kGemmThreads / 64);  // DMA instructions per wave and stage
+  static constexpr int STAGE = (XG + WG) * kGroupBytes;        // 40 KiB (TR 256) / 32 KiB (TR 128)
+  static_assert(TR == 256 || TR == 128, "tile rows");
+};
 
-// DMA of stage `st` (K offset k0) into `buf`: wave w moves groups w, w + 4, ... of X then of W.
+// First weight row of W group j (8 rows) of column tile `tile`. Plain: rows tile * TC + 8 j. Gated
+// GELU: each 64-column wave slice holds the 32 gate rows and the 32 up rows of the same 32 outputs
+// (gate rows of output o at o, up rows at half + o), tile * TC / 2 outputs before this tile.
+template <int TC>
+__device__ __forceinline__ int gemm_wrow(bool gelu, int half, int tile, int j) {
+  if (!gelu) return tile * TC + 8 * j;
+  const int o = tile * (TC / 2) + 32 * (j >> 3) + 8 * (j & 3);
+  return (j & 7) < 4 ? o : half + o;
+}
+
+// DMA of the stage at K offset k0 into `buf`: wave w moves groups w, w + 4, ... of X then of W.
 // Lane l of a group instruction takes row 8 g + l / 8 and the 16-byte piece (l % 8) ^ (row % 8) of
-// its 128-byte K slice. W group j (rows 8 j .. 8 j + 7 of the tile) starts at weight row
-// wrow[j >> 2] + 8 (j & 3). Past the last stage every load reads beyond its resource (zeros, no
-// memory request), so every wave always issues kDmaPerWave loads per stage.
+// its 128-byte K slice. Past the last stage every load reads beyond its resource (zeros, no memory
+// request), so every wave always issues the same number of loads per stage.
+template <int TR>
 __device__ __forceinline__ void gemm_dma(unsigned char* __restrict__ buf, __amdgpu_buffer_rsrc_t rx,
                                          __amdgpu_buffer_rsrc_t rw, int K, int k0, bool live, uint32_t oob_x,
-                                         uint32_t oob_w, int w, int lane, int wrow0, int wrow1) {
-  const int rl = lane >> 3;                       // row within the group
-  const int kc = (lane & 7) ^ rl;                 // 16-byte piece this lane fetches (row % 8 == rl)
+                                         uint32_t oob_w, int w, int lane, int m0, bool gelu, int half, int tile) {
+  using T = GemmTile<TR>;
+  const int rl = lane >> 3;        // row within the group
+  const int kc = (lane & 7) ^ rl;  // 16-byte piece this lane fetches (row % 8 == rl)
 #pragma unroll
-  for (int i = 0; i < kDmaPerWave; ++i) {
-    const int g = w + 4 * i;  // groups 0..31: X, 32..39: W
-    const bool is_x = g < kXGroups;
-    const int gw = g - kXGroups;
-    const int row = is_x ? 8 * g + rl : (gw < 4 ? wrow0 : wrow1) + 8 * (gw & 3) + rl;
+  for (int i = 0; i < T::DMA; ++i) {
+    const int g = w + 4 * i;  // groups 0..XG-1: X, then W
+    const bool is_x = g < T::XG;
+    const int row = is_x ? m0 + 8 * g + rl : gemm_wrow<T::TC>(gelu, half, tile, g - T::XG) + rl;
     const uint32_t off = (uint32_t)(row * K + k0 + 8 * kc) * 2u;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(is_x ? rx : rw,
                                              (__attribute__((address_space(3))) void*)(buf + g * kGroupBytes), 16,
@@ -75,18 +94,20 @@ __device__ __forceinline__ uint32_t gemm_operand_at(uint32_t part, int row, int 
 // tell the stage being multiplied from the stages the DMA is still filling, and at some steps of
 // the ring waited for every DMA in flight (vmcnt(0)); the stage's own DMAs are already covered by
 // the s_waitcnt vmcnt + s_barrier that starts each step.
-
-__device__ __forceinline__ void gemm_compute(const unsigned char* __restrict__ buf, floatx4 (&acc)[4][4], int w,
-                                             int col, int grp) {
+// Wave (wr, wc) multiplies rows [64 wr, 64 wr + 64) of the X part by rows [64 wc, 64 wc + 64) of
+// the W part.
+template <int TR>
+__device__ __forceinline__ void gemm_compute(const unsigned char* __restrict__ buf, floatx4 (&acc)[4][4], int wr,
+                                             int wc, int col, int grp) {
   const uint32_t xs = lds_addr(buf);
-  const uint32_t ws = xs + kXGroups * kGroupBytes;
+  const uint32_t ws = xs + GemmTile<TR>::XG * kGroupBytes;
 #pragma unroll
   for (int kh = 0; kh < 2; ++kh) {
     u32x4 a[4], b[4];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) a[cb] = lds_read16(gemm_operand_at(ws, 16 * cb + col, 4 * kh + grp));
+    for (int cb = 0; cb < 4; ++cb) a[cb] = lds_read16(gemm_operand_at(ws, 64 * wc + 16 * cb + col, 4 * kh + grp));
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) b[rb] = lds_read16(gemm_operand_at(xs, 64 * w + 16 * rb + col, 4 * kh + grp));
+    for (int rb = 0; rb < 4; ++rb) b[rb] = lds_read16(gemm_operand_at(xs, 64 * wr + 16 * rb + col, 4 * kh + grp));
     __asm__ volatile("s_waitcnt lgkmcnt(0)"
                      : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
 #pragma unroll
@@ -96,81 +117,107 @@ __device__ __forceinline__ void gemm_compute(const unsigned char* __restrict__ b
   }
 }
 
-// One pipeline step: stage s is in `cur`; `nxt` holds stage s + 1 (in flight, with s + 2); stage
-// s + 3 is requested into `fre` (the buffer of stage s - 1, which every wave has finished with)
-// after the stage's MFMAs are issued, so a DMA issue that waits for room in the memory queue
-// does not hold them back (down projection 19.3 -> 18.6 us).
-__device__ __forceinline__ void gemm_step(unsigned char* __restrict__ cur, unsigned char* __restrict__ nxt,
-                                          unsigned char* __restrict__ fre, floatx4 (&acc)[4][4],
-                                          __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw, int K, int kbeg,
-                                          int s, int nst, uint32_t oob_x, uint32_t oob_w, int w, int lane, int col,
-                                          int grp, int wrow0, int wrow1) {
-  (void)nxt;
+struct GemmLoop {
+  __amdgpu_buffer_rsrc_t rx, rw;
+  int K, kbeg, nst;
+  uint32_t oob_x, oob_w;
+  int w, lane, col, grp, wr, wc, m0, half, tile;
+  bool gelu;
+};
+
+// One pipeline step: stage s is in `cur` (stages s + 1, s + 2 in flight); stage s + 3 is
+// requested into `fre` (the buffer of stage s - 1, which every wave has finished with) after the
+// stage's MFMAs are issued, so a DMA issue that waits for room in the memory queue does not hold
+// them back (down projection 19.3 -> 18.6 us).
+template <int TR>
+__device__ __forceinline__ void gemm_step(const unsigned char* __restrict__ cur, unsigned char* __restrict__ fre,
+                                          floatx4 (&acc)[4][4], const GemmLoop& L, int s) {
   // this wave's DMAs of stage s have landed (stages s + 1, s + 2 may not have), then every wave's
-  __asm__ volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * kDmaPerWave) : "memory");
-  gemm_compute(cur, acc, w, col, grp);
-  gemm_dma(fre, rx, rw, K, kbeg + (s + 3) * kGemmKT, s + 3 < nst, oob_x, oob_w, w, lane, wrow0, wrow1);
+  __asm__ volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * GemmTile<TR>::DMA) : "memory");
+  gemm_compute<TR>(cur, acc, L.wr, L.wc, L.col, L.grp);
+  gemm_dma<TR>(fre, L.rx, L.rw, L.K, L.kbeg + (s + 3) * kGemmKT, s + 3 < L.nst, L.oob_x, L.oob_w, L.w, L.lane, L.m0,
+               L.gelu, L.half, L.tile);
 }
 
-// grid: (N / 64) * ksplit workgroups, workgroup i = (column tile i / ksplit, K split i % ksplit).
-// Workgroups are dealt to the 8 XCDs round robin (i mod 8), so with ksplit dividing 8 every XCD
-// works on one K split and its L2 holds only that split's slice of X, which all its column tiles
-// re-read. K / ksplit must be a multiple of 64. With the gated-GELU epilogue the workgroup's 64
-// weight rows are 32 gate rows and the 32 up rows of the same output columns.
+// Work units (column tile, K split), each covered by n_halves = ceil(M / TR) workgroups (row
+// halves). Workgroups are dealt to the 8 XCDs round robin (i mod 8); when the unit count is a
+// multiple of 8, workgroup i takes unit 8 (j / n_halves) + i mod 8 and half j mod n_halves
+// (j = i / 8), so all halves of a unit share an XCD (one HBM read of its W) and, with ksplit
+// dividing 8, every XCD works on one K split, whose slice of X its L2 then holds for all its
+// column tiles. The unit is (tile u / ksplit, split u mod ksplit). K / ksplit must be a multiple
+// of 64.
+template <int TR>
 __global__ __launch_bounds__(kGemmThreads) void linear_bf16_kernel(G4LinearArgs a, float* partials) {
-  __shared__ __attribute__((aligned(1024))) StageBuf b0, b1, b2, b3;
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int col = lane & 15, grp = lane >> 4;
-  const int tile = (int)blockIdx.x / a.ksplit;
-  const int split = (int)blockIdx.x - tile * a.ksplit;
-  const int n0 = tile * kGemmCols;
-  const int K = a.k;
-  const int kper = K / a.ksplit;
-  const int kbeg = split * kper;
-  const int nst = kper / kGemmKT;
-  const uint32_t xbytes = (uint32_t)a.m * (uint32_t)K * 2u;  // rows >= M read as zeros
-  const uint32_t wbytes = (uint32_t)a.n * (uint32_t)K * 2u;
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, xbytes);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, wbytes);
-  const bool gelu = a.epilogue == G4_LINEAR_GELU_MUL;
-  const int half = a.n / 2;
-  // weight rows of tile groups 0..3 and 4..7
-  const int wrow0 = gelu ? tile * 32 : n0;
-  const int wrow1 = gelu ? half + tile * 32 : n0 + 32;
+  using T = GemmTile<TR>;
+  __shared__ __attribute__((aligned(1024))) unsigned char b0[T::STAGE], b1[T::STAGE], b2[T::STAGE], b3[T::STAGE];
+  GemmLoop L;
+  L.lane = threadIdx.x & 63;
+  L.w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  L.col = L.lane & 15;
+  L.grp = L.lane >> 4;
+  L.wr = L.w % T::WR;
+  L.wc = L.w / T::WR;
+  const int n_halves = (a.m + TR - 1) / TR;
+  const int n_units = a.n / T::TC * a.ksplit;
+  const int i = (int)blockIdx.x;
+  int unit, hf;
+  if (n_units % 8 == 0) {
+    const int j = i >> 3;
+    unit = 8 * (j / n_halves) + (i & 7);
+    hf = j % n_halves;
+  } else {
+    unit = i / n_halves;
+    hf = i % n_halves;
+  }
+  L.tile = unit / a.ksplit;
+  const int split = unit - L.tile * a.ksplit;
+  L.m0 = hf * TR;
+  const int n0 = L.tile * T::TC;
+  L.K = a.k;
+  const int kper = L.K / a.ksplit;
+  L.kbeg = split * kper;
+  L.nst = kper / kGemmKT;
+  const uint32_t xbytes = (uint32_t)a.m * (uint32_t)L.K * 2u;  // rows >= M read as zeros
+  const uint32_t wbytes = (uint32_t)a.n * (uint32_t)L.K * 2u;
+  L.oob_x = xbytes;
+  L.oob_w = wbytes;
+  L.rx = make_rsrc(a.x, xbytes);
+  L.rw = make_rsrc(a.w, wbytes);
+  L.gelu = a.epilogue == G4_LINEAR_GELU_MUL;
+  L.half = a.n / 2;
 
   floatx4 acc[4][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < 4; ++c) acc[r][c] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  gemm_dma(b0, rx, rw, K, kbeg, true, xbytes, wbytes, w, lane, wrow0, wrow1);
-  gemm_dma(b1, rx, rw, K, kbeg + kGemmKT, nst > 1, xbytes, wbytes, w, lane, wrow0, wrow1);
-  gemm_dma(b2, rx, rw, K, kbeg + 2 * kGemmKT, nst > 2, xbytes, wbytes, w, lane, wrow0, wrow1);
-  for (int s = 0; s < nst; s += 4) {
-    gemm_step(b0, b1, b3, acc, rx, rw, K, kbeg, s, nst, xbytes, wbytes, w, lane, col, grp, wrow0, wrow1);
-    if (s + 1 < nst)
-      gemm_step(b1, b2, b0, acc, rx, rw, K, kbeg, s + 1, nst, xbytes, wbytes, w, lane, col, grp, wrow0, wrow1);
-    if (s + 2 < nst)
-      gemm_step(b2, b3, b1, acc, rx, rw, K, kbeg, s + 2, nst, xbytes, wbytes, w, lane, col, grp, wrow0, wrow1);
-    if (s + 3 < nst)
-      gemm_step(b3, b0, b2, acc, rx, rw, K, kbeg, s + 3, nst, xbytes, wbytes, w, lane, col, grp, wrow0, wrow1);
+  gemm_dma<TR>(b0, L.rx, L.rw, L.K, L.kbeg, true, xbytes, wbytes, L.w, L.lane, L.m0, L.gelu, L.half, L.tile);
+  gemm_dma<TR>(b1, L.rx, L.rw, L.K, L.kbeg + kGemmKT, L.nst > 1, xbytes, wbytes, L.w, L.lane, L.m0, L.gelu, L.half,
+               L.tile);
+  gemm_dma<TR>(b2, L.rx, L.rw, L.K, L.kbeg + 2 * kGemmKT, L.nst > 2, xbytes, wbytes, L.w, L.lane, L.m0, L.gelu,
+               L.half, L.tile);
+  for (int s = 0; s < L.nst; s += 4) {
+    gemm_step<TR>(b0, b3, acc, L, s);
+    if (s + 1 < L.nst) gemm_step<TR>(b1, b0, acc, L, s + 1);
+    if (s + 2 < L.nst) gemm_step<TR>(b2, b1, acc, L, s + 2);
+    if (s + 3 < L.nst) gemm_step<TR>(b3, b2, acc, L, s + 3);
   }
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the trailing (zero) DMAs
 
-  // lane (grp, col) holds Y[m = 64 w + 16 rb + col][n = n0 + 16 cb + 4 grp + j]
-  if (gelu) {  // cb 0, 1: gate columns; cb 2, 3: the up columns of the same outputs
+  // lane (grp, col) holds Y[m = m0 + 64 wr + 16 rb + col][n = n0 + 64 wc + 16 cb + 4 grp + j]
+  if (L.gelu) {  // cb 0, 1: gate columns; cb 2, 3: the up columns of the same outputs
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
-      const int m = 64 * w + 16 * rb + col;
+      const int m = L.m0 + 64 * L.wr + 16 * rb + L.col;
       if (m < a.m) {
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
           float y[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) y[j] = gelu_tanh_mul(round_bf16(acc[rb][cb][j]), round_bf16(acc[rb][cb + 2][j]));
-          uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + (int64_t)m * a.ldy + tile * 32 + 16 * cb + 4 * grp;
+          uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + (int64_t)m * a.ldy + L.tile * (T::TC / 2) + 32 * L.wc +
+                          16 * cb + 4 * L.grp;
           *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
         }
       }
@@ -179,11 +226,11 @@ __global__ __launch_bounds__(kGemmThreads) void linear_bf16_kernel(G4LinearArgs 
   }
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb) {
-    const int m = 64 * w + 16 * rb + col;
+    const int m = L.m0 + 64 * L.wr + 16 * rb + L.col;
     if (m < a.m) {
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
-        const int n = n0 + 16 * cb + 4 * grp;
+        const int n = n0 + 64 * L.wc + 16 * cb + 4 * L.grp;
         if (a.ksplit == 1) {
           uint16_t* y = reinterpret_cast<uint16_t*>(a.y) + (int64_t)m * a.ldy + n;
           *reinterpret_cast<uint2*>(y) = make_uint2(pack_bf16x2(acc[rb][cb][0], acc[rb][cb][1]),
@@ -223,7 +270,7 @@ extern "C" int g4_linear_bf16(const G4LinearArgs* args, void* stream) {
   const G4LinearArgs& a = *args;
   if (!a.x || !a.w || (!a.y && a.ksplit <= 1)) return fail(G4_ERR_INVALID, "g4_linear_bf16: NULL x/w/y");
   if (a.m <= 0 || a.m > kGemmRows) return fail(G4_ERR_UNSUPPORTED, "g4_linear_bf16: m %d (1..%d)", a.m, kGemmRows);
-  if (a.n <= 0 || a.n % kGemmCols) return fail(G4_ERR_UNSUPPORTED, "g4_linear_bf16: n %d (a multiple of %d)", a.n, kGemmCols);
+  if (a.n <= 0 || a.n % 64) return fail(G4_ERR_UNSUPPORTED, "g4_linear_bf16: n %d (a multiple of 64)", a.n);
   if (a.ksplit < 1 || a.ksplit > 64) return fail(G4_ERR_INVALID, "g4_linear_bf16: ksplit %d (1..64)", a.ksplit);
   if (a.k <= 0 || a.k % (kGemmKT * a.ksplit))
     return fail(G4_ERR_UNSUPPORTED, "g4_linear_bf16: k %d (a multiple of %d x ksplit %d)", a.k, kGemmKT, a.ksplit);
@@ -245,8 +292,13 @@ extern "C" int g4_linear_bf16(const G4LinearArgs* args, void* stream) {
                 a.workspace ? a.workspace_bytes : (size_t)0);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   float* partials = reinterpret_cast<float*>(a.workspace);
-  hipLaunchKernelGGL(linear_bf16_kernel, dim3((unsigned)(a.n / kGemmCols * a.ksplit)), dim3(kGemmThreads), 0,
-                     st, a, partials);
+  // 128 x 128 tiles when the rows fill two halves and the columns divide by 128; else 256 x 64
+  if (a.m > 128 && a.n % 128 == 0)
+    hipLaunchKernelGGL(linear_bf16_kernel<128>, dim3((unsigned)(a.n / 128 * a.ksplit * 2)), dim3(kGemmThreads), 0,
+                       st, a, partials);
+  else
+    hipLaunchKernelGGL(linear_bf16_kernel<256>, dim3((unsigned)(a.n / 64 * a.ksplit)), dim3(kGemmThreads), 0, st,
+                       a, partials);
   if (int rc = check_launch("g4_linear_bf16")) return rc;
   if (a.ksplit > 1 && a.y) {  // without y the partials stay in the workspace for the consumer
     const int64_t quads = ((int64_t)a.m * a.n) / 4;
