@@ -37,12 +37,14 @@ def test_linear_e2b_projection_shapes(device, n, k, ksplit):
     _check(256, n, k, ksplit, seed=n + k + ksplit)
 
 
-@pytest.mark.parametrize("m", [1, 17, 64, 200])
-def test_linear_partial_row_blocks(device, m):
-    """Fewer rows than the 256-row tile (rows past m read as zero, never stored); split-K; a
-    strided output with columns past n left untouched."""
+@pytest.mark.parametrize("m,n", [(1, 192), (17, 192), (64, 192), (200, 192), (200, 256), (129, 384), (255, 128),
+                                 (200, 1024)])
+def test_linear_partial_row_blocks(device, m, n):
+    """Fewer rows than the tile (rows past m read as zero, never stored): the 256 x 64 tiles, and the
+    128 x 128 tiles (m > 128, n a multiple of 128) whose second row half is partly filled; split-K;
+    a strided output with columns past n left untouched."""
 
-    _check(m, 192, 640, 5 if m != 64 else 1, seed=m, ldy=256)
+    _check(m, n, 640, 5 if m != 64 else 1, seed=m + n, ldy=n + 64)
 
 
 @pytest.mark.parametrize("rows,cols,k,ksplit,with_scalar", [(256, 2048, 8192, 8, True), (37, 4096, 1536, 3, False),
@@ -67,7 +69,7 @@ def test_residual_norm_splitk_equals_unfused(device, rows, cols, k, ksplit, with
     assert torch.equal(h1.view(torch.int16), h2.view(torch.int16))
 
 
-@pytest.mark.parametrize("m,f,k", [(256, 8192, 2048), (19, 96, 320)])
+@pytest.mark.parametrize("m,f,k", [(256, 8192, 2048), (19, 96, 320), (200, 192, 512)])
 def test_linear_gelu_epilogue(device, m, f, k):
     """The gated-GELU epilogue equals g4_linear_bf16's own gate/up product followed by
     g4_gelu_mul bit for bit, and the fp32 reference within the bf16 bar."""
