@@ -14,12 +14,12 @@ constexpr int kEosRowLoop = 64;  // up to this many EOS ids each row scans them;
 // One workgroup; rows in blocks of blockDim.x (thread t takes row b0 + t of each block). The EOS
 // test of a row block: with few ids each row scans them (staged in LDS, 16-byte reads padded with a
 // copy of the first id, which changes no match); with many, each thread holds up to four ids per
-// pass and scans the block's tokens (an LDS broadcast read per row), flagging the rows that match,
-// so a thread does rows x 4 compares per pass instead of one per id (4096 ids at B = 256:
-// ~150 us -> a few us per step).
+// pass and scans the block's tokens (LDS broadcast reads of four rows), flagging the rows that
+// match, so a thread does rows x 4 compares per pass instead of one per id; such a launch takes
+// 1024 threads whatever the batch (4096 ids at B = 256: one pass, ~150 us -> a few us per step).
 __global__ __launch_bounds__(kRolloutThreads) void rollout_step_kernel(G4RolloutStepArgs a) {
   __shared__ __attribute__((aligned(16))) int32_t eos_lds[kEosRowLoop];
-  __shared__ int32_t tok_lds[kRolloutThreads];
+  __shared__ __attribute__((aligned(16))) int32_t tok_lds[kRolloutThreads];
   __shared__ int32_t hit_lds[kRolloutThreads];
   bool stays_any = false;
   const int nt = (int)blockDim.x;
@@ -54,9 +54,15 @@ __global__ __launch_bounds__(kRolloutThreads) void rollout_step_kernel(G4Rollout
           const int32_t e1 = i0 + nt < a.n_eos ? a.eos_ids[i0 + nt] : e0;
           const int32_t e2 = i0 + 2 * nt < a.n_eos ? a.eos_ids[i0 + 2 * nt] : e0;
           const int32_t e3 = i0 + 3 * nt < a.n_eos ? a.eos_ids[i0 + 3 * nt] : e0;
-          for (int r = 0; r < nrows; ++r) {
-            const int32_t t = tok_lds[r];
-            if (t == e0 || t == e1 || t == e2 || t == e3) hit_lds[r] = 1;
+          const int4* t4 = reinterpret_cast<const int4*>(tok_lds);  // four rows per read
+          for (int r4 = 0; r4 < (nrows + 3) / 4; ++r4) {
+            const int4 t = t4[r4];
+            const int32_t tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int r = 4 * r4 + q;
+              if (r < nrows && (tv[q] == e0 || tv[q] == e1 || tv[q] == e2 || tv[q] == e3)) hit_lds[r] = 1;
+            }
           }
         }
       }
@@ -97,7 +103,8 @@ extern "C" int g4_rollout_step(const G4RolloutStepArgs* args, void* stream) {
     return fail(G4_ERR_INVALID, "g4_rollout_step: NULL pointer");
   if (reinterpret_cast<uintptr_t>(a.completion_ids) % (uintptr_t)a.id_bytes)
     return fail(G4_ERR_INVALID, "g4_rollout_step: completion_ids not %d-byte aligned", a.id_bytes);
-  const int threads = a.batch < kRolloutThreads ? (a.batch + 63) / 64 * 64 : kRolloutThreads;
+  // a large EOS set is split over the threads: take all of them whatever the batch
+  const int threads = a.batch < kRolloutThreads && a.n_eos <= kEosRowLoop ? (a.batch + 63) / 64 * 64 : kRolloutThreads;
   hipLaunchKernelGGL(rollout_step_kernel, dim3(1), dim3(threads), 0, reinterpret_cast<hipStream_t>(stream), a);
   return check_launch("g4_rollout_step");
 }
