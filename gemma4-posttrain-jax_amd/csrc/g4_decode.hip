@@ -14,6 +14,8 @@
 //   PV on MFMA 16x16x32: A = V^T rows (16-byte loads along keys from the transposed cache),
 //   B = probabilities, accumulators = O^T[d, head].
 // f32 path: a VALU kernel with the same two-phase structure (the tiny fp32 configs).
+#include <type_traits>
+
 #include "g4_common.h"
 #include "g4_internal.h"
 #include "g4_prep.h"

@@ -2,16 +2,19 @@
 // D / NSPLIT = 128 value dims per workgroup; included by g4_decode.hip after g4_decode_fast.h.
 //
 // Requests: q (straight into MFMA operand registers), the key-mask bytes and two 32-slot K
-// chunks per wave (registers) go out first, with the first half of the workgroup's V^T slice
-// DMA'd into LDS (buffer_load ... lds); the second half (chunks 8..15) is queued after the
-// softmax's second barrier. Wave w stages the tiles of its own 16-row d-block, each tile
+// chunks per wave (registers) go out first, with V^T chunks 0..10 of the workgroup's slice DMA'd
+// into LDS (buffer_load ... lds); chunks 11..15 are queued after the softmax's second barrier
+// (config 2: 15.39-15.48 us with 8 + 8 chunks, 15.14-15.17 with 10 + 6, 15.09-15.10 with 11 + 5,
+// 15.27-15.35 with 12 + 4: each chunk requested early adds to the K loads' contention, each one
+// requested late to the tail after the softmax). Wave w stages the tiles of its own 16-row d-block, each tile
 // lane-ordered so that it is read back as that lane's MFMA operand. The split keeps the memory
 // queue busy through the scores and the softmax without making the barriers wait for the whole
 // V issue (a wave blocked on a full queue reaches no barrier), and the value MFMAs of the first
 // half run while the second half lands. The barriers wait only for LDS traffic (a
 // __syncthreads() fence would also wait for the DMA, which writes LDS); each wave waits for its
 // own DMA right before the value MFMAs that read it (the two halves are separate LDS arrays, so
-// the compiler's wait for the first does not include the second).
+// the compiler's wait for the first does not include the second). The value MFMAs accumulate the
+// even chunks in one register set and the odd ones in another, whatever the split.
 //
 // The appended token: the wave that scores the chunk holding the slot stages the new K row in
 // LDS for itself (no barrier) and substitutes it into that chunk's K operand registers; every
@@ -32,18 +35,21 @@ __device__ __forceinline__ float wave_sum64(float v) {
   return v;
 }
 
-using VtTiles = unsigned char[NW][NW][1024];  // [wave][chunk][lane*16]
+constexpr int kVtEarly = 11;                // V^T chunks requested with K (the rest after the softmax)
+constexpr int kVtLate = 2 * NW - kVtEarly;
+template <int N>
+using VtTiles = unsigned char[NW][N][1024];  // [wave][chunk][lane*16]
 
 // The body takes every LDS region as a restrict pointer: once inlined, the compiler knows that the
 // score / statistics accesses never touch the tiles the V^T DMA writes, so it does not make them
 // wait for that DMA.
 template <int D, int NSPLIT>
-__device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles* __restrict__ vt_lo_p,
-                                           VtTiles* __restrict__ vt_hi_p, uint16_t* __restrict__ nk_lds,
+__device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles<kVtEarly>* __restrict__ vt_lo_p,
+                                           VtTiles<kVtLate>* __restrict__ vt_hi_p, uint16_t* __restrict__ nk_lds,
                                            uint16_t* __restrict__ sp, float* __restrict__ wmax,
                                            float* __restrict__ bsum) {
-  VtTiles& vt_lo = *vt_lo_p;
-  VtTiles& vt_hi = *vt_hi_p;
+  VtTiles<kVtEarly>& vt_lo = *vt_lo_p;
+  VtTiles<kVtLate>& vt_hi = *vt_hi_p;
   const int R = a.group;
 
   const int npairs = a.batch * a.kv_heads;
@@ -100,18 +106,18 @@ __device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles* __res
   // Every byte is requested before any compute: a wave stalled on a full memory queue cannot
   // compute anyway, and its K (requested first) has landed by the time its last DMA is queued.
   const uint32_t soff = 256u * db;  // value dims 16 db + col
-  // Every wave issues all 8 DMAs of a half (a chunk past the row's last one re-reads that last
+  // Every wave issues all the DMAs of each part (a chunk past the row's last one re-reads that last
   // chunk, which stays inside the pair's slots), so the compiler knows how many loads are in
   // flight behind each K load and waits for exactly the one it needs.
   const int c_last = n_chunks > 0 ? n_chunks - 1 : 0;
-  auto dma_v = [&](VtTiles& tiles, int c) {
+  auto dma_v = [&](auto& tiles, int c, int first) {  // chunk c into tile c - first
     const int cs = c < n_chunks ? c : c_last;
     const uint32_t voff = vt_operand_bytes(4 * cs + grp, col, D);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&tiles[w][c & (NW - 1)][0],
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&tiles[w][c - first][0],
                                              16, voff, soff, 0, kNonTemporal);
   };
 #pragma unroll
-  for (int c = 0; c < NW; ++c) dma_v(vt_lo, c);
+  for (int c = 0; c < kVtEarly; ++c) dma_v(vt_lo, c, 0);
   __builtin_amdgcn_sched_barrier(0);
   if (owner && lane < D / 8) reinterpret_cast<u32x4*>(nk_lds)[lane] = nkv;  // read back by this wave only
   const uint64_t vb0 = __ballot(ok0 && mb0 != 0);
@@ -162,7 +168,7 @@ __device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles* __res
   wg_barrier();  // block sums are in LDS
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int c = NW; c < 2 * NW; ++c) dma_v(vt_hi, c);
+  for (int c = kVtEarly; c < 2 * NW; ++c) dma_v(vt_hi, c, kVtEarly);
   __builtin_amdgcn_sched_barrier(0);
   const float pu = round_bf16(1.0f / (float)a.capacity);
 #pragma unroll
@@ -190,27 +196,30 @@ __device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles* __res
   const int cn = (int)(kr.new_slot >> 5), gn = (int)(kr.new_slot & 31) >> 3, en = (int)(kr.new_slot & 7);
   const int n_chunks2 = all_masked ? (a.capacity + 31) >> 5 : n_chunks;
   floatx4 oacc = {0.f, 0.f, 0.f, 0.f}, oacc1 = {0.f, 0.f, 0.f, 0.f};  // even / odd chunks
-  auto value_half = [&](VtTiles& tiles, int c_first) {
+  auto value_half = [&](auto& tiles, int c_first, auto count) {
+    constexpr int N = decltype(count)::value;
     // the appended slot's value into the staged tile (the lanes of the slot's 8-slot group)
-    if (has_new && cn >= c_first && cn < c_first + NW && grp == gn)
+    if (has_new && cn >= c_first && cn < c_first + N && grp == gn)
       *reinterpret_cast<uint16_t*>(&tiles[w][cn - c_first][16 * lane + 2 * en]) = (uint16_t)nvb;
-    u32x4 vt[NW];  // every operand read before the MFMA chain (LDS latency paid once)
-    bf16x8 pp[NW];
+    u32x4 vt[N];  // every operand read before the MFMA chain (LDS latency paid once)
+    bf16x8 pp[N];
 #pragma unroll
-    for (int i = 0; i < NW; ++i) {
+    for (int i = 0; i < N; ++i) {
       if (c_first + i < n_chunks) {
         vt[i] = *reinterpret_cast<const u32x4*>(&tiles[w][i][16 * lane]);
         pp[i] = prob_operand(sp, kStageStride, ((c_first + i) << 5) + 8 * grp, R, col);
       }
     }
 #pragma unroll
-    for (int i = 0; i < NW; i += 2) {
-      if (c_first + i < n_chunks) oacc = mfma16x16x32(as_bf16x8(vt[i]), pp[i], oacc);
-      if (c_first + i + 1 < n_chunks) oacc1 = mfma16x16x32(as_bf16x8(vt[i + 1]), pp[i + 1], oacc1);
+    for (int i = 0; i < N; ++i) {  // even chunks into oacc, odd ones into oacc1
+      if (c_first + i < n_chunks) {
+        if (((c_first + i) & 1) == 0) oacc = mfma16x16x32(as_bf16x8(vt[i]), pp[i], oacc);
+        else oacc1 = mfma16x16x32(as_bf16x8(vt[i]), pp[i], oacc1);
+      }
     }
   };
-  value_half(vt_lo, 0);
-  value_half(vt_hi, NW);
+  value_half(vt_lo, 0, std::integral_constant<int, kVtEarly>{});
+  value_half(vt_hi, kVtEarly, std::integral_constant<int, kVtLate>{});
   oacc += oacc1;
   for (int c = n_chunks; c < n_chunks2; ++c) {  // fully masked linear row: slots never scanned
     const u32x4 v = buffer_load16(rv, vt_operand_bytes(4 * c + grp, col, D), 256u * db);
@@ -243,8 +252,8 @@ __device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles* __res
 template <int D, int NSPLIT>
 __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_stage_kernel(G4DecodeArgs a) {
   static_assert(D / NSPLIT == 16 * NW, "one 16-row d-block of V^T per wave");
-  __shared__ __attribute__((aligned(1024))) VtTiles vt_lo;  // chunks 0..7
-  __shared__ __attribute__((aligned(1024))) VtTiles vt_hi;  // chunks 8..15
+  __shared__ __attribute__((aligned(1024))) VtTiles<kVtEarly> vt_lo;  // chunks 0..10
+  __shared__ __attribute__((aligned(1024))) VtTiles<kVtLate> vt_hi;   // chunks 11..15
   __shared__ __attribute__((aligned(16))) uint16_t nk_lds[D];
   extern __shared__ float smem[];
   uint16_t* sp = reinterpret_cast<uint16_t*>(smem);                      // [R][stride] scores, then probabilities
