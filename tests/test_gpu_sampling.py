@@ -326,6 +326,8 @@ def _top_k_case(device, B, V, temperature, top_k, top_p, *, dtype=torch.bfloat16
     (16, 32768, 1.0, 64, 0.95, torch.bfloat16, None),
     (256, 262144, 1.0, 50, 1.0, torch.bfloat16, 30.0),
     (256, 262144, 0.7, 50, 0.9, torch.bfloat16, 30.0),
+    (40, 8192, 0.9, 100, 0.8, torch.float32, 30.0),  # f32 rows read 8 columns per load
+    (20, 1001, 1.0, 30, 1.0, torch.bfloat16, 30.0),  # bf16 rows read column by column (V % 8 != 0)
 ])
 def test_native_top_k_matches_oracle(device, B, V, temperature, top_k, top_p, dtype, cap):
     """Vocabularies from TINY_A's 97 to the E2B shape's 262,144 columns (the reference harness's
