@@ -320,8 +320,12 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_k
 }
 
 // O = sum of the split partials (split order), bf16. Workgroup (pair, y) owns outputs
-// [256 y, 256 y + 256) of the pair's R x D; the partials of 8 splits are loaded before they are
-// added (in split order), so the loads overlap instead of forming one dependent chain per split.
+// [256 y, 256 y + 256) of the pair's R x D. The partials of the row's scanned splits (known from
+// the key range alone) are requested first, 64 splits per batch, before the statistics that only
+// tell whether the row is fully masked (then the unscanned splits below the capacity follow, still
+// in split order): one round trip per 64 splits instead of one per 8 behind the statistics' loads.
+constexpr int kCombineBatch = 64;
+
 __global__ __launch_bounds__(256) void decode_splitk_combine_kernel(G4DecodeArgs a, SplitKWorkspace ws) {
   __shared__ float mh[16], lh[16];
   const int R = a.group, D = a.head_dim;
@@ -331,20 +335,36 @@ __global__ __launch_bounds__(256) void decode_splitk_combine_kernel(G4DecodeArgs
   const int n_chunks = (kr.n_keys + 31) >> 5;
   const int n_splits_row = (n_chunks + 2 * NW - 1) / (2 * NW);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int idx = (int)blockIdx.y * 256 + tid;
+  const bool out_here = idx < R * D;
+  // a thread past the pair's outputs reads output 0's partials (in bounds, never stored)
+  const float* part = ws.partials + (int64_t)pair * ws.n_splits * R * D + (out_here ? idx : 0);
+  // v[j] = partial of split s + j, clamped to the last split (an L2 hit) where s + j >= n
+  auto load_batch = [&](int s, int n, float (&v)[kCombineBatch]) {
+#pragma unroll
+    for (int j = 0; j < kCombineBatch; ++j) v[j] = part[(int64_t)(s + j < n ? s + j : n - 1) * R * D];
+  };
+  auto add_batch = [](float o, int s, int n, const float (&v)[kCombineBatch]) {
+#pragma unroll
+    for (int j = 0; j < kCombineBatch; ++j)
+      if (s + j < n) o += v[j];
+    return o;
+  };
+  float v[kCombineBatch];
+  if (n_splits_row > 0) load_batch(0, n_splits_row, v);
   const bool all_masked = splitk_row_stats(ws, pair, R, n_splits_row, mh, lh, w, (int)(blockDim.x >> 6), lane);
   const int n = all_masked ? ws.n_splits : n_splits_row;
-  const int idx = (int)blockIdx.y * 256 + tid;
-  if (idx >= R * D) return;
-  const float* part = ws.partials + (int64_t)pair * ws.n_splits * R * D + idx;
+  if (!out_here) return;
   float o = 0.f;
   int s = 0;
-  for (; s + 8 <= n; s += 8) {
-    float v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = part[(int64_t)(s + j) * R * D];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o += v[j];
+  if (n_splits_row > 0) {
+    o = add_batch(o, 0, n_splits_row < kCombineBatch ? n_splits_row : kCombineBatch, v);
+    s = n_splits_row < kCombineBatch ? n_splits_row : kCombineBatch;
   }
-  for (; s < n; ++s) o += part[(int64_t)s * R * D];
+  for (; s < n; s += kCombineBatch) {
+    const int e = n - s < kCombineBatch ? n : s + kCombineBatch;  // splits [s, e) of this batch
+    load_batch(s, e, v);
+    o = add_batch(o, s, e, v);
+  }
   reinterpret_cast<uint16_t*>(a.out)[(int64_t)pair * R * D + idx] = (uint16_t)f32_to_bf16_bits(o);
 }

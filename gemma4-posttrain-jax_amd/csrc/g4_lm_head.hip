@@ -294,16 +294,34 @@ constexpr int kCombineThreads = 256;
 
 __global__ __launch_bounds__(kCombineThreads) void lm_head_combine_kernel(G4LmHeadSampleArgs a, int grid) {
   __shared__ LhState red[kCombineThreads];
-  const int row = blockIdx.x;
+  // Workgroups are dealt to the 8 XCDs round robin (blockIdx mod 8). The states of consecutive rows
+  // share cache lines (32 rows per 128-byte line of each array), so each XCD takes a contiguous
+  // block of batch / 8 rows: a line is fetched into one XCD's L2, not into all eight.
+  const int wg = (int)blockIdx.x;
+  const int row = a.batch % 8 == 0 ? (wg & 7) * (a.batch >> 3) + (wg >> 3) : wg;
   const LhStates ws = lh_states(a.workspace, grid);
   LhState st = {kF32Min, 0.f, -INFINITY, 0.f, 0x7fffffff};
-  for (int g = threadIdx.x; g < grid; g += kCombineThreads) {
-    const size_t i = (size_t)g * kLhRows + row;
-    lh_merge(st, LhState{ws.m[i], ws.s[i], ws.best[i], ws.bx[i], ws.idx[i]});
+  // states g = tid, tid + 256, ... merged in that order; two of them are requested before either
+  // is merged (one round trip for the 512-workgroup grid of 256 CUs)
+  for (int g0 = threadIdx.x; g0 < grid; g0 += 2 * kCombineThreads) {
+    LhState v[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int g = g0 + u * kCombineThreads;
+      if (g < grid) {
+        const size_t i = (size_t)g * kLhRows + row;
+        v[u] = LhState{ws.m[i], ws.s[i], ws.best[i], ws.bx[i], ws.idx[i]};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (g0 + u * kCombineThreads < grid) lh_merge(st, v[u]);
   }
+  // tree: at level h thread t < h merges thread t + h (h = 128, 64 through LDS, then 32 .. 1 by
+  // shuffles within wave 0, where lane t reads lane t ^ h = t + h)
   red[threadIdx.x] = st;
   __syncthreads();
-  for (int h = kCombineThreads / 2; h > 0; h >>= 1) {
+  for (int h = kCombineThreads / 2; h >= 64; h >>= 1) {
     if ((int)threadIdx.x < h) {
       LhState x = red[threadIdx.x];
       lh_merge(x, red[threadIdx.x + h]);
@@ -311,8 +329,14 @@ __global__ __launch_bounds__(kCombineThreads) void lm_head_combine_kernel(G4LmHe
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
-    const LhState t = red[0];
+  if (threadIdx.x < 64) {
+    LhState t = red[threadIdx.x];
+#pragma unroll
+    for (int h = 32; h >= 1; h >>= 1) {
+      const LhState y = lh_shfl(t, h);
+      if ((int)threadIdx.x < h) lh_merge(t, y);
+    }
+    if (threadIdx.x != 0) return;
     // only a row whose every score is -inf keeps no best: clamp the token into the vocab
     const int token = t.idx < 0 ? 0 : (t.idx >= a.vocab ? a.vocab - 1 : t.idx);
     a.token_out[row] = token;
