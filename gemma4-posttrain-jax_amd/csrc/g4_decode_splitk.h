@@ -226,7 +226,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_bf16_splitk_values_k
   extern __shared__ float smem[];
   const int R = a.group;
   uint16_t* sp = reinterpret_cast<uint16_t*>(smem);  // [R][stride] probabilities of the split
-  const int dh = (int)(blockIdx.x % DSPLIT), item = (int)(blockIdx.x / DSPLIT);
+  int item, dh;  // both value halves of a (pair, split) on one XCD
+  xcd_item_part((int)blockIdx.x, a.batch * a.kv_heads * ws.n_splits, DSPLIT, item, dh);
   const int pair = item / ws.n_splits, split = item % ws.n_splits;
   const int b = pair / a.kv_heads;
   const KeyRange kr = key_range(a, b);

@@ -57,7 +57,8 @@ __global__ __launch_bounds__(kTpWavesS * 64, (PREP && D <= 256) ? 4 : 1) void de
   __shared__ __attribute__((aligned(16))) uint16_t q_lds[PREP ? 16 * D : 1];  // [R][D] prepared q
   __shared__ __attribute__((aligned(16))) uint16_t nk_lds[PREP ? D : 1];      // prepared new K row
   const int R = a.group;
-  const int pair = (int)(blockIdx.x / parts), part = (int)(blockIdx.x % parts);
+  int pair, part;  // every part of a pair on one XCD
+  xcd_item_part((int)blockIdx.x, a.batch * a.kv_heads, parts, pair, part);
   const int b = pair / a.kv_heads;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -234,7 +235,8 @@ __global__ __launch_bounds__(tp_waves_v<NCH>() * 64) void decode_bf16_tp_values_
   extern __shared__ float smem[];
   uint16_t* sp = reinterpret_cast<uint16_t*>(smem);  // [R][kStride] probabilities
   const int R = a.group;
-  const int pair = (int)(blockIdx.x / kParts), part = (int)(blockIdx.x % kParts);
+  int pair, part;  // every part of a pair on one XCD
+  xcd_item_part((int)blockIdx.x, a.batch * a.kv_heads, kParts, pair, part);
   const int b = pair / a.kv_heads;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
