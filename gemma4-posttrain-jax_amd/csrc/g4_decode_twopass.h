@@ -20,7 +20,10 @@
 //
 // Workspace: scores bf16 [pairs][R][row_slots], row_slots = 512 (capacity <= 512) or 1024.
 
-constexpr int kTpWavesS = 4;  // waves per scores workgroup
+// Waves (32-slot K chunks) per scores workgroup. With the fused preparation every workgroup
+// prepares the pair's q heads for itself, so 8 waves (two workgroups per 512-slot row) repeat it
+// half as often as 4 (E2B decode step 4.484 -> 4.473 ms; 16 waves, one workgroup per row: 4.561).
+constexpr int kTpWavesS = 8;
 // Waves per values workgroup. Every workgroup forms the exact probabilities of the pair's heads for
 // itself, so fewer, larger workgroups repeat less of that work: 8 waves (two workgroups per (b, kv
 // head) at D = 256) for rows of up to 16 chunks, where the kernel holds 102 VGPRs (E2B decode step
@@ -46,11 +49,11 @@ __host__ __device__ inline size_t twopass_workspace_bytes(int npairs, int R, int
 // and stored to the cache) and the new V row (stored as the V^T column the values launch reads).
 // The K chunk is requested before any of this, so the preparation runs while it is in flight.
 
-// PREP: at most 128 registers (4 waves per SIMD; the q operand is read from LDS slice by slice, so
-// nothing spills: E2B decode step 4.76 -> 4.72 ms against 3 waves per SIMD). Head dim 512 holds
-// 128 registers of K alone, so it takes no occupancy bound.
+// PREP: at most 128 registers (two 8-wave workgroups per CU, 4 waves per SIMD; the q operand is read
+// from LDS slice by slice, so nothing spills: E2B decode step 4.76 -> 4.72 ms against 3 waves per
+// SIMD). Head dim 512 holds 128 registers of K alone, so it takes no occupancy bound.
 template <int D, bool PREP>
-__global__ __launch_bounds__(kTpWavesS * 64, (PREP && D <= 256) ? 4 : 1) void decode_bf16_tp_scores_kernel(G4DecodeArgs a, uint16_t* ws,
+__global__ __launch_bounds__(kTpWavesS * 64, (PREP && D <= 256) ? 16 / kTpWavesS : 1) void decode_bf16_tp_scores_kernel(G4DecodeArgs a, uint16_t* ws,
                                                                               int parts, int row_slots,
                                                                               G4DecodePrep pp) {
   constexpr int PER = D / 64;
