@@ -27,8 +27,8 @@ constexpr int kTpWavesS = 8;
 // Waves per values workgroup. Every workgroup forms the exact probabilities of the pair's heads for
 // itself, so fewer, larger workgroups repeat less of that work: 8 waves (two workgroups per (b, kv
 // head) at D = 256) for rows of up to 16 chunks, where the kernel holds 102 VGPRs (E2B decode step
-// 4.86 -> 4.73 ms against 4 waves); 4 waves for longer rows, whose 152+ VGPRs would leave one
-// 8-wave workgroup per CU.
+// 4.86 -> 4.73 ms against 4 waves; 16 waves, one workgroup per pair: 4.50 -> 4.60 ms); 4 waves for
+// longer rows, whose 152+ VGPRs would leave one 8-wave workgroup per CU.
 template <int NCH>
 constexpr int tp_waves_v() { return NCH <= 16 ? 8 : 4; }
 constexpr int kTpMaxSlots = 1024;
