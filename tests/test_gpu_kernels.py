@@ -121,6 +121,61 @@ def test_append_with_norms_and_q_matches_oracle(device, dtype, D):
     np.testing.assert_allclose(gv, ref.value, atol=tol, rtol=0)
 
 
+@pytest.mark.parametrize("D", [128, 256, 512])
+@pytest.mark.parametrize("ring", [True, False])
+def test_append_tiles_match_token_by_token_appends(device, D, ring):
+    """Prefill-sized bf16 appends (8 tokens per workgroup, V staged in LDS and stored as whole 16-byte
+    pieces where the 8 slots form one aligned group) against the same chunk appended one token at a
+    time (the one-token kernel): every cache element, chunk output and prepared q bit for bit. Rows
+    start on and off an 8-slot boundary; the ring's chunk is longer than the ring; S = 37 leaves a
+    partial last tile."""
+
+    rng = np.random.default_rng(D + ring)
+    dtype = O.BF16
+    B, S, H, R = 4, 37, 2, 4
+    cap = 32 if ring else 96
+    starts = np.array([0, 8, 5, 43] if ring else [0, 8, 3, 40], np.int32)
+    width = (H * R + 2 * H) * D
+    rows = to_dev(_rand(rng, (B, S, width), dtype), dtype, device)
+    qn = to_dev(O.cast(1 + 0.3 * rng.standard_normal(D), dtype), dtype, device)
+    kn = to_dev(O.cast(1 + 0.3 * rng.standard_normal(D), dtype), dtype, device)
+    pos = starts[:, None] + np.arange(S, dtype=np.int32)[None, :]
+    cos, sin = O.rotary_values(np.float32(1) / np.power(np.float32(1e4), np.arange(0, D, 2, dtype=np.float32) / D), pos)
+    cos_d, sin_d = torch.from_numpy(cos).to(device), torch.from_numpy(sin).to(device)
+    flags = (_lib.G4_APPEND_NORM_Q | _lib.G4_APPEND_ROPE_Q | _lib.G4_APPEND_NORM_K | _lib.G4_APPEND_ROPE_K
+             | _lib.G4_APPEND_NORM_V)
+    q = rows[:, :, : H * R * D].view(B, S, H, R, D)
+    k = rows[:, :, H * R * D: (H * R + H) * D].view(B, S, H, D)
+    v = rows[:, :, (H * R + H) * D:].view(B, S, H, D)
+    td = torch.bfloat16
+    wp = torch.from_numpy(starts).to(device)
+
+    tiled = new_layer_cache(B, H, D, cap, ring, td, device)
+    q_out = torch.empty((B, S, H, R, D), dtype=td, device=device)
+    k_out = torch.empty((B, H, 2, D // 32, 2, 16, 32), dtype=td, device=device)  # 64 chunk slots
+    vt_out = torch.zeros((B, H, 8, D, 8), dtype=td, device=device)
+    kernels.kv_append(tiled, k, v, write_pos=wp, flags=flags, eps=1e-6, q=q, q_out=q_out, q_norm_weight=qn,
+                      k_norm_weight=kn, rope_cos=cos_d, rope_sin=sin_d, k_out=k_out, vt_out=vt_out)
+
+    single = new_layer_cache(B, H, D, cap, ring, td, device)
+    chunk = new_layer_cache(B, H, D, 64, False, td, device)  # token s at slot s: the chunk outputs' layout
+    q_one = torch.empty((B, S, H, R, D), dtype=td, device=device)
+    for s in range(S):
+        qs = torch.empty((B, 1, H, R, D), dtype=td, device=device)
+        args = dict(flags=flags, eps=1e-6, q=q[:, s:s + 1], q_out=qs, q_norm_weight=qn, k_norm_weight=kn,
+                    rope_cos=cos_d[:, s:s + 1].contiguous(), rope_sin=sin_d[:, s:s + 1].contiguous())
+        if not ring or s >= S - cap:  # a ring keeps the chunk's last `cap` tokens
+            kernels.kv_append(single, k[:, s:s + 1], v[:, s:s + 1], write_pos=wp + s, **args)
+        kernels.kv_append(chunk, k[:, s:s + 1], v[:, s:s + 1], write_pos=s, **args)
+        q_one[:, s:s + 1] = qs
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits(q_out), bits(q_one))
+    np.testing.assert_array_equal(bits(tiled.key), bits(single.key))
+    np.testing.assert_array_equal(bits(tiled.value_t), bits(single.value_t))
+    np.testing.assert_array_equal(bits(ungroup_keys(k_out)[:, :, :S]), bits(ungroup_keys(chunk.key)[:, :, :S]))
+    np.testing.assert_array_equal(bits(ungroup_values(vt_out)[:, :, :S]), bits(ungroup_values(chunk.value_t)[:, :, :S]))
+
+
 # --- decode attention -----------------------------------------------------------------------------
 
 
