@@ -128,8 +128,8 @@ __global__ __launch_bounds__(1024) void append_kernel(G4AppendArgs a) {
 // (a cache start and ring size that are multiples of 8) their V rows are staged in LDS and stored as
 // whole 16-byte pieces, 16 D contiguous bytes per head, and the chunk copy (vt_out) likewise. Other
 // workgroups store V element by element as append_kernel does. Same arithmetic and destinations as
-// append_kernel (E2B prefill shape, B 256 x S 256, D 256: a ring layer with its chunk copy 657 -> 401
-// us, a linear layer 497 -> 332 us, q alone 251 -> 217 us).
+// append_kernel (E2B prefill shape, B 256 x S 256, D 256: a ring layer with its chunk copy 657 -> 421
+// us, a linear layer 494 -> 353 us, q alone 251 -> 232 us).
 constexpr int kTileTok = 8;
 constexpr int kTileThreads = 512;
 constexpr int kTileVtBytes = 32 * 1024;  // LDS for the staged V rows: kv_heads * D * 16 bytes at most
