@@ -18,8 +18,9 @@
 //
 // The appended token: the wave that scores the chunk holding the slot stages the new K row in
 // LDS for itself (no barrier) and substitutes it into that chunk's K operand registers; every
-// wave writes the new V value into its own staged tile once its DMA has landed. The cache
-// itself is written last (after every load of the workgroup).
+// wave writes the new V value into its own staged tile once its DMA has landed and stores the
+// patched 16-byte pieces to the cache. The K row is written last (after every load of the
+// workgroup).
 //
 // The softmax runs on all 512 threads: thread t owns 4 consecutive (head, slot) entries of the
 // [R][512] score array, so no lanes sit idle behind the R <= 16 MFMA columns.
@@ -198,9 +199,16 @@ __device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles<kVtEar
   floatx4 oacc = {0.f, 0.f, 0.f, 0.f}, oacc1 = {0.f, 0.f, 0.f, 0.f};  // even / odd chunks
   auto value_half = [&](auto& tiles, int c_first, auto count) {
     constexpr int N = decltype(count)::value;
-    // the appended slot's value into the staged tile (the lanes of the slot's 8-slot group)
-    if (has_new && cn >= c_first && cn < c_first + N && grp == gn)
+    // the appended slot's value into the staged tile (the lanes of the slot's 8-slot group), and that
+    // patched 16-byte piece (8 slots of one value dim) into the cache: whole pieces, 256 contiguous
+    // bytes per wave, instead of one two-byte value in every 16 bytes of them (configs[1]: 15.20 ->
+    // 14.94 us). Only this workgroup reads its dims' pieces, so nothing it still loads can see it.
+    if (has_new && cn >= c_first && cn < c_first + N && grp == gn) {
       *reinterpret_cast<uint16_t*>(&tiles[w][cn - c_first][16 * lane + 2 * en]) = (uint16_t)nvb;
+      uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
+      *reinterpret_cast<u32x4*>(cv + vt_index(kr.new_slot & ~(int64_t)7, 16 * db + col, D)) =
+          *reinterpret_cast<const u32x4*>(&tiles[w][cn - c_first][16 * lane]);
+    }
     u32x4 vt[N];  // every operand read before the MFMA chain (LDS latency paid once)
     bf16x8 pp[N];
 #pragma unroll
@@ -226,19 +234,15 @@ __device__ __forceinline__ void stage_body(const G4DecodeArgs& a, VtTiles<kVtEar
     oacc = mfma16x16x32(as_bf16x8(v), prob_operand(sp, kStageStride, (c << 5) + 8 * grp, R, col), oacc);
   }
 
-  // ---- the fused append's cache write (after every cache load of this workgroup) ---------------
-  // Workgroup h writes K row elements [h*D/NSPLIT, (h+1)*D/NSPLIT) and its own V^T rows. The
-  // other workgroup of the pair may still read that K row; it substitutes the staged row for
-  // it, so what it reads does not matter.
+  // ---- the fused append's K row write (after every cache load of this workgroup) ---------------
+  // Workgroup h writes K row elements [h*D/NSPLIT, (h+1)*D/NSPLIT) (its V^T pieces went out with the
+  // value MFMAs). The other workgroup of the pair may still read that K row; it substitutes the
+  // staged row for it, so what it reads does not matter.
   if (has_new) {
     constexpr int DS = D / NSPLIT;  // K row elements [h*DS, (h+1)*DS): lanes holding 8 of them each
     uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D;
     if (owner && lane >= h * DS / 8 && lane < (h + 1) * DS / 8)
       *reinterpret_cast<u32x4*>(ck + kt_index(kr.new_slot, 8 * lane, D)) = nkv;
-    if (grp == 0) {
-      uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
-      cv[vt_index(kr.new_slot, 16 * db + col, D)] = (uint16_t)nvb;
-    }
   }
   // lane (grp, col < R) holds O^T[d = 16*db + 4*grp + j][head col]
   if (col < R) {
