@@ -49,11 +49,12 @@ __host__ __device__ inline size_t twopass_workspace_bytes(int npairs, int R, int
 // and stored to the cache) and the new V row (stored as the V^T column the values launch reads).
 // The K chunk is requested before any of this, so the preparation runs while it is in flight.
 
-// PREP: at most 128 registers (two 8-wave workgroups per CU, 4 waves per SIMD; the q operand is read
-// from LDS slice by slice, so nothing spills: E2B decode step 4.76 -> 4.72 ms against 3 waves per
-// SIMD). Head dim 512 holds 128 registers of K alone, so it takes no occupancy bound.
+// PREP: at most 128 registers (HIP's second launch bound is the minimum waves per SIMD: 4, two
+// 8-wave workgroups per CU; the q operand is read from LDS slice by slice, so nothing spills: E2B
+// decode step 4.76 -> 4.72 ms against 3 waves per SIMD). Head dim 512 holds 128 registers of K alone,
+// so it takes no occupancy bound.
 template <int D, bool PREP>
-__global__ __launch_bounds__(kTpWavesS * 64, (PREP && D <= 256) ? 16 / kTpWavesS : 1) void decode_bf16_tp_scores_kernel(G4DecodeArgs a, uint16_t* ws,
+__global__ __launch_bounds__(kTpWavesS * 64, (PREP && D <= 256) ? 4 : 1) void decode_bf16_tp_scores_kernel(G4DecodeArgs a, uint16_t* ws,
                                                                               int parts, int row_slots,
                                                                               G4DecodePrep pp) {
   constexpr int PER = D / 64;
