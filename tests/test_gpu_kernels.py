@@ -341,6 +341,21 @@ def test_decode_split_keys_long_context(device, D):
                  fused=True, seed=24)
 
 
+def test_decode_split_keys_beyond_one_combine_batch(device):
+    """Split-K over more than 64 key splits (capacity 40000: 79 splits of 512 slots), so the combine
+    adds a row's partials in two batches of loads: a row over every split, a fully masked row (the
+    uniform average over all 79 splits) and a left-padded one; 6 pairs x 79 splits, not a multiple
+    of 8 items."""
+
+    B, H, R, D, C = 3, 2, 4, 256, 40000
+    q_pos = np.array([39999, 35000, 20000])
+    key_mask = np.ones((B, C), bool)
+    key_mask[1, :] = False
+    key_mask[2, :5000] = False
+    _decode_case(device, O.BF16, B=B, H=H, R=R, D=D, cap=C, ring=False, window=0, q_pos=q_pos, key_mask=key_mask,
+                 fused=True, seed=31)
+
+
 @pytest.mark.parametrize("D", [128, 256, 512])
 def test_decode_split_keys_forced_matches_one_pass(device, D):
     """num_splits = G4_DECODE_SPLIT_KEYS on a 768-slot cache (where the one-pass kernel also
