@@ -129,11 +129,24 @@ __global__ __launch_bounds__(NW * 64) void prefill_bf16_lds_kernel(G4PrefillArgs
   // 1.10 -> 0.99 ms against pair-major order). Windowed rows cost the same from block to block;
   // pair-major order (workgroup i: block nblk - 1 - i % nblk of pair i / nblk) keeps the workgroups in
   // flight on different key offsets, which measured faster there (sliding layer 0.36 against
-  // 0.49 ms block-major).
+  // 0.49 ms block-major). There, with a multiple of 8 pairs, consecutive blocks of a pair go to one
+  // XCD (workgroups are dealt to the 8 XCDs round robin, i mod 8), so the overlapping key windows
+  // of neighbouring blocks meet in one L2 (0.290-0.294 -> 0.278-0.283 ms); block-major order already
+  // keeps a pair on one XCD.
   const int npairs = a.batch * H;
   const bool blk_major = a.window <= 0 || a.window >= S;
-  const int blk = nblk - 1 - (int)(blk_major ? blockIdx.x / (unsigned)npairs : blockIdx.x % (unsigned)nblk);
-  const int pair = (int)(blk_major ? blockIdx.x % (unsigned)npairs : blockIdx.x / (unsigned)nblk);
+  int blk, pair;
+  if (blk_major) {
+    blk = nblk - 1 - (int)(blockIdx.x / (unsigned)npairs);
+    pair = (int)(blockIdx.x % (unsigned)npairs);
+  } else if (npairs % 8 == 0) {
+    const int i = (int)blockIdx.x, j = i >> 3;
+    blk = nblk - 1 - j % nblk;
+    pair = (j / nblk) * 8 + (i & 7);
+  } else {
+    blk = nblk - 1 - (int)(blockIdx.x % (unsigned)nblk);
+    pair = (int)(blockIdx.x / (unsigned)nblk);
+  }
   const int b = pair / H, h = pair - b * H;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
