@@ -12,7 +12,8 @@ rollout; ``rollout_tok_s_b256`` — 256 x 512 tokens over prefill + all decode s
 harness's slot tokens/s); and the oracle's CPU time for the same step.
 
 Also: ``long_context_decode`` (``configs[2]``, split-K decode over a 32768-slot linear cache,
-HBM-bound) and ``prefill_attention`` (``configs[3]``, causal / sliding attention on MFMA).
+HBM-bound), ``e2b_decode_attention`` (one sliding layer's decode attention at the ``configs[4]``
+batch of 256) and ``prefill_attention`` (``configs[3]``, causal / sliding attention on MFMA).
 
 Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2b] [--no-cpu] [--no-extra]``.
 """
@@ -185,10 +186,11 @@ def _graph_time(step, n_warm: int, n_timed: int) -> float:
     return e0.elapsed_time(e1) / n_timed
 
 
-def bench_long_context_decode(steps: int = 16, warmup: int = 4) -> dict:
+def bench_long_context_decode(steps: int = 16, warmup: int = 150) -> dict:
     """global-layer decode over a linear cache, B=16, Hq=8/Hkv=2, D=256,
     capacity 32768, per-row lengths U[1024, 32768] growing by one per step (split-K path).
-    Algorithmic bytes: K+V of every valid slot once, Q in, O out, the new K/V row."""
+    Algorithmic bytes: K+V of every valid slot once, Q in, O out, the new K/V row. The `warmup`
+    graphed steps (~16 ms) bring the GPU to its sustained clock first."""
 
     import torch
 
@@ -224,6 +226,49 @@ def bench_long_context_decode(steps: int = 16, warmup: int = 4) -> dict:
     small = Bq * HQ * D * 2 * 2 + Bq * HKV * D * 2 * 2 * 2
     gbs = (kv_bytes + small) / (ms * 1e-3) / 1e9
     return {"ms_per_step": ms, "gbs": gbs, "bytes_per_step": kv_bytes + small}
+
+
+def bench_e2b_decode_attention(steps: int = 64, warmup: int = 300, batch: int = 256) -> dict:
+    """The decode attention of one sliding layer of the configs[4] model at its rollout batch: B=256,
+    Hq=8/Hkv=2, D=256, a full 512-slot ring (positions U[1536, 2048), as configs[1]), one token
+    appended and attended per step (the library's automatic choice: the two-launch path). NCACHE
+    rotating 256 MiB caches as in the headline; `warmup` graphed steps (~15 ms) first. Algorithmic
+    bytes as the headline's: K+V of every valid slot once, Q in, O out, the new K/V row read and
+    written."""
+
+    import torch
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    from gemma4_posttrain_jax_amd import kernels
+    from gemma4_posttrain_jax_amd.kvcache import new_layer_cache
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(5)
+    layers = []
+    for _ in range(NCACHE):
+        layer = new_layer_cache(batch, HKV, D, W, True, torch.bfloat16, dev)
+        layer.key.normal_(generator=g)
+        layer.value_t.normal_(generator=g)
+        layers.append(layer)
+    rng = np.random.default_rng(5)
+    pos0 = rng.integers(1536, 2048, batch).astype(np.int32)
+    total = warmup + steps
+    q_pos = torch.from_numpy(pos0[None, :] + np.arange(total, dtype=np.int32)[:, None]).to(dev).contiguous()
+    key_mask = torch.ones((batch, CTX + total + 64), dtype=torch.bool, device=dev)
+    q = torch.randn((total, batch, HKV, R, D), device=dev, generator=g).to(torch.bfloat16)
+    nk = torch.randn((total, batch, HKV, D), device=dev, generator=g).to(torch.bfloat16)
+    nv = torch.randn((total, batch, HKV, D), device=dev, generator=g).to(torch.bfloat16)
+    out = torch.empty((total, batch, HKV, R, D), device=dev, dtype=torch.bfloat16)
+
+    def step(i):
+        kernels.decode_attention(layers[i % NCACHE], q[i], key_mask, q_pos=q_pos[i], window=W, out=out[i],
+                                 new_k=nk[i], new_v=nv[i])
+
+    ms = _graph_time(step, warmup, steps)
+    nbytes = batch * HKV * W * D * 2 * 2 + 2 * batch * HQ * D * 2 + batch * HKV * D * 2 * 2 * 2
+    return {"ms_per_step": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes_per_step": nbytes}
 
 
 def bench_prefill(reps: int = 10, warmup: int = 40) -> dict:
@@ -622,6 +667,11 @@ def main() -> int:
         line["long_context_decode"] = {"workload": "configs[2]: B16 Hq8/Hkv2 D256, linear cache 32768, ragged "
                                        "lengths U[1024,32768], split-K", "ms_per_step": round(lc["ms_per_step"], 4),
                                        "GB/s": round(lc["gbs"], 1), "frac_hbm_peak": round(lc["gbs"] / HBM_PEAK_GBS, 4)}
+        ea = bench_e2b_decode_attention()
+        line["e2b_decode_attention"] = {"workload": "configs[4] shape: one sliding layer's decode attention at B256 "
+                                        "Hq8/Hkv2 D256, full 512-slot ring, 1-token append + attend, two-launch path",
+                                        "ms_per_step": round(ea["ms_per_step"], 4), "GB/s": round(ea["gbs"], 1),
+                                        "frac_hbm_peak": round(ea["gbs"] / HBM_PEAK_GBS, 4)}
         pf = bench_prefill()
         line["prefill_attention"] = {
             "workload": "configs[3]: B8 S4096 Hq8/Hkv2 D256 bf16 attention, per layer",

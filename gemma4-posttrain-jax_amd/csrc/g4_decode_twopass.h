@@ -49,17 +49,20 @@ __host__ __device__ inline size_t twopass_workspace_bytes(int npairs, int R, int
 // and stored to the cache) and the new V row (stored as the V^T column the values launch reads).
 // The K chunk is requested before any of this, so the preparation runs while it is in flight.
 
-// PREP: at most 128 registers (HIP's second launch bound is the minimum waves per SIMD: 4, two
-// 8-wave workgroups per CU; the q operand is read from LDS slice by slice, so nothing spills: E2B
-// decode step 4.76 -> 4.72 ms against 3 waves per SIMD). Head dim 512 holds 128 registers of K alone,
-// so it takes no occupancy bound.
+// At most 128 registers up to head dim 256 (HIP's second launch bound is the minimum waves per SIMD:
+// 4, two 8-wave workgroups per CU; the q operand is read from LDS slice by slice, so nothing spills:
+// E2B decode step 4.76 -> 4.72 ms against 3 waves per SIMD). Without PREP the q rows are staged in
+// LDS from q for the same reason (with the operand in registers, 138 registers and one workgroup
+// per CU: 30.1 us for a full 512-slot ring at B = 256; at head dim 512, 36 bytes of spills). Head
+// dim 512 holds 128 registers of K alone, so it takes no occupancy bound.
 template <int D, bool PREP>
-__global__ __launch_bounds__(kTpWavesS * 64, (PREP && D <= 256) ? 4 : 1) void decode_bf16_tp_scores_kernel(G4DecodeArgs a, uint16_t* ws,
+__global__ __launch_bounds__(kTpWavesS * 64, D <= 256 ? 4 : 1) void decode_bf16_tp_scores_kernel(G4DecodeArgs a, uint16_t* ws,
                                                                               int parts, int row_slots,
                                                                               G4DecodePrep pp) {
   constexpr int PER = D / 64;
-  __shared__ __attribute__((aligned(16))) uint16_t q_lds[PREP ? 16 * D : 1];  // [R][D] prepared q
-  __shared__ __attribute__((aligned(16))) uint16_t nk_lds[PREP ? D : 1];      // prepared new K row
+  constexpr bool kQlds = PREP || D >= 256;  // the q operand read from LDS
+  __shared__ __attribute__((aligned(16))) uint16_t q_lds[kQlds ? 16 * D : 1];  // [R][D] (prepared) q
+  __shared__ __attribute__((aligned(16))) uint16_t nk_lds[D];  // the (prepared) new K row, for the writer wave
   const int R = a.group;
   int pair, part;  // every part of a pair on one XCD
   xcd_item_part((int)blockIdx.x, a.batch * a.kv_heads, parts, pair, part);
@@ -73,7 +76,6 @@ __global__ __launch_bounds__(kTpWavesS * 64, (PREP && D <= 256) ? 4 : 1) void de
   const int chunk = part * kTpWavesS + w;
   const int new_chunk = kr.new_slot >= 0 ? (int)(kr.new_slot >> 5) : -1;
   const bool writer = new_chunk == chunk;  // the wave that scores the appended slot's chunk
-  const uint16_t* nk = PREP ? nk_lds : reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D;
 
   // PREP: the preparation's loads go out first (they return before the K chunk: vector loads
   // complete in issue order), so its arithmetic runs while the K chunk is in flight
@@ -94,6 +96,28 @@ __global__ __launch_bounds__(kTpWavesS * 64, (PREP && D <= 256) ? 4 : 1) void de
                                    (int64_t)b * pp.in_row_stride + (int64_t)h * D,
                                w == 0 ? reinterpret_cast<const uint16_t*>(pp.k_norm_weight) : nullptr,
                                w == 0 && (pp.flags & G4_APPEND_ROPE_K) != 0, rc, rs, lane);
+  }
+  // without PREP from D = 256: thread t's 16-byte pieces t, t + 512 of the pair's q rows, requested
+  // ahead of the K chunk and stored to LDS once they land
+  constexpr int kQPieces = kQlds && !PREP ? (16 * D / 8 + kTpWavesS * 64 - 1) / (kTpWavesS * 64) : 1;
+  u32x4 qv[kQPieces];
+  const int tid = threadIdx.x;
+  if constexpr (kQlds && !PREP) {
+#pragma unroll
+    for (int j = 0; j < kQPieces; ++j) {
+      const int t = tid + kTpWavesS * 64 * j;
+      qv[j] = t < R * D / 8 ? load16(reinterpret_cast<const uint16_t*>(a.q) + (int64_t)pair * R * D + 8 * t)
+                            : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // without PREP: the writer wave's 16-byte pieces of the new K and V rows (lane l < D / 8: dims
+  // 8 l .. 8 l + 7), also requested ahead of the K chunk, so that neither the K substitution nor
+  // the cache stores at the end wait on a load (52.2 -> 48.x us per step for a full 512-slot ring
+  // at B = 256 against loading them where they are used)
+  u32x4 nkv = {0u, 0u, 0u, 0u}, nvv = {0u, 0u, 0u, 0u};
+  if (!PREP && writer && lane < D / 8) {
+    nkv = load16(reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D + 8 * lane);
+    nvv = load16(reinterpret_cast<const uint16_t*>(a.new_v) + (int64_t)pair * D + 8 * lane);
   }
   u32x4 kv[2][D / 32];
   if (chunk < n_chunks) {
@@ -128,19 +152,27 @@ __global__ __launch_bounds__(kTpWavesS * 64, (PREP && D <= 256) ? 4 : 1) void de
       }
     }
     wg_barrier();  // prepared q rows (and the new K row) are in LDS
+  } else if constexpr (kQlds) {
+#pragma unroll
+    for (int j = 0; j < kQPieces; ++j) {
+      const int t = tid + kTpWavesS * 64 * j;
+      if (t < R * D / 8) reinterpret_cast<u32x4*>(q_lds)[t] = qv[j];
+    }
+    wg_barrier();  // q rows in LDS
   }
 
+  if (!PREP && writer && lane < D / 8) reinterpret_cast<u32x4*>(nk_lds)[lane] = nkv;  // read back by this wave only
   if (chunk < n_chunks) {
     bf16x8 qop[D / 32];
 #pragma unroll
     for (int s = 0; s < D / 32; ++s) {
-      if constexpr (!PREP) qop[s] = q_operand_global(a, pair, R, D, col, grp, s);
+      if constexpr (!kQlds) qop[s] = q_operand_global(a, pair, R, D, col, grp, s);
     }
     uint8_t mb;
     const bool ok = slot_valid_flat(a, b, kr, (chunk << 5) + (lane & 31), mb);
     const uint64_t vbits = __ballot(ok && mb != 0);
-    if (writer && (!PREP || pp.k_raw)) patch_k_sel<D>(kv, nk, kr.new_slot, chunk << 5, col, grp);
-    if constexpr (PREP)
+    if (writer && (!PREP || pp.k_raw)) patch_k_sel<D>(kv, nk_lds, kr.new_slot, chunk << 5, col, grp);
+    if constexpr (kQlds)
       score_to_lds_qlds<D>(kv, q_lds, vbits, ws + (int64_t)pair * R * row_slots, row_slots, chunk << 5, R, col, grp,
                            kBf16Min);
     else
@@ -158,12 +190,13 @@ __global__ __launch_bounds__(kTpWavesS * 64, (PREP && D <= 256) ? 4 : 1) void de
         *reinterpret_cast<u32x4*>(ck + kt_index(kr.new_slot, 8 * lane, D)) = *reinterpret_cast<const u32x4*>(nk_lds + 8 * lane);
     }
   }
-  if (!PREP && writer) {
+  if (!PREP && writer && lane < D / 8) {
     uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D;
-    if (lane < D / 8) *reinterpret_cast<u32x4*>(ck + kt_index(kr.new_slot, 8 * lane, D)) = load16(nk + 8 * lane);
+    *reinterpret_cast<u32x4*>(ck + kt_index(kr.new_slot, 8 * lane, D)) = nkv;
     uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
-    const uint16_t* nv = reinterpret_cast<const uint16_t*>(a.new_v) + (int64_t)pair * D;
-    for (int d = lane; d < D; d += 64) cv[vt_index(kr.new_slot, d, D)] = nv[d];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      cv[vt_index(kr.new_slot, 8 * lane + e, D)] = (uint16_t)((e & 1) ? nvv[e >> 1] >> 16 : nvv[e >> 1] & 0xffffu);
   }
 }
 
