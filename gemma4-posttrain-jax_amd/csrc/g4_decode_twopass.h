@@ -6,10 +6,11 @@
 // softmax runs behind barriers and the value pass follows, so every CU ends each pair with a
 // compute tail during which it has no loads in flight. Here each launch is a plain stream of
 // small independent workgroups, so one workgroup's tail overlaps the next one's loads:
-//   scores  one wave per 32-slot chunk: K into registers, MFMA against the register-held q
-//           operand, bf16-rounded masked scores into the workspace. The wave whose chunk holds the
-//           appended slot substitutes the new K row and, after its loads, writes the slot back to
-//           the cache (K row and V^T column).
+//   scores  one wave per 32-slot chunk: K into registers, MFMA against the q operand (read from
+//           LDS from head dim 256), bf16-rounded masked scores into the workspace. The wave whose
+//           chunk holds the appended slot substitutes the new K row and, once its loads have
+//           landed, writes the slot back to the cache as whole lines (the K lines it shares with
+//           its neighbour slot, and, without the fused preparation, the slot's 8-slot V^T group).
 //   values  one wave per 16-row d-block of V^T: the wave requests its first score row and its
 //           whole V^T block (16 rows x the row's chunks, registers) right behind it, forms the
 //           exact probabilities bf16(exp(s - m) / l) of its head while V is in flight (one LDS
@@ -114,10 +115,23 @@ __global__ __launch_bounds__(kTpWavesS * 64, D <= 256 ? 4 : 1) void decode_bf16_
   // 8 l .. 8 l + 7), also requested ahead of the K chunk, so that neither the K substitution nor
   // the cache stores at the end wait on a load (52.2 -> 48.x us per step for a full 512-slot ring
   // at B = 256 against loading them where they are used)
-  u32x4 nkv = {0u, 0u, 0u, 0u}, nvv = {0u, 0u, 0u, 0u};
-  if (!PREP && writer && lane < D / 8) {
-    nkv = load16(reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D + 8 * lane);
-    nvv = load16(reinterpret_cast<const uint16_t*>(a.new_v) + (int64_t)pair * D + 8 * lane);
+  u32x4 nkv = {0u, 0u, 0u, 0u};
+  if (!PREP && writer && lane < D / 8) nkv = load16(reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D + 8 * lane);
+  // ... and the appended slot's 8-slot group of the value cache (lane l: the 16-byte pieces of dims
+  // l + 64 i) with the new value of each of those dims: the group is patched and stored back as
+  // whole 16-byte pieces (whole lines) as soon as these land, before the scores (no load of this
+  // launch reads the value cache; 50.5 -> 50.0 us against 2-byte stores of the column)
+  constexpr int kVp = D / 64;
+  u32x4 gv[kVp];
+  uint16_t nvd[kVp];
+  uint16_t* const cv_grp = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride +
+                           (writer ? vt_index(kr.new_slot & ~(int64_t)7, 0, D) : 0);
+  if (!PREP && writer) {
+#pragma unroll
+    for (int i = 0; i < kVp; ++i) {
+      gv[i] = load16(cv_grp + 8 * (lane + 64 * i));
+      nvd[i] = reinterpret_cast<const uint16_t*>(a.new_v)[(int64_t)pair * D + lane + 64 * i];
+    }
   }
   u32x4 kv[2][D / 32];
   if (chunk < n_chunks) {
@@ -161,7 +175,18 @@ __global__ __launch_bounds__(kTpWavesS * 64, D <= 256 ? 4 : 1) void decode_bf16_
     wg_barrier();  // q rows in LDS
   }
 
-  if (!PREP && writer && lane < D / 8) reinterpret_cast<u32x4*>(nk_lds)[lane] = nkv;  // read back by this wave only
+  if (!PREP && writer) {
+    if (lane < D / 8) reinterpret_cast<u32x4*>(nk_lds)[lane] = nkv;  // read back by this wave only
+    const int e = (int)(kr.new_slot & 7), wi = e >> 1;
+#pragma unroll
+    for (int i = 0; i < kVp; ++i) {
+      u32x4 g = gv[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (j == wi) g[j] = (e & 1) ? (g[j] & 0xffffu) | ((uint32_t)nvd[i] << 16) : (g[j] & 0xffff0000u) | nvd[i];
+      *reinterpret_cast<u32x4*>(cv_grp + 8 * (lane + 64 * i)) = g;
+    }
+  }
   if (chunk < n_chunks) {
     bf16x8 qop[D / 32];
 #pragma unroll
@@ -171,32 +196,33 @@ __global__ __launch_bounds__(kTpWavesS * 64, D <= 256 ? 4 : 1) void decode_bf16_
     uint8_t mb;
     const bool ok = slot_valid_flat(a, b, kr, (chunk << 5) + (lane & 31), mb);
     const uint64_t vbits = __ballot(ok && mb != 0);
-    if (writer && (!PREP || pp.k_raw)) patch_k_sel<D>(kv, nk_lds, kr.new_slot, chunk << 5, col, grp);
+    if (writer && (!PREP || pp.k_raw)) {
+      patch_k_sel<D>(kv, nk_lds, kr.new_slot, chunk << 5, col, grp);
+      // the fused append's K row goes to the cache as soon as the chunk's loads have landed (no other
+      // wave of the launch reads this chunk), as whole 128-byte lines: the new slot's pieces and its
+      // line neighbour's (lanes col and col ^ 1 of the slot's half bb), both from the patched registers
+      // (against the row's half lines stored after the scores: 50.0 -> 49.7 us per step for a full
+      // 512-slot ring at B = 256; E2B decode step 4.431 -> 4.411 ms)
+      const int r = (int)(kr.new_slot & 31);
+      const int nc = ((r >> 3) << 2) | (r & 3), nbb = (r >> 2) & 1;
+      if ((col >> 1) == (nc >> 1)) {
+        unsigned char* ck = reinterpret_cast<unsigned char*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D * 2;
+        const uint32_t base = (uint32_t)((chunk * (D / 32) * 2 + nbb) * 1024 + col * 64 + grp * 16);
+        if (nbb) {  // (wave-uniform; static register indices)
+#pragma unroll
+          for (int s = 0; s < D / 32; ++s) *reinterpret_cast<u32x4*>(ck + base + 2048u * s) = kv[1][s];
+        } else {
+#pragma unroll
+          for (int s = 0; s < D / 32; ++s) *reinterpret_cast<u32x4*>(ck + base + 2048u * s) = kv[0][s];
+        }
+      }
+    }
     if constexpr (kQlds)
       score_to_lds_qlds<D>(kv, q_lds, vbits, ws + (int64_t)pair * R * row_slots, row_slots, chunk << 5, R, col, grp,
                            kBf16Min);
     else
       score_to_lds<D>(kv, qop, vbits, ws + (int64_t)pair * R * row_slots, row_slots, chunk << 5, R, col, grp,
                       kBf16Min);
-  }
-  // the fused append's K row store: by the writer wave, after its K loads of the chunk have been
-  // consumed (no other wave of the launch reads that chunk), so no load of this launch can see a
-  // partly written row. With PREP the row comes from LDS (prepared by wave 0 before the barrier);
-  // its V^T column was stored by wave 1 above (read only by the values launch).
-  if constexpr (PREP) {
-    if (writer && pp.k_raw) {
-      uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D;
-      if (lane < D / 8)
-        *reinterpret_cast<u32x4*>(ck + kt_index(kr.new_slot, 8 * lane, D)) = *reinterpret_cast<const u32x4*>(nk_lds + 8 * lane);
-    }
-  }
-  if (!PREP && writer && lane < D / 8) {
-    uint16_t* ck = reinterpret_cast<uint16_t*>(a.cache_k_w) + (int64_t)pair * a.slot_stride * D;
-    *reinterpret_cast<u32x4*>(ck + kt_index(kr.new_slot, 8 * lane, D)) = nkv;
-    uint16_t* cv = reinterpret_cast<uint16_t*>(a.cache_vt) + (int64_t)pair * D * a.slot_stride;
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      cv[vt_index(kr.new_slot, 8 * lane + e, D)] = (uint16_t)((e & 1) ? nvv[e >> 1] >> 16 : nvv[e >> 1] & 0xffffu);
   }
 }
 
