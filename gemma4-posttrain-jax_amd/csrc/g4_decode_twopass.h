@@ -111,10 +111,10 @@ __global__ __launch_bounds__(kTpWavesS * 64, D <= 256 ? 4 : 1) void decode_bf16_
                             : u32x4{0u, 0u, 0u, 0u};
     }
   }
-  // without PREP: the writer wave's 16-byte pieces of the new K and V rows (lane l < D / 8: dims
-  // 8 l .. 8 l + 7), also requested ahead of the K chunk, so that neither the K substitution nor
-  // the cache stores at the end wait on a load (52.2 -> 48.x us per step for a full 512-slot ring
-  // at B = 256 against loading them where they are used)
+  // without PREP: the writer wave's 16-byte pieces of the new K row (lane l < D / 8: dims 8 l ..
+  // 8 l + 7), also requested ahead of the K chunk, so that the K substitution does not wait on a
+  // load (with the new V row requested the same way: 52.2 -> 50.5 us per step for a full 512-slot
+  // ring at B = 256 against loading the rows where they are used)
   u32x4 nkv = {0u, 0u, 0u, 0u};
   if (!PREP && writer && lane < D / 8) nkv = load16(reinterpret_cast<const uint16_t*>(a.new_k) + (int64_t)pair * D + 8 * lane);
   // ... and the appended slot's 8-slot group of the value cache (lane l: the 16-byte pieces of dims
