@@ -16,8 +16,8 @@
 //
 // MFMA v_mfma_f32_16x16x32_bf16 with A = 16 rows of W (output columns) and B = 16 rows of X
 // (output rows): lane (grp, col) accumulates Y[m = 16 rb + col][n = 16 cb + 4 grp .. + 3], four
-// consecutive outputs of one row. Each wave owns a 64 x 64 block of the tile (4 x 4 accumulator
-// blocks).
+// consecutive outputs of one row. Each wave owns a 64 x 32 block of a 128 x 128 tile (4 x 2
+// accumulator blocks; 8 waves) or a 64 x 64 block of a 256 x 64 tile (4 x 4; 4 waves).
 //
 // Split-K (ksplit > 1): a workgroup of split s covers K range s; partial sums go to an f32
 // workspace [ksplit][M][N] and a second kernel adds them in split order and rounds to bf16, or,
@@ -31,35 +31,43 @@ namespace {
 
 constexpr int kGemmRows = 256;  // M rows at most
 constexpr int kGemmKT = 64;     // K per stage
-constexpr int kGemmThreads = 256;
 constexpr int kGroupBytes = 1024;  // 8 rows x 128 B
 
-// A workgroup's tile: TR rows x TC columns, 4 waves of 64 x 64 (TR / 64 along the rows, TC / 64
-// along the columns). TR = 256: all rows, 64 columns (X re-read once per 64 columns). TR = 128: half
+// A workgroup's tile: TR rows x TC columns (TR / 64 waves along the rows, TC / WCOLS along the
+// columns). TR = 256: all rows, 64 columns (X re-read once per 64 columns). TR = 128: half
 // the rows, 128 columns (per CU 1/4 less X + W traffic; the two row halves of a column tile go to
 // one XCD, so the second read of its W is an L2 hit).
+// TR = 128 runs 8 waves of 64 x 32 (two per SIMD, so one's MFMAs run while the other waits on its
+// stage; each output keeps the same K order as with 4 waves of 64 x 64, so the results are identical):
+// gate/up 31.4-33.2 -> 29.5-31.1 us, down 18.2-18.6 -> 17.7-18.0 us, E2B decode step 4.542 -> 4.505 ms.
 template <int TR>
 struct GemmTile {
   static constexpr int TC = 16384 / TR;
-  static constexpr int WR = TR / 64;  // waves along the rows
+  static constexpr int WR = TR / 64;                  // waves along the rows
+  static constexpr int WCOLS = TR == 128 ? 32 : 64;   // columns per wave
+  static constexpr int CB = WCOLS / 16;               // 16-column MFMA blocks per wave
+  static constexpr int WAVES = WR * (TC / WCOLS);
+  static constexpr int THREADS = WAVES * 64;
   static constexpr int XG = TR / 8;   // 8-row groups of X per stage
   static constexpr int WG = TC / 8;   // of W
-  static constexpr int DMA = (XG + WG) / (kGemmThreads / 64);  // DMA instructions per wave and stage
+  static constexpr int DMA = (XG + WG) / WAVES;  // DMA instructions per wave and stage
   static constexpr int STAGE = (XG + WG) * kGroupBytes;        // 40 KiB (TR 256) / 32 KiB (TR 128)
   static_assert(TR == 256 || TR == 128, "tile rows");
 };
 
 // First weight row of W group j (8 rows) of column tile `tile`. Plain: rows tile * TC + 8 j. Gated
-// GELU: each 64-column wave slice holds the 32 gate rows and the 32 up rows of the same 32 outputs
-// (gate rows of output o at o, up rows at half + o), tile * TC / 2 outputs before this tile.
-template <int TC>
+// GELU: each WCOLS-column wave slice holds the WCOLS / 2 gate rows and the WCOLS / 2 up rows of the
+// same outputs (gate rows of output o at o, up rows at half + o), tile * TC / 2 outputs before this
+// tile.
+template <int TC, int WCOLS>
 __device__ __forceinline__ int gemm_wrow(bool gelu, int half, int tile, int j) {
   if (!gelu) return tile * TC + 8 * j;
-  const int o = tile * (TC / 2) + 32 * (j >> 3) + 8 * (j & 3);
-  return (j & 7) < 4 ? o : half + o;
+  constexpr int GS = WCOLS / 8;  // 8-row groups per wave slice: the first GS / 2 are gate rows
+  const int o = tile * (TC / 2) + (WCOLS / 2) * (j / GS) + 8 * (j % (GS / 2));
+  return j % GS < GS / 2 ? o : half + o;
 }
 
-// DMA of the stage at K offset k0 into `buf`: wave w moves groups w, w + 4, ... of X then of W.
+// DMA of the stage at K offset k0 into `buf`: wave w moves groups w, w + WAVES, ... of X then of W.
 // Lane l of a group instruction takes row 8 g + l / 8 and the 16-byte piece (l % 8) ^ (row % 8) of
 // its 128-byte K slice. Past the last stage every load reads beyond its resource (zeros, no memory
 // request), so every wave always issues the same number of loads per stage.
@@ -72,9 +80,9 @@ __device__ __forceinline__ void gemm_dma(unsigned char* __restrict__ buf, __amdg
   const int kc = (lane & 7) ^ rl;  // 16-byte piece this lane fetches (row % 8 == rl)
 #pragma unroll
   for (int i = 0; i < T::DMA; ++i) {
-    const int g = w + 4 * i;  // groups 0..XG-1: X, then W
+    const int g = w + T::WAVES * i;  // groups 0..XG-1: X, then W
     const bool is_x = g < T::XG;
-    const int row = is_x ? m0 + 8 * g + rl : gemm_wrow<T::TC>(gelu, half, tile, g - T::XG) + rl;
+    const int row = is_x ? m0 + 8 * g + rl : gemm_wrow<T::TC, T::WCOLS>(gelu, half, tile, g - T::XG) + rl;
     const uint32_t off = (uint32_t)(row * K + k0 + 8 * kc) * 2u;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(is_x ? rx : rw,
                                              (__attribute__((address_space(3))) void*)(buf + g * kGroupBytes), 16,
@@ -94,26 +102,30 @@ __device__ __forceinline__ uint32_t gemm_operand_at(uint32_t part, int row, int 
 // tell the stage being multiplied from the stages the DMA is still filling, and at some steps of
 // the ring waited for every DMA in flight (vmcnt(0)); the stage's own DMAs are already covered by
 // the s_waitcnt vmcnt + s_barrier that starts each step.
-// Wave (wr, wc) multiplies rows [64 wr, 64 wr + 64) of the X part by rows [64 wc, 64 wc + 64) of
-// the W part.
+// Wave (wr, wc) multiplies rows [64 wr, 64 wr + 64) of the X part by rows [WCOLS wc, WCOLS wc +
+// WCOLS) of the W part.
 template <int TR>
-__device__ __forceinline__ void gemm_compute(const unsigned char* __restrict__ buf, floatx4 (&acc)[4][4], int wr,
-                                             int wc, int col, int grp) {
+__device__ __forceinline__ void gemm_compute(const unsigned char* __restrict__ buf,
+                                             floatx4 (&acc)[4][GemmTile<TR>::CB], int wr, int wc, int col, int grp) {
+  constexpr int CB = GemmTile<TR>::CB, WCOLS = GemmTile<TR>::WCOLS;
   const uint32_t xs = lds_addr(buf);
   const uint32_t ws = xs + GemmTile<TR>::XG * kGroupBytes;
 #pragma unroll
   for (int kh = 0; kh < 2; ++kh) {
     u32x4 a[4], b[4];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) a[cb] = lds_read16(gemm_operand_at(ws, 64 * wc + 16 * cb + col, 4 * kh + grp));
+    for (int cb = 0; cb < CB; ++cb) a[cb] = lds_read16(gemm_operand_at(ws, WCOLS * wc + 16 * cb + col, 4 * kh + grp));
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) b[rb] = lds_read16(gemm_operand_at(xs, 64 * wr + 16 * rb + col, 4 * kh + grp));
-    __asm__ volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+    if constexpr (CB == 4)
+      __asm__ volatile("s_waitcnt lgkmcnt(0)"
+                       : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+    else
+      __asm__ volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = mfma16x16x32(as_bf16x8(a[cb]), as_bf16x8(b[rb]), acc[rb][cb]);
+      for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = mfma16x16x32(as_bf16x8(a[cb]), as_bf16x8(b[rb]), acc[rb][cb]);
   }
 }
 
@@ -131,7 +143,7 @@ struct GemmLoop {
 // them back (down projection 19.3 -> 18.6 us).
 template <int TR>
 __device__ __forceinline__ void gemm_step(const unsigned char* __restrict__ cur, unsigned char* __restrict__ fre,
-                                          floatx4 (&acc)[4][4], const GemmLoop& L, int s) {
+                                          floatx4 (&acc)[4][GemmTile<TR>::CB], const GemmLoop& L, int s) {
   // this wave's DMAs of stage s have landed (stages s + 1, s + 2 may not have), then every wave's
   __asm__ volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * GemmTile<TR>::DMA) : "memory");
   gemm_compute<TR>(cur, acc, L.wr, L.wc, L.col, L.grp);
@@ -147,7 +159,7 @@ __device__ __forceinline__ void gemm_step(const unsigned char* __restrict__ cur,
 // column tiles. The unit is (tile u / ksplit, split u mod ksplit). K / ksplit must be a multiple
 // of 64.
 template <int TR>
-__global__ __launch_bounds__(kGemmThreads) void linear_bf16_kernel(G4LinearArgs a, float* partials) {
+__global__ __launch_bounds__(GemmTile<TR>::THREADS) void linear_bf16_kernel(G4LinearArgs a, float* partials) {
   using T = GemmTile<TR>;
   __shared__ __attribute__((aligned(1024))) unsigned char b0[T::STAGE], b1[T::STAGE], b2[T::STAGE], b3[T::STAGE];
   GemmLoop L;
@@ -186,11 +198,12 @@ __global__ __launch_bounds__(kGemmThreads) void linear_bf16_kernel(G4LinearArgs 
   L.gelu = a.epilogue == G4_LINEAR_GELU_MUL;
   L.half = a.n / 2;
 
-  floatx4 acc[4][4];
+  constexpr int CB = T::CB;
+  floatx4 acc[4][CB];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[r][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < CB; ++c) acc[r][c] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   gemm_dma<TR>(b0, L.rx, L.rw, L.K, L.kbeg, true, xbytes, wbytes, L.w, L.lane, L.m0, L.gelu, L.half, L.tile);
   gemm_dma<TR>(b1, L.rx, L.rw, L.K, L.kbeg + kGemmKT, L.nst > 1, xbytes, wbytes, L.w, L.lane, L.m0, L.gelu, L.half,
@@ -205,19 +218,20 @@ __global__ __launch_bounds__(kGemmThreads) void linear_bf16_kernel(G4LinearArgs 
   }
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the trailing (zero) DMAs
 
-  // lane (grp, col) holds Y[m = m0 + 64 wr + 16 rb + col][n = n0 + 64 wc + 16 cb + 4 grp + j]
-  if (L.gelu) {  // cb 0, 1: gate columns; cb 2, 3: the up columns of the same outputs
+  // lane (grp, col) holds Y[m = m0 + 64 wr + 16 rb + col][n = n0 + WCOLS wc + 16 cb + 4 grp + j]
+  if (L.gelu) {  // cb < CB / 2: gate columns; cb + CB / 2: the up columns of the same outputs
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       const int m = L.m0 + 64 * L.wr + 16 * rb + L.col;
       if (m < a.m) {
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
+        for (int cb = 0; cb < CB / 2; ++cb) {
           float y[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) y[j] = gelu_tanh_mul(round_bf16(acc[rb][cb][j]), round_bf16(acc[rb][cb + 2][j]));
-          uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + (int64_t)m * a.ldy + L.tile * (T::TC / 2) + 32 * L.wc +
-                          16 * cb + 4 * L.grp;
+          for (int j = 0; j < 4; ++j)
+            y[j] = gelu_tanh_mul(round_bf16(acc[rb][cb][j]), round_bf16(acc[rb][cb + CB / 2][j]));
+          uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + (int64_t)m * a.ldy + L.tile * (T::TC / 2) +
+                          (T::WCOLS / 2) * L.wc + 16 * cb + 4 * L.grp;
           *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
         }
       }
@@ -229,8 +243,8 @@ __global__ __launch_bounds__(kGemmThreads) void linear_bf16_kernel(G4LinearArgs 
     const int m = L.m0 + 64 * L.wr + 16 * rb + L.col;
     if (m < a.m) {
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) {
-        const int n = n0 + 64 * L.wc + 16 * cb + 4 * L.grp;
+      for (int cb = 0; cb < CB; ++cb) {
+        const int n = n0 + T::WCOLS * L.wc + 16 * cb + 4 * L.grp;
         if (a.ksplit == 1) {
           uint16_t* y = reinterpret_cast<uint16_t*>(a.y) + (int64_t)m * a.ldy + n;
           *reinterpret_cast<uint2*>(y) = make_uint2(pack_bf16x2(acc[rb][cb][0], acc[rb][cb][1]),
@@ -294,10 +308,10 @@ extern "C" int g4_linear_bf16(const G4LinearArgs* args, void* stream) {
   float* partials = reinterpret_cast<float*>(a.workspace);
   // 128 x 128 tiles when the rows fill two halves and the columns divide by 128; else 256 x 64
   if (a.m > 128 && a.n % 128 == 0)
-    hipLaunchKernelGGL(linear_bf16_kernel<128>, dim3((unsigned)(a.n / 128 * a.ksplit * 2)), dim3(kGemmThreads), 0,
+    hipLaunchKernelGGL(linear_bf16_kernel<128>, dim3((unsigned)(a.n / 128 * a.ksplit * 2)), dim3(GemmTile<128>::THREADS), 0,
                        st, a, partials);
   else
-    hipLaunchKernelGGL(linear_bf16_kernel<256>, dim3((unsigned)(a.n / 64 * a.ksplit)), dim3(kGemmThreads), 0, st,
+    hipLaunchKernelGGL(linear_bf16_kernel<256>, dim3((unsigned)(a.n / 64 * a.ksplit)), dim3(GemmTile<256>::THREADS), 0, st,
                        a, partials);
   if (int rc = check_launch("g4_linear_bf16")) return rc;
   if (a.ksplit > 1 && a.y) {  // without y the partials stay in the workspace for the consumer
