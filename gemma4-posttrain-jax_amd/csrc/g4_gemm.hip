@@ -16,8 +16,8 @@
 //
 // MFMA v_mfma_f32_16x16x32_bf16 with A = 16 rows of W (output columns) and B = 16 rows of X
 // (output rows): lane (grp, col) accumulates Y[m = 16 rb + col][n = 16 cb + 4 grp .. + 3], four
-// consecutive outputs of one row. Each wave owns a 64 x 32 block of a 128 x 128 tile (4 x 2
-// accumulator blocks; 8 waves) or a 64 x 64 block of a 256 x 64 tile (4 x 4; 4 waves).
+// consecutive outputs of one row. Each of the 8 waves owns a 64 x 32 block of the 128 x 128 or
+// 256 x 64 tile (4 x 2 accumulator blocks).
 //
 // Split-K (ksplit > 1): a workgroup of split s covers K range s; partial sums go to an f32
 // workspace [ksplit][M][N] and a second kernel adds them in split order and rounds to bf16, or,
@@ -37,14 +37,16 @@ constexpr int kGroupBytes = 1024;  // 8 rows x 128 B
 // columns). TR = 256: all rows, 64 columns (X re-read once per 64 columns). TR = 128: half
 // the rows, 128 columns (per CU 1/4 less X + W traffic; the two row halves of a column tile go to
 // one XCD, so the second read of its W is an L2 hit).
-// TR = 128 runs 8 waves of 64 x 32 (two per SIMD, so one's MFMAs run while the other waits on its
-// stage; each output keeps the same K order as with 4 waves of 64 x 64, so the results are identical):
-// gate/up 31.4-33.2 -> 29.5-31.1 us, down 18.2-18.6 -> 17.7-18.0 us, E2B decode step 4.542 -> 4.505 ms.
+// Every wave owns 64 x 32 outputs: 8 waves per workgroup, two per SIMD, so one's MFMAs run while the
+// other waits on its stage; each output keeps the same K order as with 4 waves of 64 x 64, so the
+// results are identical. TR = 128 (M 256): gate/up 31.4-33.2 -> 29.5-31.1 us, down 18.2-18.6 ->
+// 17.7-18.0 us, E2B decode step 4.542 -> 4.505 ms; TR = 256 (M 128 / 64): gate/up 29.3-31.3 ->
+// 25.9-27.5 / 28.8-29.7 -> 25.4-26.4 us, down 16.2-16.5 -> 14.2-14.9 / 15.0 -> 12.9-13.2 us.
 template <int TR>
 struct GemmTile {
   static constexpr int TC = 16384 / TR;
   static constexpr int WR = TR / 64;                  // waves along the rows
-  static constexpr int WCOLS = TR == 128 ? 32 : 64;   // columns per wave
+  static constexpr int WCOLS = 32;                    // columns per wave
   static constexpr int CB = WCOLS / 16;               // 16-column MFMA blocks per wave
   static constexpr int WAVES = WR * (TC / WCOLS);
   static constexpr int THREADS = WAVES * 64;
@@ -112,16 +114,13 @@ __device__ __forceinline__ void gemm_compute(const unsigned char* __restrict__ b
   const uint32_t ws = xs + GemmTile<TR>::XG * kGroupBytes;
 #pragma unroll
   for (int kh = 0; kh < 2; ++kh) {
-    u32x4 a[4], b[4];
+    static_assert(CB == 2, "operand wait list");
+    u32x4 a[CB], b[4];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) a[cb] = lds_read16(gemm_operand_at(ws, WCOLS * wc + 16 * cb + col, 4 * kh + grp));
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) b[rb] = lds_read16(gemm_operand_at(xs, 64 * wr + 16 * rb + col, 4 * kh + grp));
-    if constexpr (CB == 4)
-      __asm__ volatile("s_waitcnt lgkmcnt(0)"
-                       : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
-    else
-      __asm__ volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
