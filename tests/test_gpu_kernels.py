@@ -291,6 +291,20 @@ def test_decode_two_pass_edge_rows(device, D, ring, cap):
                  key_mask=key_mask, fused=True, seed=27, num_splits=_lib.G4_DECODE_TWO_PASS)
 
 
+@pytest.mark.parametrize("D", [256, 512])
+def test_decode_two_pass_ring_end_group(device, D):
+    """G4_DECODE_TWO_PASS appends into a 100-slot ring at its last 8-slot value group (slots 96..103
+    of a 128-slot stride: the launch rewrites the appended value's group whole, including the slots
+    past the capacity), after wrapping, and at slot 3; the cache stays bit-exact."""
+
+    B, H, R, cap = 4, 2, 4, 100
+    q_pos = np.array([96, 99, 197, 303])
+    key_mask = np.ones((B, 320), bool)
+    key_mask[2, :20] = False
+    _decode_case(device, O.BF16, B=B, H=H, R=R, D=D, cap=cap, ring=True, window=cap, q_pos=q_pos,
+                 key_mask=key_mask, fused=True, seed=31, num_splits=_lib.G4_DECODE_TWO_PASS)
+
+
 @pytest.mark.parametrize("R,W", [(1, 512), (2, 512), (8, 512), (16, 512), (4, 768), (16, 1024)])
 def test_decode_two_pass_group_sizes(device, R, W):
     """G4_DECODE_TWO_PASS with 1..16 query heads per KV head: values waves with no head of their
