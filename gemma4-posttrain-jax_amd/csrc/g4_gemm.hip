@@ -55,6 +55,7 @@ struct GemmTile {
   static constexpr int DMA = (XG + WG) / WAVES;  // DMA instructions per wave and stage
   static constexpr int STAGE = (XG + WG) * kGroupBytes;        // 40 KiB (TR 256) / 32 KiB (TR 128)
   static_assert(TR == 256 || TR == 128, "tile rows");
+  static_assert((XG + WG) % WAVES == 0 && WAVES * 64 <= 1024, "every wave issues the same DMA count");
 };
 
 // First weight row of W group j (8 rows) of column tile `tile`. Plain: rows tile * TC + 8 j. Gated
